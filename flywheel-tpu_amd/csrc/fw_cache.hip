@@ -1,0 +1,142 @@
+// Bit-exact writes into the merged paged KV pool, and the library's error
+// plumbing.
+//
+// fw_append_ragged replaces append_ragged / append_kernel
+// (flywheel_tpu/softmax_attention/kernels/kv_append.py:116-184, :32-114): the
+// reference walks requests and pages serially with one DMA per page; here one
+// workgroup writes one whole merged token row ([k0, v0, k1, v1, ...] plus an
+// fp8 pool's zero pad head) with 16-byte stores, all tokens in parallel.
+//
+// fw_write_kv_cache_pages replaces write_kv_cache_pages
+// (softmax_attention/page.py:32-73, kernels/kv_cache_write.py:153).
+//
+// Device metadata (cu_seqlens, lengths, tables, slices) is trusted as in the
+// reference; out-of-range entries are skipped so a bad table cannot fault.
+#include "fw_common.h"
+
+#include <string>
+
+namespace fw {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FW_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
+  return FW_OK;
+}
+
+// One merged row: chunk c (16 bytes) of head row hr = c / chunks_per_head.
+__device__ __forceinline__ u32x4_t merged_chunk(const uint8_t *k_row, const uint8_t *v_row, int c,
+                                                int chunks_per_head, int nheads_k) {
+  const int hr = c / chunks_per_head;
+  const int off = (c % chunks_per_head) * 16;
+  const int kvh = hr >> 1;
+  if (kvh >= nheads_k) return u32x4_t{0u, 0u, 0u, 0u};
+  const uint8_t *src = (hr & 1 ? v_row : k_row) + (size_t)kvh * chunks_per_head * 16 + off;
+  return *(const u32x4_t *)src;
+}
+
+__global__ __launch_bounds__(256) void fw_append_kernel(
+    uint8_t *cache, const uint8_t *k, const uint8_t *v, const int32_t *cu, const int32_t *lens,
+    const int32_t *table, const int32_t *num_active, int B, int T, int Hk, int head_bytes, int CH,
+    int P, int num_pages, int max_pages) {
+  const int i = blockIdx.x;
+  const int nact = num_active ? min(*num_active, B) : B;
+  if (i >= cu[nact]) return;  // rows past the last active request are padding
+  // request r: the last r with cu[r] <= i
+  int lo = 0, hi = nact;  // cu[lo] <= i < cu[hi]
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (cu[mid] <= i) lo = mid; else hi = mid;
+  }
+  const int r = lo;
+  if (i < cu[r]) return;
+  const int pos = lens[r] + (i - cu[r]);
+  if (pos < 0 || pos / P >= max_pages) return;
+  const int page = table[(size_t)r * max_pages + pos / P];
+  if (page < 0 || page >= num_pages) return;
+  const size_t row_bytes = (size_t)CH * head_bytes;
+  uint8_t *dst = cache + ((size_t)page * P + pos % P) * row_bytes;
+  const uint8_t *k_row = k + (size_t)i * Hk * head_bytes;
+  const uint8_t *v_row = v + (size_t)i * Hk * head_bytes;
+  const int cph = head_bytes / 16;
+  const int nchunks = CH * cph;
+  for (int c = threadIdx.x; c < nchunks; c += blockDim.x)
+    *(u32x4_t *)(dst + (size_t)c * 16) = merged_chunk(k_row, v_row, c, cph, Hk);
+}
+
+__global__ __launch_bounds__(256) void fw_write_pages_kernel(
+    uint8_t *cache, const uint8_t *k, const uint8_t *v, const int32_t *slices, int n_cols,
+    const int32_t *num_slices, int T, int Hk, int head_bytes, int CH, int num_rows) {
+  const int j = blockIdx.x;
+  if (j >= *num_slices) return;
+  const int c0 = slices[j], n0 = slices[n_cols + j], len = slices[2 * n_cols + j];
+  const size_t row_bytes = (size_t)CH * head_bytes;
+  const int cph = head_bytes / 16;
+  const int nchunks = CH * cph;
+  for (int t = 0; t < len; ++t) {
+    const int cr = c0 + t, nr = n0 + t;
+    if (cr < 0 || cr >= num_rows || nr < 0 || nr >= T) continue;
+    uint8_t *dst = cache + (size_t)cr * row_bytes;
+    const uint8_t *k_row = k + (size_t)nr * Hk * head_bytes;
+    const uint8_t *v_row = v + (size_t)nr * Hk * head_bytes;
+    for (int c = threadIdx.x; c < nchunks; c += blockDim.x)
+      *(u32x4_t *)(dst + (size_t)c * 16) = merged_chunk(k_row, v_row, c, cph, Hk);
+  }
+}
+
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" const char *fw_last_error(void) { return g_last_error.c_str(); }
+extern "C" int fw_abi_version(void) { return 1; }
+
+extern "C" int fw_append_ragged(void *kv_cache, const void *k, const void *v,
+                                const int32_t *cu_seqlens, const int32_t *cache_seqlens,
+                                const int32_t *block_table, const int32_t *num_active,
+                                int32_t batch, int32_t total_tokens, int32_t nheads_k,
+                                int32_t head_dim, int32_t page_size, int32_t num_pages,
+                                int32_t max_pages, int32_t kv_dtype, fw_stream_t stream) {
+  FW_REQUIRE(kv_dtype >= FW_BF16 && kv_dtype <= FW_FP8_E5M2, FW_ERR_NOT_IMPLEMENTED,
+             "kv_dtype %d is not bf16 / fp8 e4m3 / fp8 e5m2", kv_dtype);
+  FW_REQUIRE(batch > 0 && nheads_k > 0 && page_size > 0 && max_pages > 0, FW_ERR_VALUE,
+             "batch, nheads_k, page_size and max_pages must be positive");
+  const int head_bytes = head_dim * dtype_bytes(kv_dtype);
+  FW_REQUIRE(head_bytes % 16 == 0, FW_ERR_VALUE, "head_dim %d is not a multiple of 16 bytes",
+             head_dim);
+  if (total_tokens <= 0) return FW_OK;
+  fw_append_kernel<<<total_tokens, 256, 0, (hipStream_t)stream>>>(
+      (uint8_t *)kv_cache, (const uint8_t *)k, (const uint8_t *)v, cu_seqlens, cache_seqlens,
+      block_table, num_active, batch, total_tokens, nheads_k, head_bytes,
+      merged_heads(nheads_k, kv_dtype), page_size, num_pages, max_pages);
+  return check_launch("fw_append_kernel");
+}
+
+extern "C" int fw_write_kv_cache_pages(const void *k, const void *v, void *kv_cache,
+                                       const int32_t *slices, int32_t n_cols,
+                                       const int32_t *num_slices, int32_t total_tokens,
+                                       int32_t nheads_k, int32_t head_dim, int32_t num_rows,
+                                       int32_t kv_dtype, fw_stream_t stream) {
+  FW_REQUIRE(kv_dtype >= FW_BF16 && kv_dtype <= FW_FP8_E5M2, FW_ERR_NOT_IMPLEMENTED,
+             "kv_dtype %d is not bf16 / fp8 e4m3 / fp8 e5m2", kv_dtype);
+  const int head_bytes = head_dim * dtype_bytes(kv_dtype);
+  FW_REQUIRE(head_bytes % 16 == 0 && nheads_k > 0, FW_ERR_VALUE,
+             "head_dim %d / nheads_k %d invalid", head_dim, nheads_k);
+  if (n_cols <= 0) return FW_OK;
+  fw_write_pages_kernel<<<n_cols, 256, 0, (hipStream_t)stream>>>(
+      (uint8_t *)kv_cache, (const uint8_t *)k, (const uint8_t *)v, slices, n_cols, num_slices,
+      total_tokens, nheads_k, head_bytes, merged_heads(nheads_k, kv_dtype), num_rows);
+  return check_launch("fw_write_pages_kernel");
+}

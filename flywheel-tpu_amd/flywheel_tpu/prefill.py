@@ -1,0 +1,376 @@
+"""flash_attn_func and flash_attn_varlen_func on the gfx950 MFMA kernel.
+
+Mirrors the reference's API layer (flywheel_tpu/softmax_attention/
+prefill.py:62-341, 437-661, 664-963): argument names, order, defaults,
+layouts (head-major (B, H, S, D) / (H, total, D), token-major with head_dim,
+heads_outer_fold), bottom-right causal / window alignment and exception types.
+Every layout is addressed in place through strides; nothing is padded or
+transposed.  Sequence lengths need not be multiples of 128 (the reference's
+padding rule, prefill.py:176-194, is a TPU tiling constraint).
+"""
+
+import torch
+
+from . import _native as N
+from .decode import paged_prefill, _num_active_tensor
+from .inputs import (
+    as_tensor,
+    check_common_kwargs,
+    check_paged_window,
+    check_sinks,
+    descale_scalar,
+    effective_window,
+    int32_device,
+    resolve_scale,
+)
+from .kv_layout import resolve_merged_kv_heads
+
+_ROTARY_MSG = (
+    "fused RoPE (rotary_cos / rotary_sin) is not implemented on this backend;"
+    " rotate q / k before the call."
+)
+
+
+def _check_bf16(*ts):
+    if not all(t.dtype == torch.bfloat16 for t in ts):
+        raise NotImplementedError(
+            f"Only bfloat16 is supported; got {tuple(str(t.dtype) for t in ts)}."
+        )
+
+
+def _split_token_major(x, head_dim):
+    """(…, S, nheads * head_dim) -> nheads."""
+    if x.shape[-1] % head_dim:
+        raise ValueError(f"head_dim {head_dim} must divide the fused width {x.shape[-1]}.")
+    return x.shape[-1] // head_dim
+
+
+def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads, nheads_k,
+                 head_dim, seqlen_q, seqlen_k, causal, window_size, softmax_scale, softcap,
+                 sinks, cu_q=None, cu_k=None, max_seqlen_q=0):
+    left, right = effective_window(causal, window_size)
+    p = N.PrefillParams()
+    p.kv_mode = mode
+    p.q, p.out, p.lse, p.k, p.v = N.ptr(q), N.ptr(out), N.ptr(lse), N.ptr(k), N.ptr(v)
+    p.cu_seqlens_q, p.cu_seqlens_k, p.sinks = N.ptr(cu_q), N.ptr(cu_k), N.ptr(sinks)
+    p.q_stride_b, p.q_stride_h, p.q_stride_t = qs
+    p.k_stride_b, p.k_stride_h, p.k_stride_t = ks
+    p.v_stride_b, p.v_stride_h, p.v_stride_t = vs
+    p.o_stride_b, p.o_stride_h, p.o_stride_t = os_
+    p.lse_stride_b, p.lse_stride_h = ls
+    p.batch, p.nheads, p.nheads_k, p.head_dim = batch, nheads, nheads_k, head_dim
+    p.seqlen_q, p.seqlen_k, p.max_seqlen_q = seqlen_q, seqlen_k, max_seqlen_q
+    p.kv_dtype = N.FW_BF16
+    p.softmax_scale, p.softcap = softmax_scale, float(softcap)
+    p.causal, p.window_left, p.window_right = int(causal), left, right
+    p.k_descale, p.v_descale = 1.0, 1.0
+    lib = N.lib()
+    nbytes = lib.fw_prefill_workspace_bytes(p)
+    ws = None
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        p.workspace, p.workspace_bytes = N.ptr(ws), nbytes
+    N.check(lib.fw_prefill(p, N.stream_of(q)))
+
+
+def flash_attn_func(
+    q,
+    k,
+    v,
+    dropout_p=0.0,
+    softmax_scale=None,
+    causal=False,
+    window_size=(-1, -1),
+    attention_chunk=None,
+    softcap=0.0,
+    alibi_slopes=None,
+    deterministic=False,
+    return_attn_probs=False,
+    return_softmax_lse=False,
+    interpret=False,
+    head_dim=None,
+    token_major=False,
+    *,
+    rotary_cos=None,
+    rotary_sin=None,
+    rotary_interleaved=False,
+    rotary_k=True,
+    heads_outer_fold=False,
+    learnable_sink=None,
+):
+    """flash_attn.flash_attn_func, `prefill.py:62-341`.
+
+    Head-major: q (batch, nheads, seqlen_q, d), k / v (batch, nheads_k,
+    seqlen_k, d), out like q; token-major (token_major=True): (batch, seqlen,
+    nheads * head_dim) with head_dim given; heads_outer_fold: (nheads, batch,
+    seqlen, d).  causal is bottom-right aligned: query i sees key j iff
+    j <= i + seqlen_k - seqlen_q.  Rows with no reachable key return out 0 and
+    lse -inf (or the sink).  lse (batch, nheads, seqlen_q) f32.
+    """
+    del interpret, rotary_interleaved
+    window_size = check_common_kwargs(
+        window_size, dropout_p=dropout_p, softcap=softcap, alibi_slopes=alibi_slopes,
+        deterministic=deterministic, return_attn_probs=return_attn_probs)
+    if attention_chunk is not None:
+        raise NotImplementedError("attention_chunk is not implemented.")
+    if type(heads_outer_fold) is not bool:
+        raise TypeError("heads_outer_fold must be a bool.")
+    has_rotary = rotary_cos is not None or rotary_sin is not None
+    if heads_outer_fold and (token_major or return_softmax_lse or (has_rotary and rotary_k)):
+        raise NotImplementedError(
+            "heads_outer_fold is a forward-only head-major layout; it supports fused RoPE"
+            " only as Q-only rotation (rotary_k=False) and no return_softmax_lse."
+        )
+    if has_rotary:
+        raise NotImplementedError(_ROTARY_MSG)
+    q, k, v = as_tensor(q), as_tensor(k), as_tensor(v)
+    if token_major:
+        if head_dim is None:
+            raise ValueError(
+                "token-major (fused head_dim) inputs require head_dim=; the fused width"
+                f" alone cannot determine the head split (got {tuple(q.shape)=})."
+            )
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError(f"q/k/v ranks must be 3; got {q.shape=}, {k.shape=}, {v.shape=}.")
+        batch, seqlen_q = q.shape[:2]
+        seqlen_k = k.shape[1]
+        nheads = _split_token_major(q, head_dim)
+        nheads_k = _split_token_major(k, head_dim)
+        if v.shape[-1] != nheads_k * head_dim or v.shape[:2] != k.shape[:2]:
+            raise ValueError(f"v must be (batch, seqlen_k, {nheads_k * head_dim}); got {v.shape}.")
+        d = head_dim
+        qs = (seqlen_q * nheads * d, d, nheads * d)
+        ks = (seqlen_k * nheads_k * d, d, nheads_k * d)
+    else:
+        if head_dim is not None:
+            raise ValueError("head_dim is only meaningful for token-major inputs.")
+        if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+            raise ValueError(
+                f"q/k/v must be 4-D head-major; got {tuple(q.shape)=}, {tuple(k.shape)=},"
+                f" {tuple(v.shape)=}."
+            )
+        if heads_outer_fold:
+            nheads, batch, seqlen_q, d = q.shape
+            nheads_k, _, seqlen_k, _ = k.shape
+            qs = (seqlen_q * d, batch * seqlen_q * d, d)
+            ks = (seqlen_k * d, batch * seqlen_k * d, d)
+            kb = k.shape[1]
+        else:
+            batch, nheads, seqlen_q, d = q.shape
+            _, nheads_k, seqlen_k, _ = k.shape
+            qs = (nheads * seqlen_q * d, seqlen_q * d, d)
+            ks = (nheads_k * seqlen_k * d, seqlen_k * d, d)
+            kb = k.shape[0]
+        if kb != batch or v.shape != k.shape or k.shape[-1] != d:
+            raise ValueError(f"k / v must match q's batch and head_dim; got {k.shape=}, {v.shape=}.")
+    if nheads_k <= 0 or nheads % nheads_k:
+        raise ValueError(f"{nheads=} must be a multiple of {nheads_k=}.")
+    _check_bf16(q, k, v)
+    N.require_device(q, k, v)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    softmax_scale = resolve_scale(softmax_scale, d)
+    sinks = check_sinks(learnable_sink, nheads, q.device)
+    out = torch.empty_like(q)
+    lse = (torch.empty((batch, nheads, seqlen_q), dtype=torch.float32, device=q.device)
+           if return_softmax_lse else None)
+    _run_prefill(N.FW_KV_DENSE, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+                 ls=(nheads * seqlen_q, seqlen_q), batch=batch, nheads=nheads,
+                 nheads_k=nheads_k, head_dim=d, seqlen_q=seqlen_q, seqlen_k=seqlen_k,
+                 causal=causal, window_size=window_size, softmax_scale=softmax_scale,
+                 softcap=softcap, sinks=sinks)
+    if return_softmax_lse:
+        return out, lse
+    return out
+
+
+def flash_attn_varlen_func(
+    q,
+    k,
+    v,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    max_seqlen_q,
+    max_seqlen_k,
+    dropout_p=0.0,
+    softmax_scale=None,
+    causal=False,
+    window_size=(-1, -1),
+    softcap=0.0,
+    alibi_slopes=None,
+    deterministic=False,
+    return_attn_probs=False,
+    return_softmax_lse=False,
+    interpret=False,
+    head_dim=None,
+    token_major=False,
+    block_sizes=None,
+    *,
+    rotary_cos=None,
+    rotary_sin=None,
+    rotary_interleaved=False,
+    rotary_k=True,
+    block_table=None,
+    seqused_k=None,
+    num_active=None,
+    k_descale=None,
+    v_descale=None,
+    nheads_k=None,
+    learnable_sink=None,
+    guard_replay_unroll=1,
+):
+    """flash_attn.flash_attn_varlen_func for packed sequences, `prefill.py:664-963`.
+
+    Packed K/V: q (nheads, total_q, d), k / v (nheads_k, total_k, d) with
+    cu_seqlens_q / cu_seqlens_k (token-major: (total, nheads * head_dim)).
+    Paged KV cache (block_table given, read-only): k is the merged pool, v None,
+    cu_seqlens_k None, seqused_k (batch,) each sequence's kv length.  Padding q
+    rows return out 0, lse -inf; lse is (nheads, total_q).  block_sizes and
+    guard_replay_unroll are accepted for compatibility (tiles are chosen by
+    this backend).
+    """
+    del interpret, rotary_interleaved
+    window_size = check_common_kwargs(
+        window_size, dropout_p=dropout_p, softcap=softcap, alibi_slopes=alibi_slopes,
+        deterministic=deterministic, return_attn_probs=return_attn_probs)
+    if block_sizes is not None:
+        bs = tuple(block_sizes)
+        if len(bs) != 4 or not all(type(b) is int and b > 0 for b in bs):
+            raise ValueError(
+                "block_sizes must be 4 positive ints (block_q, block_kv, block_q_compute,"
+                f" block_kv_compute); got {bs!r}."
+            )
+        if bs[0] % 128 or bs[1] % 128:
+            raise ValueError(f"block_q and block_kv must be multiples of 128; got {bs!r}.")
+    if rotary_cos is not None or rotary_sin is not None:
+        raise NotImplementedError(_ROTARY_MSG)
+    for name, bound in (("max_seqlen_q", max_seqlen_q), ("max_seqlen_k", max_seqlen_k)):
+        if isinstance(bound, torch.Tensor):
+            bound = int(bound)
+        if int(bound) <= 0:
+            raise ValueError(f"{name} must be positive; got {bound}.")
+    q = as_tensor(q)
+    k = as_tensor(k)
+    v = as_tensor(v)
+    if block_table is not None:
+        if guard_replay_unroll != 1:
+            raise ValueError(
+                "guard_replay_unroll applies to packed K/V; a paged KV cache always"
+                " unrolls its replay."
+            )
+        if token_major:
+            raise NotImplementedError(
+                "a paged KV cache takes head-major q (nheads, total_q, headdim);"
+                " token_major=True is not supported."
+            )
+        if head_dim is not None:
+            raise ValueError("head_dim is only meaningful for token-major inputs; a paged call"
+                             " takes head-major q.")
+        if cu_seqlens_k is not None:
+            raise ValueError("with block_table, pass cu_seqlens_k=None: seqused_k gives each"
+                             " sequence's kv length.")
+        if v is not None:
+            raise ValueError("with block_table, pass one merged (num_pages, page_size,"
+                             " cache_heads, headdim) cache as k and v=None; separate paged K"
+                             " and V caches are not supported.")
+        if seqused_k is None:
+            raise ValueError("block_table needs seqused_k, the (batch,) kv length of each"
+                             " sequence (its new tokens included).")
+        if q.ndim != 3:
+            raise ValueError(f"with block_table, q must be (nheads, total_q, headdim); got"
+                             f" {tuple(q.shape)=}.")
+        cu = as_tensor(cu_seqlens_q)
+        if cu.ndim != 1 or cu.shape[0] < 2 or cu.is_floating_point():
+            raise ValueError("cu_seqlens_q must be a 1-D integer array of batch + 1 boundaries;"
+                             f" got {tuple(cu.shape)} {cu.dtype}.")
+        batch = cu.shape[0] - 1
+        if not cu.is_cuda and int(cu[0]) != 0:
+            raise ValueError(f"with block_table, cu_seqlens_q must start at 0; got"
+                             f" cu_seqlens_q[0]={int(cu[0])}.")
+        if isinstance(num_active, int) and not 0 <= num_active <= batch:
+            raise ValueError(f"num_active must be in [0, {batch}]; got {num_active}.")
+        check_paged_window(causal, window_size)
+        if k.ndim != 4:
+            raise ValueError(f"k must be the merged (num_pages, page_size, cache_heads, head_dim)"
+                             f" pool; got {tuple(k.shape)}.")
+        nheads, total_q, d = q.shape
+        nkv = resolve_merged_kv_heads(k.shape[2], k.dtype, nheads_k)
+        if k.shape[3] != d:
+            raise ValueError(f"cache head_dim {k.shape[3]} must match q's {d}.")
+        if nheads % nkv:
+            raise ValueError(f"{nheads=} must be a multiple of nheads_k={nkv}.")
+        if k.shape[1] % 16:
+            raise ValueError(f"page_size must be a multiple of 16; got {k.shape[1]}.")
+        if q.dtype != torch.bfloat16:
+            raise NotImplementedError(f"q must be bfloat16; got {q.dtype}.")
+        N.require_device(q, k)
+        device = q.device
+        bt = as_tensor(block_table)
+        if bt.ndim != 2 or bt.shape[0] != batch or bt.is_floating_point():
+            raise ValueError(f"block_table must be (batch={batch}, max_pages) int; got"
+                             f" {tuple(bt.shape)} {bt.dtype}.")
+        out, lse = paged_prefill(
+            q.contiguous(), k, int32_device(cu, device, "cu_seqlens_q"),
+            int32_device(seqused_k, device, "seqused_k", (batch,)),
+            bt.to(device=device, dtype=torch.int32).contiguous(),
+            _num_active_tensor(num_active, batch, device),
+            check_sinks(learnable_sink, nheads, device),
+            nheads_k=nkv, softmax_scale=resolve_scale(softmax_scale, d), softcap=float(softcap),
+            causal=causal, window_size=window_size,
+            k_descale=descale_scalar(k_descale, "k_descale"),
+            v_descale=descale_scalar(v_descale, "v_descale"),
+            max_seqlen_q=int(max_seqlen_q), return_lse=return_softmax_lse, token_major_q=False)
+        return (out, lse) if return_softmax_lse else out
+    if seqused_k is not None or num_active is not None:
+        raise ValueError("seqused_k and num_active describe a paged KV cache and need"
+                         " block_table; packed K/V takes cu_seqlens_k.")
+    if any(x is not None for x in (k_descale, v_descale, nheads_k)):
+        raise ValueError("k_descale, v_descale and nheads_k describe an fp8 paged pool and need"
+                         " block_table; packed K/V is bf16.")
+    cu_q = as_tensor(cu_seqlens_q)
+    cu_k = as_tensor(cu_seqlens_k)
+    if cu_q.ndim != 1 or tuple(cu_q.shape) != tuple(cu_k.shape):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must be equal-shaped 1-D arrays; got"
+                         f" {tuple(cu_q.shape)=}, {tuple(cu_k.shape)=}.")
+    batch = cu_q.shape[0] - 1
+    if token_major:
+        if head_dim is None:
+            raise ValueError("token-major (fused head_dim) inputs require head_dim=.")
+        if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
+            raise ValueError(f"token-major packed q/k/v must be 2-D; got {q.shape=}.")
+        total_q, total_k = q.shape[0], k.shape[0]
+        nheads = _split_token_major(q, head_dim)
+        nkv = _split_token_major(k, head_dim)
+        d = head_dim
+        qs = (0, d, nheads * d)
+        ks = (0, d, nkv * d)
+    else:
+        if head_dim is not None:
+            raise ValueError("head_dim is only meaningful for token-major inputs.")
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError(f"q/k/v must be (heads, total, d); got {q.shape=}, {k.shape=}.")
+        nheads, total_q, d = q.shape
+        nkv, total_k, _ = k.shape
+        qs = (0, total_q * d, d)
+        ks = (0, total_k * d, d)
+    if tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"v must match k's shape; got {k.shape=}, {v.shape=}.")
+    if nkv <= 0 or nheads % nkv:
+        raise ValueError(f"{nheads=} must be a multiple of nheads_k={nkv}.")
+    _check_bf16(q, k, v)
+    N.require_device(q, k, v)
+    device = q.device
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    out = torch.empty_like(q)
+    lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
+           if return_softmax_lse else None)
+    _run_prefill(N.FW_KV_VARLEN, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+                 ls=(0, total_q), batch=batch, nheads=nheads, nheads_k=nkv, head_dim=d,
+                 seqlen_q=total_q, seqlen_k=total_k, causal=causal, window_size=window_size,
+                 softmax_scale=resolve_scale(softmax_scale, d), softcap=softcap,
+                 sinks=check_sinks(learnable_sink, nheads, device),
+                 cu_q=int32_device(cu_q, device, "cu_seqlens_q"),
+                 cu_k=int32_device(cu_k, device, "cu_seqlens_k"),
+                 max_seqlen_q=int(max_seqlen_q))
+    if return_softmax_lse:
+        return out, lse
+    return out

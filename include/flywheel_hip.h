@@ -1,0 +1,182 @@
+/*
+ * flywheel_hip.h -- C-ABI of the MI355X (gfx950) softmax-attention hot path.
+ *
+ * The reference (heavyball-research/flywheel-tpu v0.4.1) has no native code and
+ * no FFI: its three API functions call JAX Pallas kernels through
+ * `pl.pallas_call`.  Each entry point below replaces one of those kernel calls
+ * and is what a binding of the reference's Python API (ctypes here, see
+ * flywheel-tpu_amd/flywheel_tpu/_native.py) calls.  All pointers are device
+ * pointers unless stated; all launches go on `stream` and never synchronise
+ * the host.  Every function returns 0 on success and a nonzero fw_status on
+ * failure, with a message retrievable by fw_last_error() (thread-local).
+ *
+ * Layouts (element strides are in elements of the tensor's own dtype):
+ *   merged paged pool  (num_pages, page_size, cache_heads, head_dim): a token
+ *                      row is [k0, v0, k1, v1, ...]; an fp8 pool pads an odd
+ *                      KV head count with one zero head
+ *                      (reference kv_layout.py:39-46, 67-70).
+ *   block_table        (batch, max_pages) int32, row-major.
+ */
+#ifndef FLYWHEEL_HIP_H
+#define FLYWHEEL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *fw_stream_t; /* a hipStream_t; NULL = the default stream */
+
+enum fw_status {
+  FW_OK = 0,
+  FW_ERR_VALUE = 1,           /* bad shape / argument: Python ValueError */
+  FW_ERR_NOT_IMPLEMENTED = 2, /* unsupported feature: NotImplementedError */
+  FW_ERR_RUNTIME = 3          /* HIP launch / device error: RuntimeError */
+};
+
+enum fw_dtype {
+  FW_BF16 = 0,
+  FW_FP8_E4M3 = 1, /* OCP float8_e4m3fn */
+  FW_FP8_E5M2 = 2  /* OCP float8_e5m2 */
+};
+
+/* The last error message of the calling thread ("" if none). */
+const char *fw_last_error(void);
+/* ABI version of this header: 1. */
+int fw_abi_version(void);
+
+/*
+ * Paged decode over a merged cache, with the new token's K/V append fused in.
+ * Replaces the reference's decode kernel call `flash_attn_kvcache_pallas`
+ * (flywheel_tpu/softmax_attention/kernels/decode.py:2046-2475, kernel body
+ * :463-1915, fused append _append_new_token :933-957) as routed by
+ * flash_attn_with_kvcache (softmax_attention/decode.py:469-478, 512-596) for
+ * a single-token step and for a folded verify window.
+ *
+ * q        (batch, seqlen_q, nheads, head_dim) bf16, token-major, contiguous.
+ * k_new/v_new  (batch, nheads_k, head_dim) in the pool dtype, or NULL: the
+ *          token appended at position cache_seqlens[b] (seqlen_q must be 1).
+ * Row b attends keys [0, cache_seqlens[b] + seqlen_add) where seqlen_add is 1
+ * with k_new, else the caller's count of tokens it appended beforehand.
+ * Query token t sits at position total - seqlen_q + t.
+ * out      (batch, seqlen_q, nheads, head_dim) bf16.
+ * lse      (batch, nheads, seqlen_q) f32 natural-log, or NULL.
+ * sinks    (nheads,) f32 natural-log sink logits, or NULL.
+ * num_active  device int32 scalar or NULL: rows >= *num_active are skipped
+ *          (no append; out 0, lse -inf).
+ * workspace   device scratch of at least fw_paged_decode_workspace_bytes().
+ */
+typedef struct fw_decode_params {
+  const void *q;
+  void *kv_cache;
+  const void *k_new;
+  const void *v_new;
+  const int32_t *cache_seqlens;
+  const int32_t *block_table;
+  const int32_t *num_active;
+  const float *sinks;
+  void *out;
+  float *lse;
+  void *workspace;
+  size_t workspace_bytes;
+  int32_t batch, seqlen_q, nheads, nheads_k, head_dim;
+  int32_t page_size, num_pages, max_pages;
+  int32_t kv_dtype;   /* enum fw_dtype */
+  int32_t seqlen_add; /* see above; ignored (taken as 1) with k_new */
+  float softmax_scale, softcap; /* softcap 0 = off */
+  int32_t causal;      /* a folded window's token t sees keys < total-(Sq-1-t) */
+  int32_t window_left; /* -1 = unbounded */
+  float k_descale, v_descale;
+  int32_t split_keys;  /* keys per split-K work item; 0 = heuristic */
+} fw_decode_params;
+
+size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p);
+int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream);
+
+/*
+ * Ragged append of packed new tokens into the merged pool.  Replaces
+ * append_ragged / append_kernel (kernels/kv_append.py:116-184, :32-114).
+ * k, v (total_tokens, nheads_k, head_dim) in the pool dtype, packed by
+ * cu_seqlens (batch + 1); token t of request r < *num_active goes to row
+ * cache_seqlens[r] + t - cu_seqlens[r] of its pages.  Bit-exact copy.
+ */
+int fw_append_ragged(void *kv_cache, const void *k, const void *v,
+                     const int32_t *cu_seqlens, const int32_t *cache_seqlens,
+                     const int32_t *block_table, const int32_t *num_active,
+                     int32_t batch, int32_t total_tokens, int32_t nheads_k,
+                     int32_t head_dim, int32_t page_size, int32_t num_pages,
+                     int32_t max_pages, int32_t kv_dtype, fw_stream_t stream);
+
+/*
+ * Host-sliced page writer.  Replaces write_kv_cache_pages
+ * (softmax_attention/page.py:32-73, kernels/kv_cache_write.py:153).
+ * slices: (3, n_cols) int32 = (cache_row_start, new_row_start, length) per
+ * column over the flat (num_pages * page_size) row view; columns
+ * j < *num_slices are copied.
+ */
+int fw_write_kv_cache_pages(const void *k, const void *v, void *kv_cache,
+                            const int32_t *slices, int32_t n_cols,
+                            const int32_t *num_slices, int32_t total_tokens,
+                            int32_t nheads_k, int32_t head_dim,
+                            int32_t num_rows, int32_t kv_dtype,
+                            fw_stream_t stream);
+
+/*
+ * Flash-attention forward (prefill) on bf16 MFMA.  Replaces the dense,
+ * packed-varlen and paged-varlen forward kernels:
+ *   FW_KV_DENSE  fwd_dense.flash_attn_forward (kernels/fwd_dense.py:1023)
+ *   FW_KV_VARLEN fwd_varlen.flash_attn_forward_varlen (kernels/fwd_varlen.py:1129)
+ *   FW_KV_PAGED  fwd_paged.flash_attn_varlen_paged (kernels/fwd_paged.py:1351)
+ *
+ * q / out addressed as base + b*stride_b + h*stride_h + t*stride_t (elements,
+ * bf16); for varlen modes b is 0 and t the packed token index.
+ * Dense:   k / v (batch, nheads_k, seqlen_k, head_dim) with strides.
+ * Varlen:  k / v packed by cu_seqlens_k, same stride convention (b = 0).
+ * Paged:   k = merged pool, v = NULL; seqused_k (batch,) gives each
+ *          sequence's kv length; block_table (batch, max_pages).
+ * Causal / window are bottom-right aligned per sequence.  Rows with no
+ * visible key and packed padding rows return out 0, lse -inf (or the sink).
+ * lse is written at lse + b*lse_stride_b + h*lse_stride_h + t (f32), if given.
+ * workspace: fw_prefill_workspace_bytes() bytes (varlen / paged schedules).
+ */
+enum fw_kv_mode { FW_KV_DENSE = 0, FW_KV_VARLEN = 1, FW_KV_PAGED = 2 };
+
+typedef struct fw_prefill_params {
+  int32_t kv_mode;
+  const void *q;
+  void *out;
+  float *lse;
+  const void *k;
+  const void *v;
+  const int32_t *cu_seqlens_q; /* varlen / paged */
+  const int32_t *cu_seqlens_k; /* varlen */
+  const int32_t *seqused_k;    /* paged */
+  const int32_t *block_table;  /* paged */
+  const int32_t *num_active;   /* paged, or NULL */
+  const float *sinks;
+  void *workspace;
+  size_t workspace_bytes;
+  int64_t q_stride_b, q_stride_h, q_stride_t;
+  int64_t o_stride_b, o_stride_h, o_stride_t;
+  int64_t k_stride_b, k_stride_h, k_stride_t;
+  int64_t v_stride_b, v_stride_h, v_stride_t;
+  int64_t lse_stride_b, lse_stride_h;
+  int32_t batch, nheads, nheads_k, head_dim;
+  int32_t seqlen_q, seqlen_k; /* dense: lengths; varlen/paged: total_q, total_k */
+  int32_t max_seqlen_q;       /* varlen / paged: longest request's q length */
+  int32_t page_size, num_pages, max_pages;
+  int32_t kv_dtype;
+  float softmax_scale, softcap;
+  int32_t causal, window_left, window_right;
+  float k_descale, v_descale;
+} fw_prefill_params;
+
+size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);
+int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLYWHEEL_HIP_H */

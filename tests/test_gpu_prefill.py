@@ -1,0 +1,196 @@
+"""GPU parity of the MFMA prefill kernel (dense, packed varlen, paged varlen,
+and chunked prefill through flash_attn_with_kvcache) against the oracle."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flywheel_tpu import flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache
+from oracle import attention as A
+from oracle import paged as P
+from tests.gpu_util import (DEV, FP8, PagedCase, announce, assert_close, assert_lse, codes_of,
+                            dev_from_codes, randn, to_dev_bf16)
+
+pytestmark = pytest.mark.gpu
+
+
+def head_major(x):  # (B, S, H, D) -> (B, H, S, D)
+    return np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize(
+    "b,h,hk,sq,sk,causal,window,softcap,sinks",
+    [
+        (1, 8, 2, 512, 512, True, (-1, -1), 0.0, False),
+        (2, 4, 4, 200, 333, True, (-1, -1), 0.0, False),
+        (1, 4, 1, 333, 200, True, (-1, -1), 0.0, False),  # leading rows see nothing
+        (1, 8, 2, 300, 300, False, (-1, -1), 0.0, False),
+        (2, 4, 2, 257, 257, False, (64, 17), 0.0, False),
+        (1, 4, 2, 384, 384, True, (100, -1), 30.0, False),
+        (1, 4, 2, 130, 130, True, (-1, -1), 0.0, True),
+    ],
+)
+def test_flash_attn_func(b, h, hk, sq, sk, causal, window, softcap, sinks):
+    announce(f"dense b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window} softcap={softcap}")
+    rng = np.random.default_rng(10)
+    q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
+    s = rng.standard_normal(h).astype(np.float32) if sinks else None
+    out, lse = flash_attn_func(
+        to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)), to_dev_bf16(head_major(v)),
+        causal=causal, window_size=window, softcap=softcap, return_softmax_lse=True,
+        learnable_sink=None if s is None else torch.tensor(s, device=DEV))
+    torch.cuda.synchronize()
+    ro, rl = A.attention_ref(q, k, v, causal=causal, window_size=window, softcap=softcap, sinks=s,
+                             round_scaled_q=True)
+    assert_close(out.float().cpu().numpy(), head_major(ro))
+    assert_lse(lse.cpu().numpy(), rl)
+
+
+def test_flash_attn_func_layouts():
+    """token_major and heads_outer_fold address the same math in place."""
+    announce("dense layouts")
+    rng = np.random.default_rng(11)
+    b, h, hk, s, d = 2, 4, 2, 160, 128
+    q, k, v = randn(rng, (b, s, h, d)), randn(rng, (b, s, hk, d)), randn(rng, (b, s, hk, d))
+    ro, _ = A.attention_ref(q, k, v, causal=True, round_scaled_q=True)
+    out = flash_attn_func(to_dev_bf16(q.reshape(b, s, h * d)), to_dev_bf16(k.reshape(b, s, hk * d)),
+                          to_dev_bf16(v.reshape(b, s, hk * d)), causal=True, head_dim=d,
+                          token_major=True)
+    assert_close(out.float().cpu().numpy().reshape(b, s, h, d), ro)
+    hof = lambda x: np.ascontiguousarray(x.transpose(2, 0, 1, 3))  # (H, B, S, D)
+    out = flash_attn_func(to_dev_bf16(hof(q)), to_dev_bf16(hof(k)), to_dev_bf16(hof(v)),
+                          causal=True, heads_outer_fold=True)
+    assert_close(out.float().cpu().numpy(), hof(ro))
+
+
+def test_flash_attn_func_c2_full_size():
+    """BASELINE config 2 at full size; the oracle checks 4 of the 32 heads."""
+    announce("dense C2 1x32/4x4096")
+    rng = np.random.default_rng(12)
+    q, k, v = randn(rng, (1, 4096, 32, 128)), randn(rng, (1, 4096, 4, 128)), randn(rng, (1, 4096, 4, 128))
+    out, lse = flash_attn_func(to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)),
+                               to_dev_bf16(head_major(v)), causal=True, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    heads = [0, 9, 18, 31]  # query head h reads KV head h // 8
+    outs = out.float().cpu().numpy()
+    lses = lse.cpu().numpy()
+    for hh in heads:
+        ro, rl = A.attention_ref(q[:, :, [hh]], k[:, :, [hh // 8]], v[:, :, [hh // 8]], causal=True,
+                                 round_scaled_q=True)
+        assert_close(outs[:, hh], ro[:, :, 0], what=f"head {hh}")
+        assert_lse(lses[:, [hh]], rl)
+
+
+@pytest.mark.parametrize("causal,window,softcap", [(True, (-1, -1), 0.0), (False, (-1, -1), 0.0),
+                                                   (True, (50, -1), 20.0)])
+def test_flash_attn_varlen_packed(causal, window, softcap):
+    announce(f"varlen packed causal={causal} window={window}")
+    rng = np.random.default_rng(13)
+    qlens, klens = [5, 130, 1, 300], [9, 130, 40, 512]
+    h, hk, d = 8, 2, 128
+    cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    pad = 7
+    q = randn(rng, (h, cu_q[-1] + pad, d))
+    k = randn(rng, (hk, cu_k[-1] + 3, d))
+    v = randn(rng, (hk, cu_k[-1] + 3, d))
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), torch.tensor(cu_q, device=DEV),
+        torch.tensor(cu_k, device=DEV), max(qlens), max(klens), causal=causal, window_size=window,
+        softcap=softcap, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    outs, lses = out.float().cpu().numpy(), lse.cpu().numpy()
+    for s in range(4):
+        qs = q[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2)[None]
+        ks = k[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        vs = v[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        ro, rl = A.attention_ref(qs, ks, vs, causal=causal, window_size=window, softcap=softcap,
+                                 round_scaled_q=True)
+        got = outs[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2)
+        rows_ok = np.isfinite(rl[0]).all(axis=0)  # rows with no visible key are unspecified
+        assert_close(got[rows_ok], ro[0][rows_ok], what=f"seq {s}")
+        assert_lse(lses[:, cu_q[s]:cu_q[s + 1]][:, rows_ok], rl[0][:, rows_ok])
+    assert not outs[:, cu_q[-1]:].any()
+    assert np.isneginf(lses[:, cu_q[-1]:]).all()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "e4m3", "e5m2"])
+def test_paged_varlen_read_only(dtype):
+    """flash_attn_varlen_func(block_table=...) over a merged pool; reference
+    edge case random_ragged_case lengths (3, 0, 5) on prefixes (127, 0, 251)."""
+    announce(f"paged varlen {dtype}")
+    rng = np.random.default_rng(14)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.5, 2.0)
+    qlens = [3, 0, 5, 200]
+    prefix = [127, 0, 251, 1000]
+    totals = np.array(qlens) + np.array(prefix)
+    case = PagedCase(rng, batch=4, nheads=4, nheads_k=2, lengths=totals, new_tokens=[0] * 4,
+                     dtype=dt, k_descale=ks, v_descale=vs)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = randn(rng, (cu[-1] + 7, 4, 128))
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
+        torch.tensor(cu, device=DEV), None, max(qlens), int(totals.max()), causal=True,
+        return_softmax_lse=True, block_table=torch.tensor(case.table, device=DEV),
+        seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), k_descale=ks,
+        v_descale=vs, nheads_k=2)
+    torch.cuda.synchronize()
+    kp, vp = case.kv_pages(case.pool_codes)
+    ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True, k_descale=ks,
+                                v_descale=vs, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy().transpose(1, 0, 2), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
+def test_chunked_prefill_kvcache(dtype):
+    """BASELINE config 4's call at reduced size: packed chunks appended to the
+    paged cache then attended causally with a sliding window and softcap;
+    num_active leaves the last request out."""
+    announce(f"chunked prefill {dtype}")
+    rng = np.random.default_rng(15)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (1.5, 0.7)
+    chunks = [256, 700, 1, 129, 64]
+    prior = [0, 3000, 17, 999, 50]
+    case = PagedCase(rng, batch=5, nheads=8, nheads_k=2, lengths=prior, new_tokens=chunks,
+                     dtype=dt, k_descale=ks, v_descale=vs)
+    cu = case.cu
+    q = randn(rng, (cu[-1] + 5, 8, 128))
+    k_dev = dev_from_codes(np.concatenate([case.k_codes, np.zeros((5, 2, 128), case.k_codes.dtype)]), dt)
+    v_dev = dev_from_codes(np.concatenate([case.v_codes, np.zeros((5, 2, 128), case.v_codes.dtype)]), dt)
+    pool = case.pool()
+    out, lse, pool2 = flash_attn_with_kvcache(
+        to_dev_bf16(q), pool, None, k_dev, v_dev,
+        cache_seqlens=torch.tensor(prior, dtype=torch.int32, device=DEV),
+        block_table=torch.tensor(case.table, device=DEV),
+        cu_seqlens_q=torch.tensor(cu, device=DEV), max_seqlen_q=max(chunks), causal=True,
+        window_size=(4095 // 8, 0), softcap=50.0, return_softmax_lse=True, num_active=4,
+        k_descale=ks, v_descale=vs)
+    torch.cuda.synchronize()
+    assert pool2 is pool
+    exp_pool = case.expected_pool(num_active=4)
+    np.testing.assert_array_equal(codes_of(pool), exp_pool)
+    kp, vp = case.kv_pages(exp_pool)
+    totals = case.lengths + case.new_tokens
+    ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True,
+                                window_left=4095 // 8, softcap=50.0, k_descale=ks, v_descale=vs,
+                                round_scaled_q=True, num_active=4)
+    assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
+    assert not out[cu[4]:].float().abs().sum().item()
+
+
+def test_prefill_bitwise_repeat():
+    """test_prefill.py:827-875's race check: repeats are bitwise equal."""
+    announce("dense repeat")
+    rng = np.random.default_rng(16)
+    q = to_dev_bf16(randn(rng, (1, 8, 1024, 128)))
+    k = to_dev_bf16(randn(rng, (1, 2, 1024, 128)))
+    v = to_dev_bf16(randn(rng, (1, 2, 1024, 128)))
+    ref = flash_attn_func(q, k, v, causal=True)
+    for _ in range(20):
+        assert torch.equal(flash_attn_func(q, k, v, causal=True), ref)
