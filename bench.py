@@ -1,0 +1,354 @@
+"""Benchmark of the softmax-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|all]
+
+Workloads (inputs synthetic, seeded, resident in HBM
+before the timed region):
+  c2  flash_attn_func causal GQA prefill, 1 x 32q/4kv x 4096 x 128, bf16
+      -> TFLOP/s (4*S^2*H*D/2 algorithmic FLOPs), roofline vs dense bf16 MFMA
+  c3  flash_attn_with_kvcache paged decode + fused append, B=64, 32q/8kv,
+      page 16, ctx U[1024, 32768] -> HBM GB/s (sum (len+1)*4 KiB + writes)
+  c4  ragged chunked prefill over the paged cache (append + attend), 8 requests,
+      chunk U[256, 2048], prior U[0, 16384], window (4095, 0), softcap 50
+      -> TFLOP/s
+  c5  fp8 e4m3 paged decode with a 4-token verify window, B=128,
+      ctx U[4096, 65536] -> HBM GB/s
+The printed JSON line's headline is c2; with
+--workload all (the default) c3/c4/c5 follow in "also".  Each carries
+"roofline" (events on the launch stream) and "cpu_baseline" (the NumPy oracle on
+a bounded sample, host cores).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flywheel-tpu_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "paged decode HBM GB/s (% of 8 TB/s); prefill TFLOP/s (% MFMA peak)"
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+CPU_THREADS = 16
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup):
+    """Mean ms per call of fn over `steps` calls after `warmup`, bracketed by
+    events on the current stream (the stream every kernel is launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_time(fn, min_rounds=3):
+    """Median seconds of fn over rounds after one warm-up."""
+    fn()
+    ts = []
+    for _ in range(min_rounds):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, copy-calibrated), from profiles/traffic_<name>.txt."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
+def cpu_limits():
+    try:
+        from threadpoolctl import threadpool_limits
+        return threadpool_limits(limits=CPU_THREADS)
+    except ImportError:  # pragma: no cover
+        import contextlib
+        return contextlib.nullcontext()
+
+
+# ------------------------------------------------------------------ workloads
+
+
+def paged_pool(gen, rng, lengths, new_tokens, hk, d, page, dtype, device, descales=(1.0, 1.0)):
+    """Pool sized to the total (+ slack), block table = random permutation; an
+    fp8 pool stores N(0,1)/descale (K rows by k_descale, V rows by v_descale)."""
+    need = [-(-(int(l) + new_tokens) // page) for l in lengths]
+    num_pages = sum(need) + 8
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.zeros((len(lengths), max(need)), np.int32)
+    o = 0
+    for r, c in enumerate(need):
+        table[r, :c] = perm[o:o + c]
+        o += c
+    ch = 2 * hk if dtype == torch.bfloat16 else 2 * (hk + hk % 2)
+    pool = torch.empty((num_pages, page, ch, d), dtype=dtype, device=device)
+    chunk = 8192
+    for i in range(0, num_pages, chunk):
+        x = torch.randn((min(chunk, num_pages - i), page, ch, d), generator=gen, device=device)
+        if dtype != torch.bfloat16:
+            x[:, :, 0:2 * hk:2] /= descales[0]
+            x[:, :, 1:2 * hk:2] /= descales[1]
+            x[:, :, 2 * hk:] = 0
+        pool[i:i + chunk] = x.to(dtype)
+    return pool, torch.from_numpy(table).to(device), table
+
+
+def workload_c2(args, device):
+    from flywheel_tpu import flash_attn_func
+    b, h, hk, s, d = 1, 32, 4, 4096, 128
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    flops = 4.0 * s * s * h * d / 2 * b
+    ms = timed(lambda: flash_attn_func(q, k, v, causal=True), args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    def cpu():
+        from oracle import attention as A
+        rng = np.random.default_rng(0)
+        heads = 8  # sample: 8 of the 32 heads (2 KV heads), full 4096 length
+        qc = rng.standard_normal((1, s, heads, d), dtype=np.float32)
+        kc = rng.standard_normal((1, s, 2, d), dtype=np.float32)
+        vc = rng.standard_normal((1, s, 2, d), dtype=np.float32)
+        with cpu_limits():
+            t = cpu_time(lambda: A.attention_ref(qc, kc, vc, causal=True))
+        return {"value": round(4.0 * s * s * heads * d / 2 / t / 1e12, 5), "unit": "TFLOP/s",
+                "cores": CPU_THREADS, "kind": "port",
+                "sample": "oracle.attention_ref, 8 of 32 heads (2 KV heads) at full 4096 causal,"
+                          " median of 3 after 1 warm-up"}
+
+    return dict(
+        name="c2", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_func causal GQA prefill", "batch": b, "nheads": h,
+                "nheads_k": hk, "seqlen": s, "head_dim": d, "layout": "head-major (B,H,S,D)"},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                  "traffic": read_traffic("c2"), "kernel": "fw_prefill_kernel<DENSE,bf16>",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=cpu)
+
+
+def workload_c3(args, device):
+    from flywheel_tpu import flash_attn_with_kvcache
+    b, h, hk, d, page = 64, 32, 8, 128, 16
+    rng = np.random.default_rng(0)
+    lengths = rng.integers(1024, 32768 + 1, b)
+    gen = torch.Generator(device=device).manual_seed(0)
+    pool, table, table_np = paged_pool(gen, rng, lengths, 1, hk, d, page, torch.bfloat16, device)
+    q = torch.randn((b, 1, h, d), generator=gen, device=device, dtype=torch.bfloat16)
+    kn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    vn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    step = lambda: flash_attn_with_kvcache(q, pool, None, kn, vn, cache_seqlens=lens,
+                                           block_table=table)
+    ms = timed(step, args.steps, args.warmup)
+    row_bytes = 2 * hk * d * 2
+    nbytes = (float(np.sum(lengths + 1)) * row_bytes + b * row_bytes + 2 * q.numel() * 2
+              + sum(-(-(int(l) + 1) // page) for l in lengths) * 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def cpu():
+        from oracle import attention as A
+        from oracle import paged as P
+        rows = 4  # sample: 4 of the 64 rows, gathered from the same pool
+        pl = pool.view(torch.int16)
+        with cpu_limits():
+            sel = list(range(rows))
+            tabs = table_np[sel]
+            used = np.unique(tabs)
+            codes = pl[torch.from_numpy(used).to(device)].cpu().numpy().view(np.uint16)
+            remap = {int(p): i for i, p in enumerate(used)}
+            tloc = np.vectorize(lambda p: remap[int(p)])(tabs)
+            from oracle.dtypes import bf16_to_f32
+            kp, vp = P.split_kv_heads(bf16_to_f32(codes), hk)
+            krows, vrows = P.gather_rows(kp, tloc), P.gather_rows(vp, tloc)
+            qn = q[:rows].float().cpu().numpy()
+            tot = lengths[:rows] + 1
+            t = cpu_time(lambda: A.kvcache_reference(qn, krows, vrows, tot))
+        sample_bytes = float(np.sum(tot)) * row_bytes
+        return {"value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": CPU_THREADS,
+                "kind": "port",
+                "sample": f"oracle.kvcache_reference on rows 0..{rows - 1} of the same pool"
+                          f" ({int(np.sum(tot))} keys), median of 3 after 1 warm-up"}
+
+    return dict(
+        name="c3", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_with_kvcache paged decode + fused append", "batch": b,
+                "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
+                "ctx": "U[1024, 32768]", "mean_ctx": float(lengths.mean())},
+        roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                  "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic("c3"),
+                  "kernel": "fw_decode_kernel<bf16> + fw_decode_combine (whole step)",
+                  "algorithmic_per_launch": f"{nbytes:.4e} B"},
+        cpu=cpu)
+
+
+def workload_c4(args, device):
+    from flywheel_tpu import flash_attn_with_kvcache
+    n, h, hk, d, page, window = 8, 32, 8, 128, 16, 4096
+    rng = np.random.default_rng(0)
+    chunks = rng.integers(256, 2048 + 1, n)
+    prior = rng.integers(0, 16384 + 1, n)
+    gen = torch.Generator(device=device).manual_seed(0)
+    totals = prior + chunks
+    need = [-(-int(t) // page) for t in totals]
+    num_pages = sum(need) + 8
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.zeros((n, max(need)), np.int32)
+    o = 0
+    for r, c in enumerate(need):
+        table[r, :c] = perm[o:o + c]
+        o += c
+    pool = torch.randn((num_pages, page, 2 * hk, d), generator=gen, device=device,
+                       dtype=torch.bfloat16)
+    tq = int(chunks.sum())
+    q = torch.randn((tq, h, d), generator=gen, device=device, dtype=torch.bfloat16)
+    kn = torch.randn((tq, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    vn = torch.randn((tq, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(chunks)]), dtype=torch.int32, device=device)
+    lens = torch.tensor(prior, dtype=torch.int32, device=device)
+    tab = torch.from_numpy(table).to(device)
+    step = lambda: flash_attn_with_kvcache(
+        q, pool, None, kn, vn, cache_seqlens=lens, block_table=tab, cu_seqlens_q=cu,
+        max_seqlen_q=int(chunks.max()), causal=True, window_size=(window - 1, 0), softcap=50.0)
+    ms = timed(step, args.steps, args.warmup)
+    pairs = 0
+    for p, c in zip(prior, chunks):
+        vis = np.minimum(p + np.arange(c) + 1, window)
+        pairs += int(vis.sum())
+    flops = 4.0 * h * d * pairs
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(
+        name="c4", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        config={"workload": "ragged chunked prefill over paged cache (append + attend)",
+                "requests": n, "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
+                "window_size": [window - 1, 0], "softcap": 50.0, "total_q": tq,
+                "visible_pairs": pairs},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                  "traffic": read_traffic("c4"),
+                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_kernel<PAGED> (whole step)",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=None)
+
+
+def workload_c5(args, device):
+    from flywheel_tpu import flash_attn_with_kvcache
+    b, h, hk, d, page, sq = 128, 32, 8, 128, 16, 4
+    rng = np.random.default_rng(0)
+    lengths = rng.integers(4096, 65536 + 1, b)
+    k_descale, v_descale = (float(x) for x in rng.uniform(0.5, 2.0, 2))
+    gen = torch.Generator(device=device).manual_seed(0)
+    pool, table, _ = paged_pool(gen, rng, lengths, sq, hk, d, page, torch.float8_e4m3fn, device,
+                                descales=(k_descale, v_descale))
+    q = torch.randn((b, sq, h, d), generator=gen, device=device, dtype=torch.bfloat16)
+    kn = (torch.randn((b, sq, hk, d), generator=gen, device=device) / k_descale).to(torch.float8_e4m3fn)
+    vn = (torch.randn((b, sq, hk, d), generator=gen, device=device) / v_descale).to(torch.float8_e4m3fn)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    step = lambda: flash_attn_with_kvcache(q, pool, None, kn, vn, cache_seqlens=lens,
+                                           block_table=table, causal=True, k_descale=k_descale,
+                                           v_descale=v_descale)
+    ms = timed(step, args.steps, args.warmup)
+    nbytes = float(np.sum(lengths + sq)) * 2 * hk * d * 1
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(
+        name="c5", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
+        config={"workload": "fp8 e4m3 paged decode, 4-token verify window", "batch": b,
+                "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
+                "ctx": "U[4096, 65536]", "k_descale": k_descale, "v_descale": v_descale},
+        roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                  "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic("c5"),
+                  "kernel": "fw_append_kernel + fw_decode_kernel<e4m3> + fw_decode_combine (whole step)",
+                  "algorithmic_per_launch": f"{nbytes:.4e} B"},
+        cpu=None)
+
+
+WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all", choices=["all", *WORKLOADS])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build's hot path is a single-GPU kernel set"
+              " (no collectives); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    names = list(WORKLOADS) if args.workload == "all" else [args.workload]
+    results = []
+    for name in names:
+        log(f"workload {name}")
+        r = WORKLOADS[name](args, device)
+        log(f"{name}: {r['value']:.2f} {r['unit']} ({r['ms']:.4f} ms/step)")
+        if not args.no_cpu and r.get("cpu") is not None:
+            log(f"{name}: timing the CPU oracle")
+            r["cpu_baseline"] = r["cpu"]()
+        else:
+            r["cpu_baseline"] = None
+        r.pop("cpu", None)
+        results.append(r)
+        torch.cuda.empty_cache()
+    head = results[0]
+    line = {
+        "metric": METRIC,
+        "value": round(head["value"], 3),
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded N(0,1) inputs resident in HBM)",
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+    }
+    also = []
+    for r in results[1:]:
+        also.append({"workload": r["name"], "value": round(r["value"], 3), "unit": r["unit"],
+                     "ms_per_step": round(r["ms"], 5), "dtype": r["dtype"], "config": r["config"],
+                     "roofline": r["roofline"], "cpu_baseline": r["cpu_baseline"]})
+    if also:
+        line["also"] = also
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
