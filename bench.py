@@ -289,7 +289,22 @@ def workload_c5(args, device):
         cpu=None)
 
 
+def workload_copy(args, device):
+    """Calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a plain device
+    copy of exactly 1 GiB per step (reads 1 GiB, writes 1 GiB)."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    ms = timed(lambda: dst.copy_(src), args.steps, args.warmup)
+    gbs = 2 * (1 << 30) / (ms * 1e-3) / 1e9
+    return dict(name="copy", unit="GB/s", value=gbs, ms=ms, dtype="u8",
+                config={"workload": "calibration copy, 1 GiB read + 1 GiB write"},
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                cpu=None)
+
+
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
+EXTRA = {"copy": workload_copy}
 
 
 def main():
@@ -297,7 +312,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", choices=["all", *WORKLOADS])
+    ap.add_argument("--workload", default="all", choices=["all", *WORKLOADS, *EXTRA])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -312,7 +327,7 @@ def main():
     results = []
     for name in names:
         log(f"workload {name}")
-        r = WORKLOADS[name](args, device)
+        r = {**WORKLOADS, **EXTRA}[name](args, device)
         log(f"{name}: {r['value']:.2f} {r['unit']} ({r['ms']:.4f} ms/step)")
         if not args.no_cpu and r.get("cpu") is not None:
             log(f"{name}: timing the CPU oracle")

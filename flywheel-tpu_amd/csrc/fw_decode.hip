@@ -22,6 +22,10 @@
 // Both products use v_mfma_f32_16x16x32_bf16; nothing goes through LDS.
 #include "fw_common.h"
 
+#include <algorithm>
+#include <type_traits>
+#include <cstdlib>
+
 namespace fw {
 
 struct DecodeArgs {
@@ -51,28 +55,39 @@ __device__ __forceinline__ int row_lo_all(const DecodeArgs &a, int total) {
   return lo > 0 ? lo : 0;
 }
 
+// K of one key row: bf16 is loaded straight into the A-operand registers;
+// fp8 stays as raw bytes (two 16-byte loads) until the compute stage.
 template <int KV>
-__device__ __forceinline__ void load_k_op(const uint8_t *row, int g, bf16x8_t (&op)[4]) {
+struct KRow {
+  typename std::conditional<KV == FW_BF16, bf16x8_t, u32x4_t>::type w[KV == FW_BF16 ? 4 : 2];
+};
+
+template <int KV>
+__device__ __forceinline__ void load_k_row(const uint8_t *row, int g, KRow<KV> &k) {
   if constexpr (KV == FW_BF16) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      op[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(row + 64 * j + 16 * g));
+      k.w[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(row + 64 * j + 16 * g));
   } else {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      u32x4_t w = *(const u32x4_t *)(row + 64 * hh + 16 * g);
-      u32x4_t lo, hi;
-      lo[0] = fp8x2_to_bf16x2<KV>(w[0], false);
-      lo[1] = fp8x2_to_bf16x2<KV>(w[0], true);
-      lo[2] = fp8x2_to_bf16x2<KV>(w[1], false);
-      lo[3] = fp8x2_to_bf16x2<KV>(w[1], true);
-      hi[0] = fp8x2_to_bf16x2<KV>(w[2], false);
-      hi[1] = fp8x2_to_bf16x2<KV>(w[2], true);
-      hi[2] = fp8x2_to_bf16x2<KV>(w[3], false);
-      hi[3] = fp8x2_to_bf16x2<KV>(w[3], true);
-      op[2 * hh] = __builtin_bit_cast(bf16x8_t, lo);
-      op[2 * hh + 1] = __builtin_bit_cast(bf16x8_t, hi);
-    }
+    for (int hh = 0; hh < 2; ++hh) k.w[hh] = *(const u32x4_t *)(row + 64 * hh + 16 * g);
+  }
+}
+
+// A operand of MFMA step j from a loaded K row.
+template <int KV>
+__device__ __forceinline__ bf16x8_t k_operand(const KRow<KV> &k, int j) {
+  if constexpr (KV == FW_BF16) {
+    return k.w[j];
+  } else {
+    const u32x4_t w = k.w[j >> 1];
+    const int o = 2 * (j & 1);
+    u32x4_t r;
+    r[0] = fp8x2_to_bf16x2<KV>(w[o], false);
+    r[1] = fp8x2_to_bf16x2<KV>(w[o], true);
+    r[2] = fp8x2_to_bf16x2<KV>(w[o + 1], false);
+    r[3] = fp8x2_to_bf16x2<KV>(w[o + 1], true);
+    return __builtin_bit_cast(bf16x8_t, r);
   }
 }
 
@@ -84,14 +99,31 @@ __device__ __forceinline__ int qk_dim(int j, int g) {
 }
 
 template <int KV>
-__global__ __launch_bounds__(256) void fw_decode_kernel(DecodeArgs a) {
+struct DecodeTile {
+  KRow<KV> krow[2];  // K of the two 16-key sub-tiles (lane row n)
+  // V of keys 4g+i / 16+4g+i, dims 8n .. 8n+7 (16 or 8 bytes a key)
+  typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8];
+};
+
+
+// Register-ring depth and waves/SIMD: bf16 2 stages at 2 waves; fp8 2 stages
+// at 3 waves (its tiles are half the bytes, so more waves keep more in flight).
+template <int KV> constexpr int kDecodeStages = 2;
+template <int KV> constexpr int kDecodeWaves = KV == FW_BF16 ? 2 : 3;
+
+template <int KV>
+__global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(DecodeArgs a) {
   constexpr int EB = KV == FW_BF16 ? 2 : 1;  // bytes per cache element
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int s = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int h = blockIdx.y / a.n_qtiles;
-  const int qt = blockIdx.y % a.n_qtiles;
+  // A workgroup's waves are the KV heads (and q tiles) of one (row, split):
+  // they walk the same pages at the same time.
+  const int s = blockIdx.x;
+  const int hq_item = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (hq_item >= a.Hk * a.n_qtiles) return;
+  const int h = hq_item / a.n_qtiles;
+  const int qt = hq_item % a.n_qtiles;
   const int b = blockIdx.z;
   if (s >= a.nsplit) return;
   if (a.num_active && b >= *a.num_active) return;
@@ -158,61 +190,91 @@ __global__ __launch_bounds__(256) void fw_decode_kernel(DecodeArgs a) {
   const size_t vh_off = (size_t)(2 * h + 1) * kD * EB;
   const size_t new_off = ((size_t)b * a.Hk + h) * kD * EB;
   const int last_key = total - 1;
+  // Block-table entries of the whole split, one per lane (a split spans at
+  // most 64 pages); a sub-tile's page is then a readlane, off the load path.
+  const int first_page = k_begin / a.P;
+  const int tbl_lane = table[min(first_page + lane, a.max_pages - 1)];
 
-  for (int tb = k_begin; tb < k_end; tb += 32) {
-    // -------- loads: K rows (A operand) and V rows for both sub-tiles.
-    bf16x8_t kop[2][4];
-    u32x2_t vraw[8][2];
+  // Per-lane byte offsets inside a 16-row sub-tile: a load is the sub-tile's
+  // uniform page row pointer plus a 32-bit lane offset.
+  const uint32_t k_lane_off = (uint32_t)(n * row_bytes + kh_off);
+  uint32_t v_lane_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v_lane_off[i] = (uint32_t)((4 * g + i) * row_bytes + vh_off + (KV == FW_BF16 ? 16 : 8) * n);
+
+  // Loads are branch-free so the compiler can count them: a tile past the end
+  // is clamped onto the last valid sub-tile (an L2 hit, never used).
+  auto load_tile = [&](int tb, DecodeTile<KV> &tl) {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      int sb = tb + 16 * sub;
-      int sbc = min(sb, last_key) & ~15;  // clamp the sub-tile into valid pages
-      const int page = min(max(table[sbc / a.P], 0), a.num_pages - 1);
+      const int sbc = min(tb + 16 * sub, last_key) & ~15;  // clamp into valid pages
+      int page = __builtin_amdgcn_readlane(tbl_lane, sbc / a.P - first_page);
+      page = min(max(page, 0), a.num_pages - 1);
       const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
-      // K: lane row n
-      {
-        int key = sbc + n;
-        const uint8_t *kp = prow + (size_t)n * row_bytes + kh_off;
-        if (a.has_new && key == L0) kp = a.k_new + new_off;
-        load_k_op<KV>(kp, g, kop[sub]);
-      }
-      // V: keys sbc + 4g + i
+      load_k_row<KV>(prow + k_lane_off, g, tl.krow[sub]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int kr = 4 * g + i;
-        int key = sbc + kr;
-        const uint8_t *vp = prow + (size_t)kr * row_bytes + vh_off;
-        if (a.has_new && key == L0) vp = a.v_new + new_off;
-        if constexpr (KV == FW_BF16) {
-          vraw[4 * sub + i][0] = *(const u32x2_t *)(vp + 8 * n);
-          vraw[4 * sub + i][1] = *(const u32x2_t *)(vp + 128 + 8 * n);
-        } else {
-          vraw[4 * sub + i][0] = *(const u32x2_t *)(vp + 8 * n);
-        }
+        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(prow + v_lane_off[i]);
+        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(prow + v_lane_off[i]);
       }
     }
+  };
+  // The appended token's K/V, from k_new / v_new into every key slot (only the
+  // slot of key L0 is unmasked).
+  auto load_new_tile = [&](DecodeTile<KV> &tl) {
+    const uint8_t *kp = a.k_new + new_off;
+    const uint8_t *vp = a.v_new + new_off + (KV == FW_BF16 ? 16 : 8) * n;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) load_k_row<KV>(kp, g, tl.krow[sub]);
+#pragma unroll
+    for (int k8 = 0; k8 < 8; ++k8) {
+      if constexpr (KV == FW_BF16) tl.vraw[k8] = *(const u32x4_t *)vp;
+      else tl.vraw[k8] = *(const u32x2_t *)vp;
+    }
+  };
+
+  // Cache keys of this split are [k_begin, k_stop): the appended token (key
+  // L0) is folded in after the loop from k_new / v_new.
+  const int k_stop = a.has_new ? min(k_end, L0) : k_end;
+  const int row_hi = min(key_hi, k_stop);
+  // Keys every row of this wave sees: tiles inside need no mask.
+  int all_lo = row_ok ? key_lo : k_begin, all_hi = row_ok ? row_hi : k_stop;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    all_lo = max(all_lo, __shfl_xor(all_lo, m, 64));
+    all_hi = min(all_hi, __shfl_xor(all_hi, m, 64));
+  }
+
+  auto compute_tile = [&](int tb, const DecodeTile<KV> &tl, int lo, int hi, bool edge) {
     // -------- S^T = K Q^T
     f32x4_t sacc[2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       sacc[sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sacc[sub] = mfma16(kop[sub][j], qop[j], sacc[sub]);
+      for (int j = 0; j < 4; ++j) sacc[sub] = mfma16(k_operand<KV>(tl.krow[sub], j), qop[j], sacc[sub]);
     }
     // -------- online softmax on this lane's 8 (row n, key) scores
     float sc[8];
-    float tmax = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int key = tb + 16 * sub + 4 * g + i;
-        float v = sacc[sub][i];
-        if (a.softcap_log2 != 0.f) v = tanhf(v) * a.softcap_log2;
-        v = (key >= key_lo && key < key_hi) ? v : -INFINITY;
-        sc[4 * sub + i] = v;
-        tmax = fmaxf(tmax, v);
+      for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
+    if (a.softcap_log2 != 0.f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sc[e] = tanhf(sc[e]) * a.softcap_log2;
+    }
+    if (edge) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = tb + 16 * (e >> 2) + 4 * g + (e & 3);
+        sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
       }
+    }
+    float tmax = sc[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sc[e]);
     tmax = wave_max_xor(tmax, 16);
     tmax = wave_max_xor(tmax, 32);
     const float m_new = fmaxf(m_run, tmax);
@@ -223,35 +285,57 @@ __global__ __launch_bounds__(256) void fw_decode_kernel(DecodeArgs a) {
     uint32_t pw[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      float p0 = fast_exp2(sc[2 * p] - m_use);
-      float p1 = fast_exp2(sc[2 * p + 1] - m_use);
+      const float p0 = fast_exp2(sc[2 * p] - m_use);
+      const float p1 = fast_exp2(sc[2 * p + 1] - m_use);
       psum += p0 + p1;
       pw[p] = pack_bf16(p0, p1);
     }
     l_run = l_run * alpha + psum;
-    const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, (u32x4_t){pw[0], pw[1], pw[2], pw[3]});
-    // -------- O^T += V^T P^T, 8 tiles of 16 dims
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      oacc[c] *= alpha;
-      u32x4_t vw;
-      if constexpr (KV == FW_BF16) {
-        const int hh = c >> 2, e = c & 3;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          uint32_t w0 = vraw[2 * p][hh][e >> 1], w1 = vraw[2 * p + 1][hh][e >> 1];
-          vw[p] = (e & 1) ? perm_hi(w0, w1) : perm_lo(w0, w1);
-        }
-      } else {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          uint32_t c0 = fp8x2_to_bf16x2<KV>(vraw[2 * p][0][c >> 2], (c >> 1) & 1);
-          uint32_t c1 = fp8x2_to_bf16x2<KV>(vraw[2 * p + 1][0][c >> 2], (c >> 1) & 1);
-          vw[p] = (c & 1) ? perm_hi(c0, c1) : perm_lo(c0, c1);
-        }
-      }
-      oacc[c] = mfma16(__builtin_bit_cast(bf16x8_t, vw), pop, oacc[c]);
+      for (int c = 0; c < 8; ++c) oacc[c] *= alpha;
     }
+    const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, (u32x4_t){pw[0], pw[1], pw[2], pw[3]});
+    // -------- O^T += V^T P^T, 8 tiles of 16 dims; tile c holds dim 8m + c.
+    // Word w of a key's V (dims 8n+2w, 8n+2w+1) feeds tiles 2w and 2w+1.
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t vk[8];
+#pragma unroll
+      for (int k8 = 0; k8 < 8; ++k8) {
+        if constexpr (KV == FW_BF16) vk[k8] = tl.vraw[k8][w];
+        else vk[k8] = fp8x2_to_bf16x2<KV>(tl.vraw[k8][w >> 1], w & 1);
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4_t vw;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) vw[p] = half ? perm_hi(vk[2 * p], vk[2 * p + 1]) : perm_lo(vk[2 * p], vk[2 * p + 1]);
+        oacc[2 * w + half] = mfma16(__builtin_bit_cast(bf16x8_t, vw), pop, oacc[2 * w + half]);
+      }
+    }
+  };
+
+  // Register ring of two tile buffers: the next tile's loads are in flight
+  // while the current tile is computed.
+  const int last_tile = max(k_begin, (k_stop - 1) & ~31);
+  auto edge = [&](int tb) { return tb < all_lo || tb + 32 > all_hi; };
+  if (k_begin < k_stop) {
+    DecodeTile<KV> t0, t1;
+    load_tile(k_begin, t0);
+    for (int tb = k_begin;; tb += 64) {
+      load_tile(min(tb + 32, last_tile), t1);
+      compute_tile(tb, t0, key_lo, row_hi, edge(tb));
+      if (tb + 32 >= k_stop) break;
+      load_tile(min(tb + 64, last_tile), t0);
+      compute_tile(tb + 32, t1, key_lo, row_hi, edge(tb + 32));
+      if (tb + 64 >= k_stop) break;
+    }
+  }
+  if (a.has_new && L0 >= k_begin && L0 < k_end) {
+    DecodeTile<KV> tn;
+    load_new_tile(tn);
+    compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true);
   }
 
   // ---- write the partial: rows n < Rq of this q tile.
@@ -260,24 +344,13 @@ __global__ __launch_bounds__(256) void fw_decode_kernel(DecodeArgs a) {
   const size_t item = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit + s;
   if (row_ok) {
     float *po = a.ws_o + (item * 16 + n) * kD;
-    if constexpr (KV == FW_BF16) {
-      // tile c = 4hh + e, reg i -> dim 64hh + 16g + 4i + e
+    // tile c, reg i -> dim 32g + 8i + c
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f32x4_t v = {oacc[4 * hh + 0][i], oacc[4 * hh + 1][i], oacc[4 * hh + 2][i], oacc[4 * hh + 3][i]};
-          *(f32x4_t *)(po + 64 * hh + 16 * g + 4 * i) = v;
-        }
-    } else {
-      // tile c, reg i -> dim 32g + 8i + c
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4_t v0 = {oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
-        f32x4_t v1 = {oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]};
-        *(f32x4_t *)(po + 32 * g + 8 * i) = v0;
-        *(f32x4_t *)(po + 32 * g + 8 * i + 4) = v1;
-      }
+    for (int i = 0; i < 4; ++i) {
+      f32x4_t v0 = {oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
+      f32x4_t v1 = {oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]};
+      *(f32x4_t *)(po + 32 * g + 8 * i) = v0;
+      *(f32x4_t *)(po + 32 * g + 8 * i + 4) = v1;
     }
     if (g == 0) a.ws_ml[item * 16 + n] = make_float2(m_run, l_run);
   }
@@ -295,17 +368,17 @@ struct CombineArgs {
   float v_descale;
 };
 
-// One block per (b, kv head, q tile): 16 rows x 16 threads, 8 dims a thread.
+// One block per (b, kv head, q tile).  For each row of the tile, thread t
+// reads the partials of splits s = t/16, t/16 + 16, ... (dims 8*(t%16)..+7),
+// all in parallel, and the 16 split groups merge through LDS.
 __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
-  const int row = threadIdx.x >> 4;
+  __shared__ float s_acc[16][16][8];
+  __shared__ float2 s_ml[16][16];
   const int part = threadIdx.x & 15;
+  const int grp = threadIdx.x >> 4;
   const int h = blockIdx.y / a.n_qtiles;
   const int qt = blockIdx.y % a.n_qtiles;
   const int b = blockIdx.z;
-  const int r = qt * 16 + row;
-  if (r >= a.Rq) return;
-  const int tok = r / a.G;
-  const int hq = h * a.G + r % a.G;
   const bool active = !(a.num_active && b >= *a.num_active);
   int nsp = 0;
   if (active) {
@@ -316,57 +389,94 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
     nsp = total > base ? (total - base + a.split_keys - 1) / a.split_keys : 0;
   }
   const size_t item0 = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit;
-  float M = -INFINITY, Lsum = 0.f;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s = 0; s < nsp; ++s) {
-    const float2 ml = a.ws_ml[(item0 + s) * 16 + row];
-    if (ml.x == -INFINITY) continue;
-    const float Mn = fmaxf(M, ml.x);
-    const float c_old = fast_exp2(M - Mn);
-    const float c_new = fast_exp2(ml.x - Mn);
-    const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
-    const f32x4_t v0 = *(const f32x4_t *)po, v1 = *(const f32x4_t *)(po + 4);
+  const int rows = min(16, a.Rq - qt * 16);
+  for (int row = 0; row < rows; ++row) {
+    float M = -INFINITY, Lsum = 0.f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int s = grp; s < nsp; s += 16) {
+      const float2 ml = a.ws_ml[(item0 + s) * 16 + row];
+      const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
+      const f32x4_t v0 = *(const f32x4_t *)po, v1 = *(const f32x4_t *)(po + 4);
+      if (ml.x == -INFINITY) continue;
+      const float Mn = fmaxf(M, ml.x);
+      const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml.x - Mn);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[e] = acc[e] * c_old + v0[e] * c_new;
-      acc[4 + e] = acc[4 + e] * c_old + v1[e] * c_new;
-    }
-    Lsum = Lsum * c_old + ml.y * c_new;
-    M = Mn;
-  }
-  if (a.sinks) {
-    const float sk = a.sinks[hq] * kLog2e;
-    if (sk != -INFINITY) {
-      const float Mn = fmaxf(M, sk);
-      const float c_old = fast_exp2(M - Mn);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] *= c_old;
-      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = acc[e] * c_old + v0[e] * c_new;
+        acc[4 + e] = acc[4 + e] * c_old + v1[e] * c_new;
+      }
+      Lsum = Lsum * c_old + ml.y * c_new;
       M = Mn;
     }
-  }
-  const bool any = active && Lsum > 0.f;
-  const float scale = any ? a.v_descale / Lsum : 0.f;
-  uint16_t *o = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
-  u32x4_t w;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) w[e] = pack_bf16(acc[2 * e] * scale, acc[2 * e + 1] * scale);
-  *(u32x4_t *)o = w;
-  if (a.lse && part == 0) {
-    float v = any ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
-    if (!active) v = -INFINITY;
-    a.lse[((size_t)b * a.H + hq) * a.Sq + tok] = v;
+    for (int e = 0; e < 8; ++e) s_acc[grp][part][e] = acc[e];
+    if (part == 0) s_ml[grp][0] = make_float2(M, Lsum);
+    __syncthreads();
+    if (grp == 0) {
+      float Mt = -INFINITY;
+      for (int g2 = 0; g2 < 16; ++g2) Mt = fmaxf(Mt, s_ml[g2][0].x);
+      const int r = qt * 16 + row;
+      const int tok = r / a.G, hq = h * a.G + r % a.G;
+      float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float Lt = 0.f;
+      if (Mt != -INFINITY) {
+        for (int g2 = 0; g2 < 16; ++g2) {
+          const float2 ml = s_ml[g2][0];
+          if (ml.x == -INFINITY) continue;
+          const float c = fast_exp2(ml.x - Mt);
+          Lt += ml.y * c;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] += s_acc[g2][part][e] * c;
+        }
+      }
+      if (a.sinks) {
+        const float sk = a.sinks[hq] * kLog2e;
+        if (sk != -INFINITY) {
+          const float Mn = fmaxf(Mt, sk);
+          const float c_old = fast_exp2(Mt - Mn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] *= c_old;
+          Lt = Lt * c_old + fast_exp2(sk - Mn);
+          Mt = Mn;
+        }
+      }
+      const bool any = active && Lt > 0.f;
+      const float scale = any ? a.v_descale / Lt : 0.f;
+      uint16_t *op = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
+      u32x4_t w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = pack_bf16(o[2 * e] * scale, o[2 * e + 1] * scale);
+      *(u32x4_t *)op = w;
+      if (a.lse && part == 0)
+        a.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
+    }
+    __syncthreads();
   }
 }
 
+// Keys per split-K work item: about 32K items at full capacity, at least 256
+// keys, and at most what one lane-per-page table prefetch covers (64 pages
+// from a 32-key-aligned start: 63*P + gcd(32, P) keys).
+static int max_split_keys(int P) {
+  int gcd = 32;
+  while (P % gcd) gcd >>= 1;
+  return (63 * P + gcd) / 32 * 32;
+}
+
 static int pick_split(const fw_decode_params *p, int n_qtiles) {
-  if (p->split_keys > 0) return (p->split_keys + 31) / 32 * 32;
+  const int cap_split = max_split_keys(p->page_size);
+  if (p->split_keys > 0) return std::min((p->split_keys + 31) / 32 * 32, cap_split);
   const long capacity = (long)p->max_pages * p->page_size;
   const long items_per_key = (long)p->batch * p->nheads_k * n_qtiles;
-  long split = (capacity * items_per_key + 16383) / 16384;
+  long split = (capacity * items_per_key + 32767) / 32768;
   split = (split + 31) / 32 * 32;
   if (split < 256) split = 256;
-  if (split > 4096) split = 4096;
+  if (split > 896) split = 896;  // measured optimum for C3 (bf16) and C5 (fp8)
+  if (split > cap_split) split = cap_split;
+  // Power-of-two multiples of 32 keys measured ~20% slower on MI355X (C3
+  // decode: 512 or 1024 keys ~4.3 TB/s, 576..960 keys 5.3-5.5 TB/s).
+  const long units = split / 32;
+  if ((units & (units - 1)) == 0 && split * 3 / 2 <= cap_split) split = split * 3 / 2;
   return (int)split;
 }
 
@@ -452,11 +562,14 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   a.qscale = p->softcap > 0.f ? sm / p->softcap : sm * kLog2e;
   a.softcap_log2 = p->softcap > 0.f ? p->softcap * kLog2e : 0.f;
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid((L.nsplit + 3) / 4, p->nheads_k * L.n_qtiles, p->batch);
+  const int items = p->nheads_k * L.n_qtiles;
+  const int waves = items < 4 ? items : 4;
+  const int threads = 64 * waves;
+  const dim3 grid(L.nsplit, (items + waves - 1) / waves, p->batch);
   switch (p->kv_dtype) {
-    case FW_BF16: fw_decode_kernel<FW_BF16><<<grid, 256, 0, s>>>(a); break;
-    case FW_FP8_E4M3: fw_decode_kernel<FW_FP8_E4M3><<<grid, 256, 0, s>>>(a); break;
-    default: fw_decode_kernel<FW_FP8_E5M2><<<grid, 256, 0, s>>>(a); break;
+    case FW_BF16: fw_decode_kernel<FW_BF16><<<grid, threads, 0, s>>>(a); break;
+    case FW_FP8_E4M3: fw_decode_kernel<FW_FP8_E4M3><<<grid, threads, 0, s>>>(a); break;
+    default: fw_decode_kernel<FW_FP8_E5M2><<<grid, threads, 0, s>>>(a); break;
   }
   st = check_launch("fw_decode_kernel");
   if (st != FW_OK) return st;
