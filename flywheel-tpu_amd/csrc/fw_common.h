@@ -70,6 +70,13 @@ __device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Branch-free tanh: 1 - 2 / (e^{2x} + 1), from the hardware exp2 and rcp.
+// Saturates to +-1 for large |x|; absolute error ~1e-7 (the softcap scales it).
+__device__ __forceinline__ float fast_tanh(float x) {
+  const float t = __builtin_amdgcn_exp2f(x * (2.0f * 1.4426950408889634f));
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(t + 1.0f);
+}
+
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }

@@ -85,7 +85,7 @@ struct KvAddr {
 };
 
 template <int MODE, int KV>
-__global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kKsBytes + kVtBytes];
   uint16_t *Ks = (uint16_t *)smem;
   uint16_t *Vt = (uint16_t *)(smem + kKsBytes);
@@ -170,13 +170,15 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
+    u32x4_t raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      u32x4_t wv = *(const u32x4_t *)(qp + 16 * j + 8 * g);
       u32x4_t o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = row_ok ? pack_bf16(bf16_lo(wv[e]) * a.qscale, bf16_hi(wv[e]) * a.qscale) : 0u;
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
       qop[j] = __builtin_bit_cast(bf16x8_t, o);
     }
   }
@@ -236,36 +238,50 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     const int kb = t * kKT;
     if (!w_any || kb >= w_hi || kb + kKT <= w_lo) continue;  // wave sees nothing here
 
-    // ---------------- S^T = K Q^T : two 32-key sub-tiles
+    // ---------------- S^T = K Q^T : two 32-key sub-tiles.  All 16 K operands
+    // are read up front so the MFMA chain never waits on a single LDS read.
     f32x16_t sacc[2];
+    {
+      bf16x8_t kop[2][8];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+      for (int st = 0; st < 2; ++st) {
+        const uint16_t *kr = Ks + (32 * st + n) * kKS + 8 * g;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
-      const uint16_t *kr = Ks + (32 * st + n) * kKS + 8 * g;
+        for (int j = 0; j < 8; ++j)
+          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(kr + 16 * j));
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bf16x8_t kop = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(kr + 16 * j));
-        sacc[st] = mfma32(kop, qop[j], sacc[st]);
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sacc[st] = mfma32(kop[st][j], qop[j], sacc[st]);
       }
     }
     // ---------------- online softmax (log2 units), lane = query row n
+    if (a.softcap_log2 != 0.f) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
+    }
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
+    if (!full) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
+        }
+    }
     float tmax = -INFINITY;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float v = sacc[st][e];
-        if (a.softcap_log2 != 0.f) v = tanhf(v) * a.softcap_log2;
-        if (!full) {
-          const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          v = (key >= r_lo && key < r_hi) ? v : -INFINITY;
-        }
-        sacc[st][e] = v;
-        tmax = fmaxf(tmax, v);
-      }
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
     tmax = wave_max_xor(tmax, 32);
     const float m_new = fmaxf(m_run, tmax);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -290,17 +306,25 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
     }
-    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles;
+    // the V operands of step u+1 are read while step u's MFMAs run.
+    bf16x8_t vop[2][4];
+    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const uint16_t *vr = Vt + (n + 32 * c) * kVS + 16 * u + 4 * g;
         const u32x2_t lo = *(const u32x2_t *)vr;
         const u32x2_t hi = *(const u32x2_t *)(vr + 8);
-        const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
-        oacc[c] = mfma32(vop, pop[u], oacc[c]);
+        dst[c] = __builtin_bit_cast(bf16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
       }
+    };
+    read_v(0, vop[0]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
     }
   }
 
@@ -334,6 +358,336 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     if (Lsum > 0.f) v = (M + __log2f(Lsum)) * kLn2;
     else v = -INFINITY;
     a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 K/V: tiles go global -> LDS directly (global_load_lds_dwordx4, no
+// staging registers), double-buffered with one barrier per tile.  LDS rows are
+// 256 B (one key's 128 dims) with the 16-byte chunk index XOR-swizzled by
+// (key & 15), which keeps both operand reads bank-conflict-free:
+//   K operand (A of S^T = K Q^T): ds_read_b128 of row (32st + m), chunk 2j+g
+//   V operand (A of O^T = V^T P^T): ds_read_b64_tr_b16 -- within each 16-lane
+//     group, lane 4a+b points at key K0+a, dims 4b..4b+3, and receives dim
+//     (lane % 16) of keys K0..K0+3: the transposed operand without any
+//     transposing store.
+constexpr int kRowB = 256;                 // LDS bytes of one key row
+constexpr int kTileB = kKT * kRowB;        // 16 KiB per K or V tile
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+#define FW_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ void lds_dma16(const void *src, FW_LDS uint8_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, (FW_LDS void *)dst, 16, 0, 0);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
+  // two buffers of [K tile | V tile]
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kTileB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int n = lane & 31;
+  const int g = lane >> 5;
+
+  // ------------------------------------------------------------ tile decode
+  int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
+  if constexpr (MODE == FW_KV_DENSE) {
+    const int nbh = a.B * a.H;
+    const int bid = blockIdx.x;
+    int qt, bh;
+    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
+      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
+      qt = a.n_qt - 1 - wi / hx;
+      bh = x * hx + wi % hx;
+    } else {
+      qt = a.n_qt - 1 - bid / nbh;
+      bh = bid % nbh;
+    }
+    b = bh / a.H;
+    h = bh % a.H;
+    q0 = qt * kQT;
+    sq_len = a.Sq;
+    sk_len = a.Sk;
+  } else {
+    if ((int)blockIdx.x >= a.sched[0]) return;
+    seq = a.sched[1 + 2 * blockIdx.x];
+    q0 = a.sched[2 + 2 * blockIdx.x];
+    h = blockIdx.y;
+    if (seq < 0) {  // packed padding rows: out 0, lse -inf
+      const int r0 = q0 + w * 32 + n;
+      if (r0 < a.Sq) {
+        uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
+        for (int d = g * 64; d < g * 64 + 64; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
+        if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
+      }
+      return;
+    }
+    qtok0 = a.cu_q[seq];
+    sq_len = a.cu_q[seq + 1] - qtok0;
+    if constexpr (MODE == FW_KV_VARLEN) {
+      kbase = a.cu_k[seq];
+      sk_len = a.cu_k[seq + 1] - kbase;
+    } else {
+      sk_len = a.seqused_k[seq];
+    }
+  }
+  const int hk = h / a.G;
+  const int off = sk_len - sq_len;  // bottom-right alignment
+  auto row_hi = [&](int r) {
+    const int p = r + off;
+    return a.wr >= 0 ? min(sk_len, p + a.wr + 1) : sk_len;
+  };
+  auto row_lo = [&](int r) {
+    const int p = r + off;
+    return a.wl >= 0 ? max(0, p - a.wl) : 0;
+  };
+  const int last_row = min(q0 + kQT, sq_len) - 1;
+  const int wg_lo = row_lo(q0);
+  const int wg_hi = row_hi(last_row);
+  const int w_first = q0 + 32 * w;
+  const int w_last = min(w_first + 31, sq_len - 1);
+  const bool w_any = w_first <= w_last;
+  const int w_lo = w_any ? row_lo(w_first) : 0;
+  const int w_hi = w_any ? row_hi(w_last) : 0;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < sq_len;
+  const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
+
+  // ------------------------------------------------------------ Q^T operand
+  bf16x8_t qop[8];
+  {
+    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
+                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
+    u32x4_t raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
+      qop[j] = __builtin_bit_cast(bf16x8_t, o);
+    }
+  }
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
+  const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
+
+  // ---- global -> LDS: wave w fills rows 16w .. 16w+15 of the K and V tiles,
+  // four rows (1 KiB) per instruction; lane l takes row 16w + 4i + l/16,
+  // logical chunk (l % 16) ^ (row & 15).
+  const int ld_chunk = lane & 15;
+  const int ld_row0 = 16 * w + (lane >> 4);
+  auto issue_tile = [&](int t, FW_LDS uint8_t *kdst, FW_LDS uint8_t *vdst) {
+    const int kb = t * kKT;
+    const int kmax = sk_len - 1;
+    if constexpr (MODE == FW_KV_PAGED) {
+      // rows 16w .. 16w+15 sit in one page (page_size % 16 == 0)
+      const int key0 = min(kb + 16 * w, kmax) & ~15;
+      int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
+      page = min(max(page, 0), a.num_pages - 1);
+      const uint8_t *prow = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
+      const size_t rstride = (size_t)a.CH * 256;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = ld_row0 + 4 * i;
+        const int kr = min(kb + r, kmax) - key0;  // row inside the page run
+        const uint8_t *src = prow + (size_t)kr * rstride + 16 * (ld_chunk ^ (r & 15));
+        lds_dma16(src, kdst + (16 * w + 4 * i) * kRowB);
+        lds_dma16(src + 256, vdst + (16 * w + 4 * i) * kRowB);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = ld_row0 + 4 * i;
+        const size_t key = (size_t)(kbase + min(kb + r, kmax));
+        const size_t c16 = 16 * (ld_chunk ^ (r & 15));
+        lds_dma16(a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + key * a.kst) + c16,
+                  kdst + (16 * w + 4 * i) * kRowB);
+        lds_dma16(a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + key * a.vst) + c16,
+                  vdst + (16 * w + 4 * i) * kRowB);
+      }
+    }
+  };
+
+  // ---- LDS operand addressing.  Every read is a per-lane base plus a
+  // compile-time offset (buffer, sub-tile, k-step), so no address is
+  // recomputed or kept per read.
+  // K (A of S^T): row r = 32st + n, physical chunk (2j+g) ^ (r & 15); the XOR
+  // term depends only on the lane, so one base per step j.
+  const FW_LDS uint8_t *lds_base = (const FW_LDS uint8_t *)lds;
+  const FW_LDS uint8_t *kaddr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kaddr[j] = lds_base + n * kRowB + 16 * ((2 * j + g) ^ (n & 15));
+  // V (A of O^T, ds_read_b64_tr_b16): 16-lane group G covers dims
+  // 32c + 16(G&1) .. +15 for keys 16u + 8hh + 4(G>>1) + a (lane 4a+b points at
+  // dims +4b..+4b+3).  With kg = G>>1 and lo = 2(G&1) + (b>>1) the physical
+  // chunk is 4*(c ^ 2hh ^ kg) + (lo ^ a); c ^ 2hh is a constant c', and
+  // c' ^ kg = c' + (c' even ? kg : -kg), hence two bases.
+  const int tr_i = lane & 15, tr_G = lane >> 4;
+  const int tr_a = tr_i >> 2, tr_b = tr_i & 3, tr_kg = tr_G >> 1;
+  const int tr_lo = 2 * (tr_G & 1) + (tr_b >> 1);
+  const FW_LDS uint8_t *vrow = lds_base + kTileB + (4 * tr_kg + tr_a) * kRowB + 16 * (tr_lo ^ tr_a) + 8 * (tr_b & 1);
+  const FW_LDS uint8_t *vaddr_even = vrow + 64 * tr_kg;
+  const FW_LDS uint8_t *vaddr_odd = vrow - 64 * tr_kg;
+
+  auto compute_tile = [&](int t, int bufoff) {
+    const int kb = t * kKT;
+    // ---------------- S^T = K Q^T : two 32-key sub-tiles
+    f32x16_t sacc[2];
+    {
+      bf16x8_t kop[2][8];
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(kaddr[j] + bufoff + st * 32 * kRowB));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sacc[st] = mfma32(kop[st][j], qop[j], sacc[st]);
+      }
+    }
+    // ---------------- online softmax (log2 units), lane = query row n
+    if (a.softcap_log2 != 0.f) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
+    }
+    const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
+                      kb + kKT <= sk_len;
+    if (!full) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
+        }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
+    tmax = wave_max_xor(tmax, 32);
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8_t pop[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      u32x4_t pw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e] - m_use);
+        const float p1 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e + 1] - m_use);
+        psum += p0 + p1;
+        pw[e] = pack_bf16(p0, p1);
+      }
+      pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+    }
+    l_run = l_run * alpha + psum;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+    }
+    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
+    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x2_t part[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int cp = c ^ (2 * hh);
+          const FW_LDS uint8_t *src = ((cp & 1) ? vaddr_odd : vaddr_even) + bufoff + 64 * cp +
+                                      (16 * u + 8 * hh) * kRowB;
+          part[hh] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)src));
+        }
+        dst[c] = __builtin_bit_cast(bf16x8_t, u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]});
+      }
+    };
+    bf16x8_t vop[2][4];
+    read_v(0, vop[0]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
+    }
+  };
+  auto wave_needs = [&](int t) {
+    const int kb = t * kKT;
+    return w_any && kb < w_hi && kb + kKT > w_lo;
+  };
+
+  // ---- main loop: tile t computes from one buffer while tile t+1 streams
+  // into the other; one barrier per tile.
+  FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds, *vd0 = kd0 + kTileB;
+  FW_LDS uint8_t *kd1 = kd0 + 2 * kTileB, *vd1 = kd1 + kTileB;
+  if (t_begin < t_end) {
+    issue_tile(t_begin, kd0, vd0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  for (int t = t_begin; t < t_end; t += 2) {
+    if (t + 1 < t_end) issue_tile(t + 1, kd1, vd1);
+    if (wave_needs(t)) compute_tile(t, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 >= t_end) break;
+    if (t + 2 < t_end) issue_tile(t + 2, kd0, vd0);
+    if (wave_needs(t + 1)) compute_tile(t + 1, 2 * kTileB);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // ------------------------------------------------------------ epilogue
+  l_run += __shfl_xor(l_run, 32, 64);
+  float M = m_run, Lsum = l_run, oscale = 1.f;
+  if (a.sinks) {
+    const float sk = a.sinks[h] * kLog2e;
+    if (sk != -INFINITY) {
+      const float Mn = fmaxf(M, sk);
+      const float c_old = fast_exp2(M - Mn);
+      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
+      oscale = c_old;
+      M = Mn;
+    }
+  }
+  if (!row_ok) return;
+  const bool any = Lsum > 0.f && l_run > 0.f;
+  const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
+  uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
+                          pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
+      *(u32x2_t *)(op + 32 * c + 8 * rr + 4 * g) = wv;
+    }
+  if (a.lse && g == 0) {
+    a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] =
+        Lsum > 0.f ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
   }
 }
 
@@ -397,12 +751,12 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 template <int MODE>
 static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, hipStream_t s) {
   switch (kv_dtype) {
-    case FW_BF16: fw_prefill_kernel<MODE, FW_BF16><<<grid, 256, 0, s>>>(a); break;
+    case FW_BF16: fw_prefill_kernel<MODE><<<grid, 256, 0, s>>>(a); break;
     case FW_FP8_E4M3:
-      if constexpr (MODE == FW_KV_PAGED) fw_prefill_kernel<MODE, FW_FP8_E4M3><<<grid, 256, 0, s>>>(a);
+      if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E4M3><<<grid, 256, 0, s>>>(a);
       break;
     default:
-      if constexpr (MODE == FW_KV_PAGED) fw_prefill_kernel<MODE, FW_FP8_E5M2><<<grid, 256, 0, s>>>(a);
+      if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E5M2><<<grid, 256, 0, s>>>(a);
       break;
   }
 }
