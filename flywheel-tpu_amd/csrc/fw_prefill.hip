@@ -372,6 +372,11 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
 //     (lane % 16) of keys K0..K0+3: the transposed operand without any
 //     transposing store.
 constexpr int kRowB = 256;                 // LDS bytes of one key row
+constexpr float kAnchorGuard = 8.f;        // log2 units (a factor of 256)
+// 16-byte chunk swizzle of LDS row r: a bijection on r & 15 (16 consecutive
+// rows spread one logical chunk over all banks) that also gives the four rows
+// of an aligned key quad disjoint chunk pairs (ds_read_b64_tr_b16 groups).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 constexpr int kTileB = kKT * kRowB;        // 16 KiB per K or V tile
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
@@ -383,8 +388,10 @@ __device__ __forceinline__ void lds_dma16(const void *src, FW_LDS uint8_t *dst) 
 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
-  // two buffers of [K tile | V tile]
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kTileB];
+  // Two buffers of [K tile | V tile], two objects so the compiler can prove a
+  // DMA into one never aliases operand reads from the other.
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[2 * kTileB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[2 * kTileB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -503,7 +510,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < 4; ++i) {
         const int r = ld_row0 + 4 * i;
         const int kr = min(kb + r, kmax) - key0;  // row inside the page run
-        const uint8_t *src = prow + (size_t)kr * rstride + 16 * (ld_chunk ^ (r & 15));
+        const uint8_t *src = prow + (size_t)kr * rstride + 16 * (ld_chunk ^ swz(r));
         lds_dma16(src, kdst + (16 * w + 4 * i) * kRowB);
         lds_dma16(src + 256, vdst + (16 * w + 4 * i) * kRowB);
       }
@@ -512,7 +519,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < 4; ++i) {
         const int r = ld_row0 + 4 * i;
         const size_t key = (size_t)(kbase + min(kb + r, kmax));
-        const size_t c16 = 16 * (ld_chunk ^ (r & 15));
+        const size_t c16 = 16 * (ld_chunk ^ swz(r));
         lds_dma16(a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + key * a.kst) + c16,
                   kdst + (16 * w + 4 * i) * kRowB);
         lds_dma16(a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + key * a.vst) + c16,
@@ -522,27 +529,30 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   };
 
   // ---- LDS operand addressing.  Every read is a per-lane base plus a
-  // compile-time offset (buffer, sub-tile, k-step), so no address is
-  // recomputed or kept per read.
-  // K (A of S^T): row r = 32st + n, physical chunk (2j+g) ^ (r & 15); the XOR
-  // term depends only on the lane, so one base per step j.
-  const FW_LDS uint8_t *lds_base = (const FW_LDS uint8_t *)lds;
-  const FW_LDS uint8_t *kaddr[8];
+  // compile-time offset (buffer, sub-tile, k-step).
+  // K (A of S^T): row r = 32st + n, physical chunk (2j+g) ^ swz(n): one base
+  // per step j.
+  const int koff[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int kofs[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) kaddr[j] = lds_base + n * kRowB + 16 * ((2 * j + g) ^ (n & 15));
+  for (int j = 0; j < 8; ++j) kofs[j] = koff[j] + n * kRowB + 16 * ((2 * j + g) ^ swz(n));
   // V (A of O^T, ds_read_b64_tr_b16): 16-lane group G covers dims
-  // 32c + 16(G&1) .. +15 for keys 16u + 8hh + 4(G>>1) + a (lane 4a+b points at
-  // dims +4b..+4b+3).  With kg = G>>1 and lo = 2(G&1) + (b>>1) the physical
-  // chunk is 4*(c ^ 2hh ^ kg) + (lo ^ a); c ^ 2hh is a constant c', and
-  // c' ^ kg = c' + (c' even ? kg : -kg), hence two bases.
+  // 32c + 16(G&1) .. +15 for keys 16u + 8hh + 4(G>>1) + a; lane 4a+b points at
+  // dims +4b..+4b+3, i.e. logical chunk 4c + lo, lo = 2(G&1) + (b>>1).  With
+  // key & 15 = 8hh + 4kg + a the physical chunk is
+  // 4(c ^ a) + (lo ^ kg ^ 2hh): one base per (c, hh).
   const int tr_i = lane & 15, tr_G = lane >> 4;
   const int tr_a = tr_i >> 2, tr_b = tr_i & 3, tr_kg = tr_G >> 1;
   const int tr_lo = 2 * (tr_G & 1) + (tr_b >> 1);
-  const FW_LDS uint8_t *vrow = lds_base + kTileB + (4 * tr_kg + tr_a) * kRowB + 16 * (tr_lo ^ tr_a) + 8 * (tr_b & 1);
-  const FW_LDS uint8_t *vaddr_even = vrow + 64 * tr_kg;
-  const FW_LDS uint8_t *vaddr_odd = vrow - 64 * tr_kg;
+  int vofs[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      vofs[c][hh] = kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
+                    16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
-  auto compute_tile = [&](int t, int bufoff) {
+  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf) {
     const int kb = t * kKT;
     // ---------------- S^T = K Q^T : two 32-key sub-tiles
     f32x16_t sacc[2];
@@ -552,8 +562,9 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(kaddr[j] + bufoff + st * 32 * kRowB));
+          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + st * 32 * kRowB));
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
 #pragma unroll
@@ -561,6 +572,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) sacc[st] = mfma32(kop[st][j], qop[j], sacc[st]);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
     // ---------------- online softmax (log2 units), lane = query row n
     if (a.softcap_log2 != 0.f) {
@@ -586,10 +598,16 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
     tmax = wave_max_xor(tmax, 32);
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
+    // Static anchor with a guard: the anchor moves only when a tile's max
+    // exceeds it by more than kAnchorGuard (log2 units), so the O rescale is
+    // rare; exp2 arguments stay <= kAnchorGuard.
+    float alpha = 1.f;
+    if (__any(tmax > m_run + kAnchorGuard)) {
+      const float m_new = fmaxf(m_run, tmax);
+      alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float psum = 0.f;
     bf16x8_t pop[4];
 #pragma unroll
@@ -604,11 +622,12 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       }
       pop[u] = __builtin_bit_cast(bf16x8_t, pw);
     }
-    l_run = l_run * alpha + psum;
     if (__any(alpha != 1.f)) {
+      l_run *= alpha;
 #pragma unroll
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
     }
+    l_run += psum;
     // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
     auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
 #pragma unroll
@@ -616,9 +635,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
         u32x2_t part[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const int cp = c ^ (2 * hh);
-          const FW_LDS uint8_t *src = ((cp & 1) ? vaddr_odd : vaddr_even) + bufoff + 64 * cp +
-                                      (16 * u + 8 * hh) * kRowB;
+          const FW_LDS uint8_t *src = buf + vofs[c][hh] + (16 * u + 8 * hh) * kRowB;
           part[hh] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)src));
         }
         dst[c] = __builtin_bit_cast(bf16x8_t, u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]});
@@ -626,6 +643,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     };
     bf16x8_t vop[2][4];
     read_v(0, vop[0]);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
@@ -633,6 +651,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   auto wave_needs = [&](int t) {
     const int kb = t * kKT;
@@ -641,8 +660,8 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 
   // ---- main loop: tile t computes from one buffer while tile t+1 streams
   // into the other; one barrier per tile.
-  FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds, *vd0 = kd0 + kTileB;
-  FW_LDS uint8_t *kd1 = kd0 + 2 * kTileB, *vd1 = kd1 + kTileB;
+  FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds0, *vd0 = kd0 + kTileB;
+  FW_LDS uint8_t *kd1 = (FW_LDS uint8_t *)lds1, *vd1 = kd1 + kTileB;
   if (t_begin < t_end) {
     issue_tile(t_begin, kd0, vd0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -650,12 +669,12 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   }
   for (int t = t_begin; t < t_end; t += 2) {
     if (t + 1 < t_end) issue_tile(t + 1, kd1, vd1);
-    if (wave_needs(t)) compute_tile(t, 0);
+    if (wave_needs(t)) compute_tile(t, kd0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t + 1 >= t_end) break;
     if (t + 2 < t_end) issue_tile(t + 2, kd0, vd0);
-    if (wave_needs(t + 1)) compute_tile(t + 1, 2 * kTileB);
+    if (wave_needs(t + 1)) compute_tile(t + 1, kd1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
