@@ -43,9 +43,23 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def timed(fn, steps, warmup):
+BURN_IN_S = 1.0
+
+
+def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
     """Mean ms per call of fn over `steps` calls after `warmup`, bracketed by
-    events on the current stream (the stream every kernel is launched on)."""
+    events on the current stream (the stream every kernel is launched on).
+
+    Before the warm-up calls the same step runs untimed for burn_in_s seconds
+    (the reference's protocol runs rounds of at least 0.5 s,
+    benchmarks/common/timing.py:33-35): the GPU's clocks ramp up over the
+    first few hundred milliseconds of load, and timing before that measures
+    the ramp, not the kernel."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < burn_in_s:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()

@@ -552,7 +552,11 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       vofs[c][hh] = kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
                     16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
-  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf) {
+  // Computes tile t from buf; the next tile's DMA (tn >= 0, into kdn / vdn) is
+  // issued between the softmax and the PV phase, where it interferes least
+  // with the operand reads.
+  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf, int tn, FW_LDS uint8_t *kdn,
+                          FW_LDS uint8_t *vdn) {
     const int kb = t * kKT;
     // ---------------- S^T = K Q^T : two 32-key sub-tiles
     f32x16_t sacc[2];
@@ -628,6 +632,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
     }
     l_run += psum;
+    if (tn >= 0) issue_tile(tn, kdn, vdn);
     // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
     auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
 #pragma unroll
@@ -659,24 +664,28 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   };
 
   // ---- main loop: tile t computes from one buffer while tile t+1 streams
-  // into the other; one barrier per tile.
+  // into the other; one barrier per tile.  The barrier needs this wave's DMA
+  // landed (vmcnt) and its operand reads done (lgkmcnt), no memory fence.
+  auto tile_barrier = [&]() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+  auto step = [&](int t, const FW_LDS uint8_t *cur, FW_LDS uint8_t *kn, FW_LDS uint8_t *vn) {
+    const int tn = t + 1 < t_end ? t + 1 : -1;
+    if (wave_needs(t)) compute_tile(t, cur, tn, kn, vn);
+    else if (tn >= 0) issue_tile(tn, kn, vn);
+    tile_barrier();
+  };
   FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds0, *vd0 = kd0 + kTileB;
   FW_LDS uint8_t *kd1 = (FW_LDS uint8_t *)lds1, *vd1 = kd1 + kTileB;
   if (t_begin < t_end) {
     issue_tile(t_begin, kd0, vd0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    tile_barrier();
   }
   for (int t = t_begin; t < t_end; t += 2) {
-    if (t + 1 < t_end) issue_tile(t + 1, kd1, vd1);
-    if (wave_needs(t)) compute_tile(t, kd0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    step(t, kd0, kd1, vd1);
     if (t + 1 >= t_end) break;
-    if (t + 2 < t_end) issue_tile(t + 2, kd0, vd0);
-    if (wave_needs(t + 1)) compute_tile(t + 1, kd1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    step(t + 1, kd1, kd0, vd0);
   }
 
   // ------------------------------------------------------------ epilogue
