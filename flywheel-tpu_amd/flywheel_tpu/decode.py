@@ -264,6 +264,12 @@ def flash_attn_with_kvcache(
             f"k and v must be {expected_new_shape} (matching q's token layout); got"
             f" {tuple(k.shape)=}, {tuple(v.shape)=}."
         )
+    if not isinstance(cache_seqlens, int):
+        cs_shape = tuple(as_tensor(cache_seqlens).shape)
+        if cs_shape not in ((), (batch,)):
+            raise ValueError(
+                f"cache_seqlens must be a scalar or ({batch},) int array; got {cs_shape}."
+            )
     device = q.device
     N.require_device(q, k_cache, k, v)
     if isinstance(cache_seqlens, int):

@@ -1,0 +1,187 @@
+"""Host-side checks that need no GPU: the C-ABI library exports what
+include/flywheel_hip.h declares, its argument validation returns the
+documented status codes, and the Python API raises the reference's exception
+types (flywheel_tpu/softmax_attention/inputs.py:218-251, decode.py:286-435,
+prefill.py:437-963) before anything is launched."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import flywheel_tpu
+from flywheel_tpu import _native as N
+from flywheel_tpu import (flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache,
+                          write_kv_cache_pages)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flywheel_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fw_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    names = declared_functions()
+    assert len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), f"{name} is declared but not exported"
+    assert set(names) == set(N.SIGNATURES), "ctypes bindings and header disagree"
+    assert lib.fw_abi_version() == 1
+
+
+def test_struct_layouts_match_header_fields():
+    text = open(HEADER).read()
+    for struct, cls in (("fw_decode_params", N.DecodeParams), ("fw_prefill_params", N.PrefillParams)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        fields = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            names = decl.split()[-1] if "," not in decl else decl
+            for part in re.split(r",", decl):
+                m = re.search(r"\**([A-Za-z_0-9]+)\s*$", part.strip())
+                fields.append(m.group(1))
+        assert fields == [f[0] for f in cls._fields_], struct
+
+
+def test_capi_validation_status_codes():
+    lib = N.lib()
+    p = N.DecodeParams()
+    p.batch, p.seqlen_q, p.nheads, p.nheads_k, p.head_dim = 2, 1, 8, 2, 64
+    p.page_size, p.max_pages, p.num_pages = 16, 4, 8
+    assert lib.fw_paged_decode_workspace_bytes(p) == 0
+    assert lib.fw_paged_decode(p, None) == N.FW_ERR_NOT_IMPLEMENTED
+    assert b"head_dim" in lib.fw_last_error()
+    p.head_dim, p.page_size = 128, 24
+    assert lib.fw_paged_decode(p, None) == N.FW_ERR_VALUE
+    p.page_size, p.nheads = 16, 7
+    assert lib.fw_paged_decode(p, None) == N.FW_ERR_VALUE
+    p.nheads = 8
+    assert lib.fw_paged_decode_workspace_bytes(p) > 0
+    assert lib.fw_paged_decode(p, None) == N.FW_ERR_VALUE  # no workspace
+    q = N.PrefillParams()
+    q.kv_mode, q.head_dim, q.nheads, q.nheads_k = N.FW_KV_DENSE, 96, 4, 2
+    assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
+    q.head_dim, q.kv_dtype = 128, N.FW_FP8_E4M3
+    assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED  # fp8 only for a paged pool
+    assert lib.fw_append_ragged(None, None, None, None, None, None, None, 1, 0, 2, 128, 16, 1, 1,
+                                7, None) == N.FW_ERR_NOT_IMPLEMENTED
+
+
+def bf(*shape):
+    return torch.zeros(shape, dtype=torch.bfloat16)
+
+
+def test_flash_attn_func_errors():
+    q, k = bf(1, 4, 8, 128), bf(1, 2, 8, 128)
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q, k, k, dropout_p=0.1)
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q, k, k, alibi_slopes=torch.zeros(4))
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q, k, k, deterministic=True)
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q, k, k, return_attn_probs=True)
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q, k, k, attention_chunk=64)
+    with pytest.raises(ValueError):
+        flash_attn_func(q, k, k, window_size=(-2, 0))
+    with pytest.raises(ValueError):
+        flash_attn_func(q, k, k, softcap=-1.0)
+    with pytest.raises(ValueError):
+        flash_attn_func(q, bf(1, 3, 8, 128), bf(1, 3, 8, 128))
+    with pytest.raises(NotImplementedError):
+        flash_attn_func(q.float(), k.float(), k.float())
+    with pytest.raises(ValueError):
+        flash_attn_func(bf(1, 8, 512), bf(1, 8, 256), bf(1, 8, 256), token_major=True)
+    with pytest.raises(TypeError):
+        flash_attn_func(q, k, k, heads_outer_fold=1)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_func(q, k, k, causal=True)
+
+
+def test_flash_attn_varlen_func_errors():
+    q, k = bf(4, 10, 128), bf(2, 10, 128)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    with pytest.raises(ValueError):
+        flash_attn_varlen_func(q, k, k, cu, cu[:2], 6, 6)
+    with pytest.raises(ValueError):
+        flash_attn_varlen_func(q, k, k, cu, cu, 0, 6)
+    with pytest.raises(ValueError):
+        flash_attn_varlen_func(q, k, k, cu, cu, 6, 6, seqused_k=torch.tensor([4, 6]))
+    with pytest.raises(ValueError):
+        flash_attn_varlen_func(q, k, k, cu, cu, 6, 6, block_sizes=(100, 128, 1, 1))
+    pool = bf(8, 16, 4, 128)
+    table = torch.zeros(2, 4, dtype=torch.int32)
+    with pytest.raises(ValueError):  # v must be None with a block table
+        flash_attn_varlen_func(q, pool, pool, cu, None, 6, 64, block_table=table,
+                               seqused_k=torch.tensor([4, 6]))
+    with pytest.raises(ValueError):  # seqused_k required
+        flash_attn_varlen_func(q, pool, None, cu, None, 6, 64, block_table=table)
+    with pytest.raises(NotImplementedError):  # window right bound must be -1 or 0
+        flash_attn_varlen_func(q, pool, None, cu, None, 6, 64, block_table=table,
+                               seqused_k=torch.tensor([4, 6]), window_size=(-1, 3))
+    with pytest.raises(ValueError):
+        flash_attn_varlen_func(q, pool, None, cu, None, 6, 64, block_table=table,
+                               seqused_k=torch.tensor([4, 6]), num_active=3)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_varlen_func(q, pool, None, cu, None, 6, 64, block_table=table,
+                               seqused_k=torch.tensor([4, 6]))
+
+
+def test_flash_attn_with_kvcache_errors():
+    pool = bf(8, 16, 4, 128)
+    table = torch.zeros(2, 4, dtype=torch.int32)
+    q = bf(2, 1, 4, 128)
+    kw = dict(cache_seqlens=torch.tensor([3, 5], dtype=torch.int32), block_table=table)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, pool, pool, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, pool, None, cache_batch_idx=torch.tensor([0, 1]), **kw)
+    with pytest.raises(ValueError):  # page size not a multiple of 16
+        flash_attn_with_kvcache(q, bf(8, 24, 4, 128), None, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, pool, None, max_seqlen_q=1, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(bf(5, 4, 128), pool, None, cu_seqlens_q=torch.tensor([0, 2, 5]),
+                                **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, pool, None, bf(2, 1, 2, 128), None, **kw)
+    with pytest.raises(NotImplementedError):
+        flash_attn_with_kvcache(q.float(), pool, None, **kw)
+    with pytest.raises(NotImplementedError):  # multi-token call needs the paged cache
+        flash_attn_with_kvcache(bf(2, 3, 4, 128), bf(2, 64, 2, 128), bf(2, 64, 2, 128),
+                                cache_seqlens=3)
+    with pytest.raises(ValueError):  # an fp8 pool needs nheads_k
+        flash_attn_with_kvcache(q, pool.to(torch.float8_e4m3fn), None, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, pool, None, cache_seqlens=torch.tensor([1, 2, 3]),
+                                block_table=table)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_with_kvcache(q, pool, None, **kw)
+
+
+def test_write_kv_cache_pages_errors():
+    cache = bf(6, 128, 4, 128)
+    k = bf(10, 2, 128)
+    slices = torch.zeros(3, 4, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        write_kv_cache_pages(bf(10, 3, 128), bf(10, 3, 128), cache, slices, torch.tensor([1]))
+    with pytest.raises(NotImplementedError):
+        write_kv_cache_pages(k.float(), k.float(), cache, slices, torch.tensor([1]))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        write_kv_cache_pages(k, k, cache, slices, torch.tensor([1]))
+
+
+def test_package_surface():
+    assert set(flywheel_tpu.__all__) >= {"flash_attn_func", "flash_attn_varlen_func",
+                                         "flash_attn_with_kvcache"}
