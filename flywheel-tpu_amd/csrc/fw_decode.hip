@@ -368,17 +368,21 @@ struct CombineArgs {
   float v_descale;
 };
 
-// One block per (b, kv head, q tile).  For each row of the tile, thread t
-// reads the partials of splits s = t/16, t/16 + 16, ... (dims 8*(t%16)..+7),
-// all in parallel, and the 16 split groups merge through LDS.
+// One block per (b, kv head, q tile, group of 4 rows): thread t merges row
+// 4*blockIdx.x + t/64 over splits s = (t/16)%4, +4, ... for dims
+// 8*(t%16)..+7; the 4 split groups then merge through LDS.
 __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
-  __shared__ float s_acc[16][16][8];
-  __shared__ float2 s_ml[16][16];
+  __shared__ float s_acc[4][4][16][8];
+  __shared__ float2 s_ml[4][4];
   const int part = threadIdx.x & 15;
-  const int grp = threadIdx.x >> 4;
+  const int grp = (threadIdx.x >> 4) & 3;
+  const int rl = threadIdx.x >> 6;
   const int h = blockIdx.y / a.n_qtiles;
   const int qt = blockIdx.y % a.n_qtiles;
   const int b = blockIdx.z;
+  const int row = 4 * blockIdx.x + rl;  // row inside the q tile
+  const int r = qt * 16 + row;
+  const bool valid = row < 16 && r < a.Rq;
   const bool active = !(a.num_active && b >= *a.num_active);
   int nsp = 0;
   if (active) {
@@ -389,11 +393,11 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
     nsp = total > base ? (total - base + a.split_keys - 1) / a.split_keys : 0;
   }
   const size_t item0 = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit;
-  const int rows = min(16, a.Rq - qt * 16);
-  for (int row = 0; row < rows; ++row) {
-    float M = -INFINITY, Lsum = 0.f;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int s = grp; s < nsp; s += 16) {
+  float M = -INFINITY, Lsum = 0.f;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (valid) {
+#pragma unroll 2
+    for (int s = grp; s < nsp; s += 4) {
       const float2 ml = a.ws_ml[(item0 + s) * 16 + row];
       const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
       const f32x4_t v0 = *(const f32x4_t *)po, v1 = *(const f32x4_t *)(po + 4);
@@ -408,50 +412,49 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
       Lsum = Lsum * c_old + ml.y * c_new;
       M = Mn;
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s_acc[grp][part][e] = acc[e];
-    if (part == 0) s_ml[grp][0] = make_float2(M, Lsum);
-    __syncthreads();
-    if (grp == 0) {
-      float Mt = -INFINITY;
-      for (int g2 = 0; g2 < 16; ++g2) Mt = fmaxf(Mt, s_ml[g2][0].x);
-      const int r = qt * 16 + row;
-      const int tok = r / a.G, hq = h * a.G + r % a.G;
-      float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      float Lt = 0.f;
-      if (Mt != -INFINITY) {
-        for (int g2 = 0; g2 < 16; ++g2) {
-          const float2 ml = s_ml[g2][0];
-          if (ml.x == -INFINITY) continue;
-          const float c = fast_exp2(ml.x - Mt);
-          Lt += ml.y * c;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] += s_acc[g2][part][e] * c;
-        }
-      }
-      if (a.sinks) {
-        const float sk = a.sinks[hq] * kLog2e;
-        if (sk != -INFINITY) {
-          const float Mn = fmaxf(Mt, sk);
-          const float c_old = fast_exp2(Mt - Mn);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] *= c_old;
-          Lt = Lt * c_old + fast_exp2(sk - Mn);
-          Mt = Mn;
-        }
-      }
-      const bool any = active && Lt > 0.f;
-      const float scale = any ? a.v_descale / Lt : 0.f;
-      uint16_t *op = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
-      u32x4_t w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = pack_bf16(o[2 * e] * scale, o[2 * e + 1] * scale);
-      *(u32x4_t *)op = w;
-      if (a.lse && part == 0)
-        a.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
-    }
-    __syncthreads();
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_acc[rl][grp][part][e] = acc[e];
+  if (part == 0) s_ml[rl][grp] = make_float2(M, Lsum);
+  __syncthreads();
+  if (!valid || grp != 0) return;
+  float Mt = -INFINITY;
+#pragma unroll
+  for (int g2 = 0; g2 < 4; ++g2) Mt = fmaxf(Mt, s_ml[rl][g2].x);
+  const int tok = r / a.G, hq = h * a.G + r % a.G;
+  float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float Lt = 0.f;
+  if (Mt != -INFINITY) {
+#pragma unroll
+    for (int g2 = 0; g2 < 4; ++g2) {
+      const float2 ml = s_ml[rl][g2];
+      if (ml.x == -INFINITY) continue;
+      const float c = fast_exp2(ml.x - Mt);
+      Lt += ml.y * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += s_acc[rl][g2][part][e] * c;
+    }
+  }
+  if (a.sinks) {
+    const float sk = a.sinks[hq] * kLog2e;
+    if (sk != -INFINITY) {
+      const float Mn = fmaxf(Mt, sk);
+      const float c_old = fast_exp2(Mt - Mn);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= c_old;
+      Lt = Lt * c_old + fast_exp2(sk - Mn);
+      Mt = Mn;
+    }
+  }
+  const bool any = active && Lt > 0.f;
+  const float scale = any ? a.v_descale / Lt : 0.f;
+  uint16_t *op = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
+  u32x4_t w;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = pack_bf16(o[2 * e] * scale, o[2 * e + 1] * scale);
+  *(u32x4_t *)op = w;
+  if (a.lse && part == 0)
+    a.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
 }
 
 // Keys per split-K work item: about 32K items at full capacity, at least 256
@@ -594,6 +597,7 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   c.seqlen_add = a.seqlen_add;
   c.window_left = p->window_left;
   c.v_descale = p->v_descale;
-  fw_decode_combine<<<dim3(1, p->nheads_k * L.n_qtiles, p->batch), 256, 0, s>>>(c);
+  const int row_groups = (std::min(L.Rq, 16) + 3) / 4;
+  fw_decode_combine<<<dim3(row_groups, p->nheads_k * L.n_qtiles, p->batch), 256, 0, s>>>(c);
   return check_launch("fw_decode_combine");
 }
