@@ -496,11 +496,15 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   // logical chunk (l % 16) ^ (row & 15).
   const int ld_chunk = lane & 15;
   const int ld_row0 = 16 * w + (lane >> 4);
-  auto issue_tile = [&](int t, FW_LDS uint8_t *kdst, FW_LDS uint8_t *vdst) {
+  // global -> registers (asynchronous loads, they never block issue); the
+  // chunks land in LDS later through store_tile with conflict-free
+  // ds_write_b128.  (global_load_lds stalls the issuing wave on this GPU:
+  // measured ~1/3 of a tile's time.)
+  u32x4_t stg[8];
+  auto fetch_tile = [&](int t) {
     const int kb = t * kKT;
     const int kmax = sk_len - 1;
     if constexpr (MODE == FW_KV_PAGED) {
-      // rows 16w .. 16w+15 sit in one page (page_size % 16 == 0)
       const int key0 = min(kb + 16 * w, kmax) & ~15;
       int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
       page = min(max(page, 0), a.num_pages - 1);
@@ -509,10 +513,10 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = ld_row0 + 4 * i;
-        const int kr = min(kb + r, kmax) - key0;  // row inside the page run
+        const int kr = min(kb + r, kmax) - key0;
         const uint8_t *src = prow + (size_t)kr * rstride + 16 * (ld_chunk ^ swz(r));
-        lds_dma16(src, kdst + (16 * w + 4 * i) * kRowB);
-        lds_dma16(src + 256, vdst + (16 * w + 4 * i) * kRowB);
+        stg[i] = *(const u32x4_t *)src;
+        stg[4 + i] = *(const u32x4_t *)(src + 256);
       }
     } else {
 #pragma unroll
@@ -520,11 +524,17 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
         const int r = ld_row0 + 4 * i;
         const size_t key = (size_t)(kbase + min(kb + r, kmax));
         const size_t c16 = 16 * (ld_chunk ^ swz(r));
-        lds_dma16(a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + key * a.kst) + c16,
-                  kdst + (16 * w + 4 * i) * kRowB);
-        lds_dma16(a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + key * a.vst) + c16,
-                  vdst + (16 * w + 4 * i) * kRowB);
+        stg[i] = *(const u32x4_t *)(a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + key * a.kst) + c16);
+        stg[4 + i] = *(const u32x4_t *)(a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + key * a.vst) + c16);
       }
+    }
+  };
+  auto store_tile = [&](FW_LDS uint8_t *kdst, FW_LDS uint8_t *vdst) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = (16 * w + 4 * i) * kRowB + 16 * lane;
+      *(FW_LDS u32x4_t *)(kdst + off) = stg[i];
+      *(FW_LDS u32x4_t *)(vdst + off) = stg[4 + i];
     }
   };
 
@@ -552,32 +562,31 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       vofs[c][hh] = kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
                     16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
-  // Computes tile t from buf; the next tile's DMA (tn >= 0, into kdn / vdn) is
-  // issued between the softmax and the PV phase, where it interferes least
-  // with the operand reads.
-  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf, int tn, FW_LDS uint8_t *kdn,
-                          FW_LDS uint8_t *vdn) {
+  // Computes tile t from buf; the next tile's loads (tn >= 0) are issued once
+  // the QK MFMAs are in flight.
+  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf, int tn) {
     const int kb = t * kKT;
-    // ---------------- S^T = K Q^T : two 32-key sub-tiles
+    // ---------------- S^T = K Q^T : two 32-key sub-tiles; sub-tile 1's K
+    // operands are read while sub-tile 0's MFMAs run.
     f32x16_t sacc[2];
     {
-      bf16x8_t kop[2][8];
+      bf16x8_t kop0[8], kop1[8];
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int j = 0; j < 8; ++j)
+        kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + st * 32 * kRowB));
-      __builtin_amdgcn_sched_barrier(0);
+      for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sacc[st] = mfma32(kop[st][j], qop[j], sacc[st]);
+      for (int j = 0; j < 8; ++j) {
+        kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
+        sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
       __builtin_amdgcn_s_setprio(0);
     }
+    if (tn >= 0) fetch_tile(tn);
     // ---------------- online softmax (log2 units), lane = query row n
     if (a.softcap_log2 != 0.f) {
 #pragma unroll
@@ -632,7 +641,6 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
     }
     l_run += psum;
-    if (tn >= 0) issue_tile(tn, kdn, vdn);
     // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
     auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
 #pragma unroll
@@ -663,23 +671,25 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     return w_any && kb < w_hi && kb + kKT > w_lo;
   };
 
-  // ---- main loop: tile t computes from one buffer while tile t+1 streams
-  // into the other; one barrier per tile.  The barrier needs this wave's DMA
-  // landed (vmcnt) and its operand reads done (lgkmcnt), no memory fence.
+  // ---- main loop: tile t computes from one buffer while tile t+1 is fetched
+  // and then stored into the other; one barrier per tile (this wave's LDS
+  // stores and operand reads done, no memory fence).
   auto tile_barrier = [&]() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
   };
   auto step = [&](int t, const FW_LDS uint8_t *cur, FW_LDS uint8_t *kn, FW_LDS uint8_t *vn) {
     const int tn = t + 1 < t_end ? t + 1 : -1;
-    if (wave_needs(t)) compute_tile(t, cur, tn, kn, vn);
-    else if (tn >= 0) issue_tile(tn, kn, vn);
+    if (wave_needs(t)) compute_tile(t, cur, tn);
+    else if (tn >= 0) fetch_tile(tn);
+    if (tn >= 0) store_tile(kn, vn);
     tile_barrier();
   };
   FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds0, *vd0 = kd0 + kTileB;
   FW_LDS uint8_t *kd1 = (FW_LDS uint8_t *)lds1, *vd1 = kd1 + kTileB;
   if (t_begin < t_end) {
-    issue_tile(t_begin, kd0, vd0);
+    fetch_tile(t_begin);
+    store_tile(kd0, vd0);
     tile_barrier();
   }
   for (int t = t_begin; t < t_end; t += 2) {
