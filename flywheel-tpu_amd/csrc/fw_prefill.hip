@@ -8,18 +8,17 @@
 // fwd_blocks.qk / online_softmax / pv (fwd_blocks.py:812-942), and the
 // schedule tables of schedule.py:617-717.
 //
-// Workgroup = 4 waves = one 128-row q tile of one query head; wave w owns rows
-// [32w, 32w+32).  KV tiles of 64 keys are staged through LDS:
-//   Ks  [64 keys][136 bf16]  row-major (row pad keeps ds_read_b128 conflict-free)
-//   Vt  [128 dims][68 bf16]  transposed, keys in pairs (so the PV operand of a
-//                            lane is two ds_read_b64 with no repacking)
-// Per wave and KV tile:
-//   S^T (32 keys x 32 rows) = K (A, ds_read_b128) x Q^T (B, registers)   x2
-//   online softmax in log2 units, each lane owning one query row
-//   O^T (32 dims x 32 rows) += V^T (A, Vt) x P^T (B, the S^T registers)  x4
-// with v_mfma_f32_32x32x16_bf16.  The next tile's global loads are issued
-// before the current tile's math.
+// Three forward kernels share one argument block and the q-tile schedule:
+//   fw_prefill_pp_kernel     bf16 K/V, no softcap: 8 waves, ping-pong schedule
+//   fw_prefill_kernel        bf16 K/V with softcap: 4 waves, two per CU
+//   fw_prefill_staged_kernel fp8 paged pools: K/V widened to bf16 in registers
+// In all of them a wave owns 32 query rows, each lane one row, and computes
+//   S^T (32 keys x 32 rows) = K x Q^T        (Q^T resident in registers)
+//   online softmax in log2 units
+//   O^T (32 dims x 32 rows) += V^T x P^T     (P^T = the S^T registers, bf16)
+// with v_mfma_f32_32x32x16_bf16 over 64-key tiles staged through LDS.
 #include "fw_common.h"
+#include <type_traits>
 
 namespace fw {
 
@@ -84,6 +83,12 @@ struct KvAddr {
   }
 };
 
+// fp8 (and generic) K/V: 4 waves = 128 rows; K/V rows are widened to bf16 in
+// registers and staged as
+//   Ks  [64 keys][136 bf16]  row-major (row pad keeps ds_read_b128 conflict-free)
+//   Vt  [128 dims][68 bf16]  transposed, keys in pairs (so the PV operand of a
+//                            lane is two ds_read_b64 with no repacking)
+// with the next tile's global loads issued before the current tile's math.
 template <int MODE, int KV>
 __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kKsBytes + kVtBytes];
@@ -362,17 +367,16 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
 }
 
 // ---------------------------------------------------------------------------
-// bf16 K/V: tiles go global -> LDS directly (global_load_lds_dwordx4, no
-// staging registers), double-buffered with one barrier per tile.  LDS rows are
-// 256 B (one key's 128 dims) with the 16-byte chunk index XOR-swizzled by
-// (key & 15), which keeps both operand reads bank-conflict-free:
+// bf16 K/V layout in LDS, shared by the bf16 kernels: rows are 256 B (one
+// key's 128 dims) with the 16-byte chunk index XOR-swizzled by swz(key & 15),
+// which keeps both operand reads bank-conflict-free:
 //   K operand (A of S^T = K Q^T): ds_read_b128 of row (32st + m), chunk 2j+g
 //   V operand (A of O^T = V^T P^T): ds_read_b64_tr_b16 -- within each 16-lane
 //     group, lane 4a+b points at key K0+a, dims 4b..4b+3, and receives dim
 //     (lane % 16) of keys K0..K0+3: the transposed operand without any
 //     transposing store.
 constexpr int kRowB = 256;                 // LDS bytes of one key row
-constexpr float kAnchorGuard = 8.f;        // log2 units (a factor of 256)
+constexpr float kPsumTrigger = 65536.f;    // lane row-sum bound of the fast path
 // 16-byte chunk swizzle of LDS row r: a bijection on r & 15 (16 consecutive
 // rows spread one logical chunk over all banks) that also gives the four rows
 // of an aligned key quad disjoint chunk pairs (ds_read_b64_tr_b16 groups).
@@ -382,14 +386,13 @@ constexpr int kTileB = kKT * kRowB;        // 16 KiB per K or V tile
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define FW_LDS __attribute__((address_space(3)))
 
-__device__ __forceinline__ void lds_dma16(const void *src, FW_LDS uint8_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, (FW_LDS void *)dst, 16, 0, 0);
-}
-
+// bf16 K/V with softcap: 4 waves = 128 rows, two workgroups per CU, two LDS
+// buffers (tile t computes from one while tile t+1 is fetched into registers
+// and stored into the other), one barrier per tile.
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   // Two buffers of [K tile | V tile], two objects so the compiler can prove a
-  // DMA into one never aliases operand reads from the other.
+  // store into one never aliases operand reads from the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds0[2 * kTileB];
   __shared__ __attribute__((aligned(1024))) uint8_t lds1[2 * kTileB];
 
@@ -492,41 +495,50 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
 
   // ---- global -> LDS: wave w fills rows 16w .. 16w+15 of the K and V tiles,
-  // four rows (1 KiB) per instruction; lane l takes row 16w + 4i + l/16,
-  // logical chunk (l % 16) ^ (row & 15).
-  const int ld_chunk = lane & 15;
-  const int ld_row0 = 16 * w + (lane >> 4);
+  // four rows (1 KiB) per instruction; lane l takes local row l/16 + 4i
+  // (LDS row 16w + 4i + l/16) and physical chunk l % 16, which holds logical
+  // chunk (l % 16) ^ swz(row) = (l % 16) ^ 4(l/16) ^ i.
+  // The row group's base address is wave-uniform (scalar registers); lanes add
+  // a 32-bit offset min(local row, last valid row) * row stride + chunk, so the
+  // clamp at the end of the sequence costs one v_min per row.
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint32_t lr0 = lane >> 4;
+  const uint32_t c16b = 16u * ((lane & 15) ^ (lr0 << 2));
+  uint32_t kstB, vstB;
+  const uint8_t *kbase_p = nullptr, *vbase_p = nullptr;
+  if constexpr (MODE == FW_KV_PAGED) {
+    kstB = vstB = (uint32_t)a.CH * 256u;
+  } else {
+    kstB = 2u * (uint32_t)a.kst;
+    vstB = 2u * (uint32_t)a.vst;
+    kbase_p = a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kbase * a.kst);
+    vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
+  }
   // global -> registers (asynchronous loads, they never block issue); the
   // chunks land in LDS later through store_tile with conflict-free
-  // ds_write_b128.  (global_load_lds stalls the issuing wave on this GPU:
-  // measured ~1/3 of a tile's time.)
+  // ds_write_b128.  (global_load_lds stalls the issuing wave on this GPU.)
   u32x4_t stg[8];
   auto fetch_tile = [&](int t) {
-    const int kb = t * kKT;
     const int kmax = sk_len - 1;
+    int key0 = min(t * kKT + 16 * wu, kmax);
+    const uint8_t *kp, *vp;
     if constexpr (MODE == FW_KV_PAGED) {
-      const int key0 = min(kb + 16 * w, kmax) & ~15;
+      key0 &= ~15;  // a 16-row group never straddles a page (P % 16 == 0)
       int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
       page = min(max(page, 0), a.num_pages - 1);
-      const uint8_t *prow = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
-      const size_t rstride = (size_t)a.CH * 256;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = ld_row0 + 4 * i;
-        const int kr = min(kb + r, kmax) - key0;
-        const uint8_t *src = prow + (size_t)kr * rstride + 16 * (ld_chunk ^ swz(r));
-        stg[i] = *(const u32x4_t *)src;
-        stg[4 + i] = *(const u32x4_t *)(src + 256);
-      }
+      kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
+      vp = kp + 256;
     } else {
+      kp = kbase_p + (size_t)key0 * kstB;
+      vp = vbase_p + (size_t)key0 * vstB;
+    }
+    const uint32_t lim = (uint32_t)(kmax - key0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = ld_row0 + 4 * i;
-        const size_t key = (size_t)(kbase + min(kb + r, kmax));
-        const size_t c16 = 16 * (ld_chunk ^ swz(r));
-        stg[i] = *(const u32x4_t *)(a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + key * a.kst) + c16);
-        stg[4 + i] = *(const u32x4_t *)(a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + key * a.vst) + c16);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lr = min(lr0 + 4u * i, lim);
+      const uint32_t c16 = c16b ^ (16u * i);
+      stg[i] = *(const u32x4_t *)(kp + (__umul24(lr, kstB) + c16));
+      stg[4 + i] = *(const u32x4_t *)(vp + (__umul24(lr, vstB) + c16));
     }
   };
   auto store_tile = [&](FW_LDS uint8_t *kdst, FW_LDS uint8_t *vdst) {
@@ -542,10 +554,9 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   // compile-time offset (buffer, sub-tile, k-step).
   // K (A of S^T): row r = 32st + n, physical chunk (2j+g) ^ swz(n): one base
   // per step j.
-  const int koff[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int kofs[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) kofs[j] = koff[j] + n * kRowB + 16 * ((2 * j + g) ^ swz(n));
+  for (int j = 0; j < 8; ++j) kofs[j] = n * kRowB + 16 * ((2 * j + g) ^ swz(n));
   // V (A of O^T, ds_read_b64_tr_b16): 16-lane group G covers dims
   // 32c + 16(G&1) .. +15 for keys 16u + 8hh + 4(G>>1) + a; lane 4a+b points at
   // dims +4b..+4b+3, i.e. logical chunk 4c + lo, lo = 2(G&1) + (b>>1).  With
@@ -562,32 +573,34 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       vofs[c][hh] = kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
                     16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
-  // Computes tile t from buf; the next tile's loads (tn >= 0) are issued once
-  // the QK MFMAs are in flight.
-  auto compute_tile = [&](int t, const FW_LDS uint8_t *buf, int tn) {
-    const int kb = t * kKT;
-    // ---------------- S^T = K Q^T : two 32-key sub-tiles; sub-tile 1's K
-    // operands are read while sub-tile 0's MFMAs run.
-    f32x16_t sacc[2];
-    {
-      bf16x8_t kop0[8], kop1[8];
+  // ---- S^T = K Q^T for one tile: two 32-key sub-tiles; sub-tile 1's K
+  // operands are read while sub-tile 0's MFMAs run.
+  auto qk = [&](const FW_LDS uint8_t *buf, f32x16_t (&sacc)[2]) {
+    bf16x8_t kop0[8], kop1[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
+    for (int j = 0; j < 8; ++j)
+      kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
-      __builtin_amdgcn_s_setprio(1);
+    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
-        sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
-      __builtin_amdgcn_s_setprio(0);
+    for (int j = 0; j < 8; ++j) {
+      kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
+      sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
     }
-    if (tn >= 0) fetch_tile(tn);
-    // ---------------- online softmax (log2 units), lane = query row n
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // ---- online softmax (log2 units, lane = query row n) and O^T += V^T P^T.
+  // The anchor m_run is static: a tile is exponentiated against the current
+  // anchor, and only when that overflows the lane's partial row sum (> 2^16,
+  // i.e. a score more than ~11 above the anchor) or a row sees its first valid
+  // key does the wave take the slow path: row max, new anchor, O/l rescale,
+  // exponentiate again.  All exp2 arguments on the fast path are <= 16.
+  auto softmax_pv = [&](int t, const FW_LDS uint8_t *buf, f32x16_t (&sacc)[2]) {
+    const int kb = t * kKT;
     if (a.softcap_log2 != 0.f) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -596,6 +609,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     }
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
+    bool row_has_key = true;
     if (!full) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -604,38 +618,38 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
           const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
           sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
         }
+      row_has_key = max(r_lo, kb) < min(r_hi, kb + kKT);
     }
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
-    tmax = wave_max_xor(tmax, 32);
-    // Static anchor with a guard: the anchor moves only when a tile's max
-    // exceeds it by more than kAnchorGuard (log2 units), so the O rescale is
-    // rare; exp2 arguments stay <= kAnchorGuard.
-    float alpha = 1.f;
-    if (__any(tmax > m_run + kAnchorGuard)) {
-      const float m_new = fmaxf(m_run, tmax);
-      alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float psum = 0.f;
     bf16x8_t pop[4];
+    float psum;
+    auto exponentiate = [&](float m_use) {
+      psum = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      u32x4_t pw;
+      for (int u = 0; u < 4; ++u) {
+        u32x4_t pw;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e] - m_use);
-        const float p1 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e + 1] - m_use);
-        psum += p0 + p1;
-        pw[e] = pack_bf16(p0, p1);
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e] - m_use);
+          const float p1 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e + 1] - m_use);
+          psum += p0 + p1;
+          pw[e] = pack_bf16(p0, p1);
+        }
+        pop[u] = __builtin_bit_cast(bf16x8_t, pw);
       }
-      pop[u] = __builtin_bit_cast(bf16x8_t, pw);
-    }
-    if (__any(alpha != 1.f)) {
+    };
+    exponentiate(m_run == -INFINITY ? 0.f : m_run);
+    if (__any(!(psum <= kPsumTrigger) || (m_run == -INFINITY && row_has_key))) {
+      asm volatile("" ::: "memory");  // a real branch: never if-converted
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
+      tmax = wave_max_xor(tmax, 32);
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      exponentiate(m_new == -INFINITY ? 0.f : m_new);
       l_run *= alpha;
 #pragma unroll
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
@@ -645,13 +659,11 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
     auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        u32x2_t part[2];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const FW_LDS uint8_t *src = buf + vofs[c][hh] + (16 * u + 8 * hh) * kRowB;
-          part[hh] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)src));
-        }
-        dst[c] = __builtin_bit_cast(bf16x8_t, u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]});
+        const FW_LDS uint8_t *src = buf + vofs[c][0] + 16 * u * kRowB;
+        const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)src);
+        const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (FW_LDS v4i16_t *)(buf + vofs[c][1] + (16 * u + 8) * kRowB));
+        dst[c] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     };
     bf16x8_t vop[2][4];
@@ -672,16 +684,20 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   };
 
   // ---- main loop: tile t computes from one buffer while tile t+1 is fetched
-  // and then stored into the other; one barrier per tile (this wave's LDS
-  // stores and operand reads done, no memory fence).
+  // (issued once the QK MFMAs are queued) and then stored into the other; one
+  // barrier per tile (this wave's LDS stores and operand reads done, no memory
+  // fence).
   auto tile_barrier = [&]() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
   };
   auto step = [&](int t, const FW_LDS uint8_t *cur, FW_LDS uint8_t *kn, FW_LDS uint8_t *vn) {
     const int tn = t + 1 < t_end ? t + 1 : -1;
-    if (wave_needs(t)) compute_tile(t, cur, tn);
-    else if (tn >= 0) fetch_tile(tn);
+    const bool need = wave_needs(t);
+    f32x16_t sacc[2];
+    if (need) qk(cur, sacc);
+    if (tn >= 0) fetch_tile(tn);
+    if (need) softmax_pv(t, cur, sacc);
     if (tn >= 0) store_tile(kn, vn);
     tile_barrier();
   };
@@ -729,19 +745,404 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 K/V, ping-pong schedule.  Workgroup = 8 waves = 256 q rows of one query
+// head (wave w owns rows 32w .. 32w+31), one workgroup per CU, so each SIMD
+// runs one wave of group 0 (waves 0-3) and one of group 1 (waves 4-7).  Time
+// is cut into barrier-delimited slots and group 1 runs one slot behind group
+// 0, so in every slot one wave of each SIMD does matrix work (PV of tile j-1,
+// then QK of tile j) while the other does the online softmax of its tile:
+//   slot 2j   : group 0  PV(j-1) QK(j)      group 1  softmax(j-1)
+//   slot 2j+1 : group 0  softmax(j)         group 1  PV(j-1) QK(j)
+// The MFMA pipe and the VALU of a SIMD are then busy at the same time by
+// construction rather than by chance.
+// K/V tiles rotate through three LDS buffers (tile j in buffer j % 3), read in
+// slots 2j .. 2j+2; each half of a tile is written two slots after its loads
+// were issued and only after the buffer's previous tile has passed its last
+// reader's barrier.  All 8 waves share the loads (8 key rows each).
+constexpr int kPPWaves = 8;
+constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
+constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = w >> 2;
+  const int n = lane & 31;
+  const int g = lane >> 5;
+
+  // ------------------------------------------------------------ tile decode
+  int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
+  if constexpr (MODE == FW_KV_DENSE) {
+    const int nbh = a.B * a.H;
+    const int bid = blockIdx.x;
+    int qt, bh;
+    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
+      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
+      qt = a.n_qt - 1 - wi / hx;
+      bh = x * hx + wi % hx;
+    } else {
+      qt = a.n_qt - 1 - bid / nbh;
+      bh = bid % nbh;
+    }
+    b = bh / a.H;
+    h = bh % a.H;
+    q0 = qt * kPPRows;
+    sq_len = a.Sq;
+    sk_len = a.Sk;
+  } else {
+    if ((int)blockIdx.x >= a.sched[0]) return;
+    seq = a.sched[1 + 2 * blockIdx.x];
+    q0 = a.sched[2 + 2 * blockIdx.x];
+    h = blockIdx.y;
+    if (seq < 0) {  // packed padding rows: out 0, lse -inf
+      const int r0 = q0 + w * 32 + n;
+      if (r0 < a.Sq) {
+        uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
+        for (int d = g * 64; d < g * 64 + 64; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
+        if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
+      }
+      return;
+    }
+    qtok0 = a.cu_q[seq];
+    sq_len = a.cu_q[seq + 1] - qtok0;
+    if constexpr (MODE == FW_KV_VARLEN) {
+      kbase = a.cu_k[seq];
+      sk_len = a.cu_k[seq + 1] - kbase;
+    } else {
+      sk_len = a.seqused_k[seq];
+    }
+  }
+  const int hk = h / a.G;
+  const int off = sk_len - sq_len;  // bottom-right alignment
+  auto row_hi = [&](int r) {
+    const int p = r + off;
+    return a.wr >= 0 ? min(sk_len, p + a.wr + 1) : sk_len;
+  };
+  auto row_lo = [&](int r) {
+    const int p = r + off;
+    return a.wl >= 0 ? max(0, p - a.wl) : 0;
+  };
+  const int last_row = min(q0 + kPPRows, sq_len) - 1;
+  const int wg_lo = row_lo(q0);
+  const int wg_hi = row_hi(last_row);
+  const int w_first = q0 + 32 * w;
+  const int w_last = min(w_first + 31, sq_len - 1);
+  const bool w_any = w_first <= w_last;
+  const int w_lo = w_any ? row_lo(w_first) : 0;
+  const int w_hi = w_any ? row_hi(w_last) : 0;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < sq_len;
+  const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
+
+  // ------------------------------------------------------------ Q^T operand
+  bf16x8_t qop[8];
+  {
+    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
+                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
+    u32x4_t raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
+      qop[j] = __builtin_bit_cast(bf16x8_t, o);
+    }
+  }
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
+  const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
+  const int T = t_end - t_begin;
+
+  // ---- global -> registers -> LDS: wave w moves key rows 8w .. 8w+7 of a
+  // tile; lane l takes local row l/16 + 4i (LDS row 8w + 4i + l/16) and
+  // physical chunk l % 16, which holds logical chunk
+  // (l % 16) ^ swz(row) = (l % 16) ^ 4(l/16) ^ ((2w + i) & 3).
+  const uint32_t lr0 = lane >> 4;
+  const uint32_t c16b = 16u * ((lane & 15) ^ (lr0 << 2));
+  uint32_t kstB, vstB;
+  const uint8_t *kbase_p = nullptr, *vbase_p = nullptr;
+  if constexpr (MODE == FW_KV_PAGED) {
+    kstB = vstB = (uint32_t)a.CH * 256u;
+  } else {
+    kstB = 2u * (uint32_t)a.kst;
+    vstB = 2u * (uint32_t)a.vst;
+    kbase_p = a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kbase * a.kst);
+    vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
+  }
+  u32x4_t stg[4];
+  auto fetch_tile = [&](int j) __attribute__((always_inline)) {
+    const int kmax = sk_len - 1;
+    int key0 = min((t_begin + j) * kKT + 8 * w, kmax);
+    const uint8_t *kp, *vp;
+    if constexpr (MODE == FW_KV_PAGED) {
+      key0 &= ~7;  // an 8-row group never straddles a page (P % 16 == 0)
+      int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
+      page = min(max(page, 0), a.num_pages - 1);
+      kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
+      vp = kp + 256;
+    } else {
+      kp = kbase_p + (size_t)key0 * kstB;
+      vp = vbase_p + (size_t)key0 * vstB;
+    }
+    const uint32_t lim = (uint32_t)(kmax - key0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t lr = min(lr0 + 4u * i, lim);
+      const uint32_t c16 = c16b ^ (16u * ((2 * w + i) & 3));
+      stg[i] = *(const u32x4_t *)(kp + (__umul24(lr, kstB) + c16));
+      stg[2 + i] = *(const u32x4_t *)(vp + (__umul24(lr, vstB) + c16));
+    }
+  };
+  // LDS: K tiles of buffers 0,1,2 then V tiles of buffers 0,1,2, so every
+  // operand read is a per-lane base plus an immediate offset below 64 KiB.
+  FW_LDS uint8_t *const lds_base = (FW_LDS uint8_t *)lds;
+  auto store_tile = [&](int j) __attribute__((always_inline)) {
+    const int bi = j % 3;
+    FW_LDS uint8_t *kdst = lds_base + bi * kTileB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int o = (8 * w + 4 * i) * kRowB + 16 * lane;
+      *(FW_LDS u32x4_t *)(kdst + o) = stg[i];
+      *(FW_LDS u32x4_t *)(kdst + 3 * kTileB + o) = stg[2 + i];
+    }
+  };
+
+  auto store_tile_after_fetch = [&](int j) {
+    fetch_tile(j);
+    store_tile(j);
+  };
+
+  // ---- LDS operand addressing (per-lane offsets within a buffer).
+  int kofs[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kofs[j] = n * kRowB + 16 * ((2 * j + g) ^ swz(n));
+  const int tr_i = lane & 15, tr_G = lane >> 4;
+  const int tr_a = tr_i >> 2, tr_b = tr_i & 3, tr_kg = tr_G >> 1;
+  const int tr_lo = 2 * (tr_G & 1) + (tr_b >> 1);
+  int vofs[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      vofs[c][hh] = 3 * kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
+                    16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
+
+  f32x16_t sacc[2];
+  bf16x8_t pops[2][4];
+
+  auto qk = [&](const int bi) __attribute__((always_inline)) {
+    const FW_LDS uint8_t *buf = lds_base + bi * kTileB;
+    bf16x8_t kop0[8], kop1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
+      sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
+  };
+
+  auto pv = [&](const int bi, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
+    const FW_LDS uint8_t *buf = lds_base + bi * kTileB;
+    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (FW_LDS v4i16_t *)(buf + vofs[c][0] + 16 * u * kRowB));
+        const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (FW_LDS v4i16_t *)(buf + vofs[c][1] + (16 * u + 8) * kRowB));
+        dst[c] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    };
+    bf16x8_t vop[2][4];
+    read_v(0, vop[0]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
+    }
+  };
+
+  // Online softmax of tile t (log2 units, lane = query row n) into pop, with
+  // the static anchor: exponentiate against m_run, and only when the lane's
+  // partial row sum overflows 2^16 (a score more than ~11 above the anchor) or
+  // a row sees its first valid key take the slow path (row max, new anchor,
+  // O/l rescale, exponentiate again).
+  auto softmax = [&](int t, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
+    const int kb = t * kKT;
+    if (a.softcap_log2 != 0.f) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
+    }
+    const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
+                      kb + kKT <= sk_len;
+    bool row_has_key = true;
+    if (!full) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
+        }
+      row_has_key = max(r_lo, kb) < min(r_hi, kb + kKT);
+    }
+    float psum;
+    auto exponentiate = [&](float m_use) {
+      psum = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        u32x4_t pw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e] - m_use);
+          const float p1 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e + 1] - m_use);
+          psum += p0 + p1;
+          pw[e] = pack_bf16(p0, p1);
+        }
+        pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+      }
+    };
+    exponentiate(m_run == -INFINITY ? 0.f : m_run);
+    if (__any(!(psum <= kPsumTrigger) || (m_run == -INFINITY && row_has_key))) {
+      asm volatile("" ::: "memory");  // a real branch: never if-converted
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
+      tmax = wave_max_xor(tmax, 32);
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      exponentiate(m_new == -INFINITY ? 0.f : m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+    }
+    l_run += psum;
+  };
+  auto wave_needs = [&](int j) {
+    const int kb = (t_begin + j) * kKT;
+    return w_any && kb < w_hi && kb + kKT > w_lo;
+  };
+  // End of slot: this wave's LDS reads and writes are complete, then all
+  // waves meet (the register-staged global loads stay in flight).
+  auto slot_barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+
+  // Both groups run the same sequence [M(j) | barrier | S(j) | barrier],
+  // M(j) = PV(j-1) + QK(j) and S(j) = softmax(j); group 1 starts one barrier
+  // later.  In S(j) a wave also writes its rows of tile j+1+grp (fetched two
+  // slots earlier) and fetches its rows of tile j+2+grp: group 0 carries key
+  // rows 0-31 of each tile, group 1 rows 32-63.
+  if (T > 0) {
+    store_tile_after_fetch(0);
+    if (grp == 1 && T > 1) store_tile_after_fetch(1);
+    if (1 + grp < T) fetch_tile(1 + grp);
+    slot_barrier();  // tile 0 complete
+    if (grp == 1) slot_barrier();
+    // Unrolled by three so every buffer index is a compile-time constant.
+    auto body = [&](const int j, const auto bi, const auto pi) __attribute__((always_inline)) {
+      constexpr int B = decltype(bi)::value;
+      constexpr int P = decltype(pi)::value;
+      if (j < T && wave_needs(j)) qk(B);
+      if (j >= 1 && wave_needs(j - 1)) pv((B + 2) % 3, pops[P ^ 1]);
+      slot_barrier();
+      if (j + 1 + grp < T) store_tile(j + 1 + grp);
+      if (j + 2 + grp < T) fetch_tile(j + 2 + grp);
+      if (j < T && wave_needs(j)) softmax(t_begin + j, pops[P]);
+      slot_barrier();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int j = 0; j <= T; j += 6) {
+      body(j, I0(), I0());
+      if (j + 1 > T) break;
+      body(j + 1, I1(), I1());
+      if (j + 2 > T) break;
+      body(j + 2, I2(), I0());
+      if (j + 3 > T) break;
+      body(j + 3, I0(), I1());
+      if (j + 4 > T) break;
+      body(j + 4, I1(), I0());
+      if (j + 5 > T) break;
+      body(j + 5, I2(), I1());
+    }
+    if (grp == 0) slot_barrier();
+  }
+
+  // ------------------------------------------------------------ epilogue
+  l_run += __shfl_xor(l_run, 32, 64);
+  float M = m_run, Lsum = l_run, oscale = 1.f;
+  if (a.sinks) {
+    const float sk = a.sinks[h] * kLog2e;
+    if (sk != -INFINITY) {
+      const float Mn = fmaxf(M, sk);
+      const float c_old = fast_exp2(M - Mn);
+      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
+      oscale = c_old;
+      M = Mn;
+    }
+  }
+  if (!row_ok) return;
+  const bool any = Lsum > 0.f && l_run > 0.f;
+  const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
+  uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
+                          pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
+      *(u32x2_t *)(op + 32 * c + 8 * rr + 4 * g) = wv;
+    }
+  if (a.lse && g == 0) {
+    a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] =
+        Lsum > 0.f ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
+  }
+}
+
 // One workgroup: per-sequence q tiles from cu_seqlens_q, then padding tiles
 // for the packed rows past cu_seqlens_q[num_active] (schedule.py:617-717).
 __global__ __launch_bounds__(1024) void fw_prefill_schedule(const int32_t *cu_q,
                                                             const int32_t *num_active, int B,
                                                             int total_q, int32_t *sched,
-                                                            int max_tiles) {
+                                                            int max_tiles, int qt) {
   __shared__ int part[1024];
   const int tid = threadIdx.x;
   const int nact = num_active ? min(max(*num_active, 0), B) : B;
   const int per = (nact + 1023) / 1024;
   const int s0 = tid * per, s1 = min(nact, s0 + per);
   int mine = 0;
-  for (int s = s0; s < s1; ++s) mine += (cu_q[s + 1] - cu_q[s] + kQT - 1) / kQT;
+  for (int s = s0; s < s1; ++s) mine += (cu_q[s + 1] - cu_q[s] + qt - 1) / qt;
   part[tid] = mine;
   __syncthreads();
   for (int o = 1; o < 1024; o <<= 1) {  // inclusive scan
@@ -753,7 +1154,7 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(const int32_t *cu_q,
   int idx = part[tid] - mine;
   for (int s = s0; s < s1; ++s) {
     const int len = cu_q[s + 1] - cu_q[s];
-    for (int q0 = 0; q0 < len; q0 += kQT) {
+    for (int q0 = 0; q0 < len; q0 += qt) {
       if (idx < max_tiles) {
         sched[1 + 2 * idx] = s;
         sched[2 + 2 * idx] = q0;
@@ -763,18 +1164,18 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(const int32_t *cu_q,
   }
   const int real = part[1023];
   const int pad0 = nact > 0 ? cu_q[nact] : 0;
-  const int npad = total_q > pad0 ? (total_q - pad0 + kQT - 1) / kQT : 0;
+  const int npad = total_q > pad0 ? (total_q - pad0 + qt - 1) / qt : 0;
   for (int i = tid; i < npad; i += 1024) {
     if (real + i < max_tiles) {
       sched[1 + 2 * (real + i)] = -1;
-      sched[2 + 2 * (real + i)] = pad0 + i * kQT;
+      sched[2 + 2 * (real + i)] = pad0 + i * qt;
     }
   }
   if (tid == 0) sched[0] = min(real + npad, max_tiles);
 }
 
-static int max_sched_tiles(const fw_prefill_params *p) {
-  return 2 * ((p->seqlen_q + kQT - 1) / kQT) + p->batch + 1;
+static int max_sched_tiles(const fw_prefill_params *p, int qt) {
+  return 2 * ((p->seqlen_q + qt - 1) / qt) + p->batch + 1;
 }
 
 }  // namespace fw
@@ -783,13 +1184,25 @@ using namespace fw;
 
 extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
   if (p->kv_mode == FW_KV_DENSE) return 0;
-  return align_up((size_t)(1 + 2 * max_sched_tiles(p)) * sizeof(int32_t), 256);
+  return align_up((size_t)(1 + 2 * max_sched_tiles(p, kQT)) * sizeof(int32_t), 256);
+}
+
+// Kernel choice: bf16 K/V without softcap -> ping-pong kernel (256-row
+// tiles); with softcap the softmax is too heavy to hide behind one group's
+// MFMAs and the 4-wave kernel (128-row tiles, two per CU) is faster; fp8
+// pools -> register-staged kernel.
+static bool use_pingpong(const fw_prefill_params *p) {
+  return p->kv_dtype == FW_BF16 && !(p->softcap > 0.f);
 }
 
 template <int MODE>
-static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, hipStream_t s) {
+static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, bool pingpong,
+                        hipStream_t s) {
   switch (kv_dtype) {
-    case FW_BF16: fw_prefill_kernel<MODE><<<grid, 256, 0, s>>>(a); break;
+    case FW_BF16:
+      if (pingpong) fw_prefill_pp_kernel<MODE><<<grid, 512, 0, s>>>(a);
+      else fw_prefill_kernel<MODE><<<grid, 256, 0, s>>>(a);
+      break;
     case FW_FP8_E4M3:
       if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E4M3><<<grid, 256, 0, s>>>(a);
       break;
@@ -834,7 +1247,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.G = p->nheads / p->nheads_k;
   a.Sq = p->seqlen_q;
   a.Sk = p->seqlen_k;
-  a.n_qt = (p->seqlen_q + kQT - 1) / kQT;
+  const bool pingpong = use_pingpong(p);
+  const int qt_rows = pingpong ? kPPRows : kQT;
+  a.n_qt = (p->seqlen_q + qt_rows - 1) / qt_rows;
   a.P = p->page_size;
   a.max_pages = p->max_pages;
   a.num_pages = p->num_pages;
@@ -850,7 +1265,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, s);
+    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, pingpong, s);
     return check_launch("fw_prefill_kernel");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -864,13 +1279,13 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
                FW_ERR_VALUE, "paged needs seqused_k, block_table and page geometry");
   }
   if (p->seqlen_q <= 0) return FW_OK;
-  const int max_tiles = max_sched_tiles(p);
+  const int max_tiles = max_sched_tiles(p, qt_rows);
   fw_prefill_schedule<<<1, 1024, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
-                                         (int32_t *)p->workspace, max_tiles);
+                                         (int32_t *)p->workspace, max_tiles, qt_rows);
   int st = check_launch("fw_prefill_schedule");
   if (st != FW_OK) return st;
   dim3 grid(max_tiles, p->nheads);
-  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, s);
-  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, s);
+  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, pingpong, s);
+  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, pingpong, s);
   return check_launch("fw_prefill_kernel");
 }
