@@ -39,6 +39,12 @@ struct DecodeArgs {
   float *ws_o;   // [items][16][128] unnormalised partial O
   float2 *ws_ml; // [items][16] (running max in log2 units, row sum)
   int B, Sq, H, Hk, G, Rq, n_qtiles, P, max_pages, CH;
+  // Token-row geometry: a token row holds CH head rows; KV head h's K row is
+  // head row kstep*h and its V row head row kstep*h + vhead, vdelta bytes
+  // further on (merged pool: kstep 2, vhead 1, vdelta 0; contiguous K/V pair:
+  // kstep 1, vhead 0, vdelta = v_cache - k_cache).
+  int kstep, vhead;
+  int64_t vdelta;
   int split_keys, nsplit;
   int seqlen_add, has_new, causal, window_left, num_pages;
   float qscale;       // folded into q before its bf16 rounding
@@ -140,15 +146,18 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   const size_t row_bytes = (size_t)a.CH * kD * EB;
 
   // ---- fused append: the last split's wave of q tile 0 writes the new row.
-  if (a.has_new && qt == 0 && s == nsplit_row - 1) {
+  // (A row already at its capacity has no slot: nothing is written.)
+  if (a.has_new && qt == 0 && s == nsplit_row - 1 && L0 / a.P < a.max_pages) {
     const int page = min(max(table[L0 / a.P], 0), a.num_pages - 1);
     uint8_t *dst = a.cache + ((size_t)page * a.P + L0 % a.P) * row_bytes;
     const size_t hb = (size_t)kD * EB;  // bytes of one head row
     const uint8_t *kn = a.k_new + ((size_t)b * a.Hk + h) * hb;
     const uint8_t *vn = a.v_new + ((size_t)b * a.Hk + h) * hb;
+    uint8_t *kdst = dst + (size_t)(a.kstep * h) * hb;
+    uint8_t *vdst = dst + a.vdelta + (size_t)(a.kstep * h + a.vhead) * hb;
     for (int off = lane * 4; off < (int)hb; off += 256) {
-      *(uint32_t *)(dst + (2 * h) * hb + off) = *(const uint32_t *)(kn + off);
-      *(uint32_t *)(dst + (2 * h + 1) * hb + off) = *(const uint32_t *)(vn + off);
+      *(uint32_t *)(kdst + off) = *(const uint32_t *)(kn + off);
+      *(uint32_t *)(vdst + off) = *(const uint32_t *)(vn + off);
     }
     if (h == a.Hk - 1) {  // an fp8 pool's zero pad head
       for (int hp = 2 * a.Hk; hp < a.CH; ++hp)
@@ -186,8 +195,8 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   for (int c = 0; c < 8; ++c) oacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const size_t kh_off = (size_t)(2 * h) * kD * EB;
-  const size_t vh_off = (size_t)(2 * h + 1) * kD * EB;
+  const size_t kh_off = (size_t)(a.kstep * h) * kD * EB;
+  const size_t vh_off = (size_t)(a.kstep * h + a.vhead) * kD * EB;
   const size_t new_off = ((size_t)b * a.Hk + h) * kD * EB;
   const int last_key = total - 1;
   // Block-table entries of the whole split, one per lane (a split spans at
@@ -212,11 +221,12 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
       int page = __builtin_amdgcn_readlane(tbl_lane, sbc / a.P - first_page);
       page = min(max(page, 0), a.num_pages - 1);
       const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
+      const uint8_t *vrow = prow + a.vdelta;
       load_k_row<KV>(prow + k_lane_off, g, tl.krow[sub]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(prow + v_lane_off[i]);
-        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(prow + v_lane_off[i]);
+        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(vrow + v_lane_off[i]);
+        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(vrow + v_lane_off[i]);
       }
     }
   };
@@ -534,6 +544,9 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
              L.o_bytes + L.ml_bytes);
   FW_REQUIRE(p->q && p->kv_cache && p->cache_seqlens && p->block_table && p->out, FW_ERR_VALUE,
              "q, kv_cache, cache_seqlens, block_table and out are required");
+  FW_REQUIRE(!p->v_cache || (p->kv_dtype == FW_BF16 && p->max_pages == 1), FW_ERR_VALUE,
+             "a contiguous K/V pair is bf16 with a one-column table (cache_batch_idx);"
+             " got kv_dtype=%d max_pages=%d", p->kv_dtype, p->max_pages);
   DecodeArgs a;
   a.q = (const uint16_t *)p->q;
   a.cache = (uint8_t *)p->kv_cache;
@@ -553,7 +566,17 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   a.n_qtiles = L.n_qtiles;
   a.P = p->page_size;
   a.max_pages = p->max_pages;
-  a.CH = merged_heads(p->nheads_k, p->kv_dtype);
+  if (p->v_cache) {  // contiguous (batch_cache, capacity, nheads_k, head_dim) pair
+    a.CH = p->nheads_k;
+    a.kstep = 1;
+    a.vhead = 0;
+    a.vdelta = (int64_t)((const uint8_t *)p->v_cache - (const uint8_t *)p->kv_cache);
+  } else {
+    a.CH = merged_heads(p->nheads_k, p->kv_dtype);
+    a.kstep = 2;
+    a.vhead = 1;
+    a.vdelta = 0;
+  }
   a.split_keys = L.split;
   a.nsplit = L.nsplit;
   a.has_new = p->k_new != nullptr;

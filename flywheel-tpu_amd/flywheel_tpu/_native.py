@@ -39,6 +39,7 @@ class DecodeParams(ctypes.Structure):
         ("causal", _i32), ("window_left", _i32),
         ("k_descale", _f32), ("v_descale", _f32),
         ("split_keys", _i32),
+        ("v_cache", _c_p),
     ]
 
 

@@ -1,5 +1,5 @@
-"""flash_attn_with_kvcache: attention against a paged merged KV cache with
-an optional append, on the gfx950 kernels.
+"""flash_attn_with_kvcache: attention against a paged merged KV cache or a
+contiguous K/V cache pair, with an optional append, on the gfx950 kernels.
 
 Mirrors the reference's `flash_attn_with_kvcache`
 (flywheel_tpu/softmax_attention/decode.py:175-625): same argument names,
@@ -64,8 +64,10 @@ def append_ragged(kv_cache, k, v, cu_seqlens, cache_seqlens, block_table, num_ac
 
 def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_active, sinks, *,
                  nheads_k, softmax_scale, softcap, causal, window_left, k_descale, v_descale,
-                 seqlen_add=0, return_lse=False, split_keys=0):
-    """The split-K decode kernel over a merged pool (kernels/decode.py:463-1915).
+                 seqlen_add=0, return_lse=False, split_keys=0, v_cache=None):
+    """The split-K decode kernel (kernels/decode.py:463-1915) over a merged
+    pool, or with v_cache over the contiguous (batch_cache, capacity, nheads_k,
+    head_dim) K/V pair, block_table then being cache_batch_idx as (batch, 1).
 
     q (batch, seqlen_q, nheads, head_dim) bf16.  Returns (out, lse|None)."""
     batch, seqlen_q, nheads, head_dim = q.shape
@@ -74,6 +76,7 @@ def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_acti
            if return_lse else None)
     p = N.DecodeParams()
     p.q, p.kv_cache, p.k_new, p.v_new = N.ptr(q), N.ptr(kv_cache), N.ptr(k_new), N.ptr(v_new)
+    p.v_cache = N.ptr(v_cache)
     p.cache_seqlens, p.block_table = N.ptr(cache_seqlens), N.ptr(block_table)
     p.num_active, p.sinks, p.out, p.lse = N.ptr(num_active), N.ptr(sinks), N.ptr(out), N.ptr(lse)
     p.batch, p.seqlen_q, p.nheads, p.nheads_k, p.head_dim = batch, seqlen_q, nheads, nheads_k, head_dim
@@ -158,14 +161,17 @@ def flash_attn_with_kvcache(
     nheads_k=None,
     learnable_sink=None,
 ):
-    """Attention against a paged merged KV cache, with optional append.
+    """Attention against a KV cache, with optional append.
 
     Same contract as the reference (`softmax_attention/decode.py:189-285`):
     q (batch, seqlen_q, nheads, head_dim) or packed (total_q, nheads, head_dim)
     with cu_seqlens_q / max_seqlen_q; k_cache the merged
-    (num_pages, page_size, cache_heads, head_dim) pool with v_cache=None;
-    block_table (batch, max_pages_per_seq); new k / v appended after each row's
-    cache_seqlens.  Returns (out, [lse,] kv_cache), kv_cache updated in place.
+    (num_pages, page_size, cache_heads, head_dim) pool with v_cache=None and
+    block_table (batch, max_pages_per_seq), or (single-token decode) separate
+    (batch_cache, capacity, nheads_k, head_dim) k_cache / v_cache with
+    cache_batch_idx; new k / v appended after each row's cache_seqlens.
+    Returns (out, [lse,] kv_cache) or (out, [lse,] k_cache, v_cache), the
+    caches updated in place.
     `interpret` is accepted and ignored (there is no interpreter here).
     """
     del interpret
@@ -208,40 +214,57 @@ def flash_attn_with_kvcache(
             "Multi-token and packed KV-cache attention needs the paged merged cache"
             " (block_table); the contiguous K/V pair serves single-token decode only."
         )
-    if not is_paged:
-        raise NotImplementedError(
-            "the contiguous K/V cache pair (block_table=None) is not implemented on"
-            " this backend yet; pass a paged merged cache with block_table."
-        )
-    if v_cache is not None:
-        raise ValueError(
-            "With block_table, pass one merged (num_pages, page_size, cache_heads,"
-            " head_dim) cache as k_cache and v_cache=None; separate paged K and V"
-            " caches are not supported."
-        )
-    if cache_batch_idx is not None:
-        raise ValueError(
-            "block_table and cache_batch_idx are mutually exclusive: the block table"
-            " already maps each query row to its pages."
-        )
-    if k_cache.ndim != 4:
-        raise ValueError(
-            "With block_table, k_cache must be (num_pages, page_size, cache_heads,"
-            f" head_dim), the KV heads' K and V rows interleaved; got {tuple(k_cache.shape)=}."
-        )
-    if nheads_k is None and k is not None:
-        nheads_k = k.shape[-2]
-    nheads_k = resolve_merged_kv_heads(k_cache.shape[2], k_cache.dtype, nheads_k)
-    page_size = k_cache.shape[1]
-    if page_size % 16:
-        raise ValueError(f"page_size (k_cache.shape[1]) must be a multiple of 16; got {page_size}.")
-    block_table = as_tensor(block_table)
-    if block_table.is_floating_point() or block_table.dtype == torch.bool:
-        raise ValueError(f"block_table must be an integer array; got {block_table.dtype}.")
-    if block_table.ndim != 2 or block_table.shape[0] != batch:
-        raise ValueError(
-            f"block_table must be (batch={batch}, max_pages_per_seq); got {tuple(block_table.shape)}."
-        )
+    if is_paged:
+        if v_cache is not None:
+            raise ValueError(
+                "With block_table, pass one merged (num_pages, page_size, cache_heads,"
+                " head_dim) cache as k_cache and v_cache=None; separate paged K and V"
+                " caches are not supported."
+            )
+        if cache_batch_idx is not None:
+            raise ValueError(
+                "block_table and cache_batch_idx are mutually exclusive: the block table"
+                " already maps each query row to its pages."
+            )
+        if k_cache.ndim != 4:
+            raise ValueError(
+                "With block_table, k_cache must be (num_pages, page_size, cache_heads,"
+                f" head_dim), the KV heads' K and V rows interleaved; got {tuple(k_cache.shape)=}."
+            )
+        if nheads_k is None and k is not None:
+            nheads_k = k.shape[-2]
+        nheads_k = resolve_merged_kv_heads(k_cache.shape[2], k_cache.dtype, nheads_k)
+        page_size = k_cache.shape[1]
+        if page_size % 16:
+            raise ValueError(f"page_size (k_cache.shape[1]) must be a multiple of 16; got {page_size}.")
+        block_table = as_tensor(block_table)
+        if block_table.is_floating_point() or block_table.dtype == torch.bool:
+            raise ValueError(f"block_table must be an integer array; got {block_table.dtype}.")
+        if block_table.ndim != 2 or block_table.shape[0] != batch:
+            raise ValueError(
+                f"block_table must be (batch={batch}, max_pages_per_seq); got {tuple(block_table.shape)}."
+            )
+    else:
+        if v_cache is None:
+            raise ValueError(
+                "Without block_table, k_cache and v_cache must be separate (batch_cache,"
+                " capacity, nheads_k, head_dim) caches; got v_cache=None (a merged cache"
+                " must be paged)."
+            )
+        if k_cache.ndim != 4 or tuple(v_cache.shape) != tuple(k_cache.shape):
+            raise ValueError(
+                "k_cache and v_cache must share the shape (batch_cache, capacity, nheads_k,"
+                f" head_dim); got {tuple(k_cache.shape)=}, {tuple(v_cache.shape)=}."
+            )
+        if nheads_k is not None and nheads_k != k_cache.shape[2]:
+            raise ValueError(f"{nheads_k=} must match the contiguous caches' {k_cache.shape[2]}.")
+        nheads_k = k_cache.shape[2]
+        # the reference's decode tiles need whole 128-key blocks of capacity
+        # (decode.py:219-220, kernels/decode.py:2006-2011)
+        if k_cache.shape[1] <= 0 or k_cache.shape[1] % 128:
+            raise ValueError(
+                f"capacity (k_cache.shape[1]) must be a positive multiple of 128; got {k_cache.shape[1]}."
+            )
     if k_cache.shape[3] != head_dim:
         raise ValueError(f"cache head_dim {k_cache.shape[3]} must match q's {head_dim}.")
     if nheads_k <= 0 or nheads <= 0 or nheads % nheads_k:
@@ -249,8 +272,10 @@ def flash_attn_with_kvcache(
     has_new = k is not None
     if has_new != (v is not None):
         raise ValueError("k and v must be passed together, or both left out.")
-    kv_operands = (k_cache, k, v) if has_new else (k_cache,)
-    if q.dtype != torch.bfloat16 or any(t.dtype != k_cache.dtype for t in kv_operands):
+    cache_operands = (k_cache,) if is_paged else (k_cache, v_cache)
+    kv_operands = (*cache_operands, k, v) if has_new else cache_operands
+    if (q.dtype != torch.bfloat16 or any(t.dtype != k_cache.dtype for t in kv_operands)
+            or (not is_paged and k_cache.dtype != torch.bfloat16)):
         raise NotImplementedError(
             "q must be bfloat16 and the KV operands share one dtype, bfloat16 or (paged"
             f" pool) float8_e4m3fn / float8_e5m2; got q {q.dtype}, KV"
@@ -270,8 +295,12 @@ def flash_attn_with_kvcache(
             raise ValueError(
                 f"cache_seqlens must be a scalar or ({batch},) int array; got {cs_shape}."
             )
+    if cache_batch_idx is not None:
+        idx_shape = tuple(as_tensor(cache_batch_idx).shape)
+        if idx_shape != (batch,):
+            raise ValueError(f"cache_batch_idx must be a scalar or ({batch},) int array; got {idx_shape}.")
     device = q.device
-    N.require_device(q, k_cache, k, v)
+    N.require_device(q, k_cache, v_cache, k, v)
     if isinstance(cache_seqlens, int):
         row_cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=device)
     else:
@@ -292,7 +321,12 @@ def flash_attn_with_kvcache(
                      and seqlen_q * (nheads // nheads_k) <= MAX_FOLDED_QUERY_ROWS)
     else:
         is_folded = False
-    table = block_table.to(device=device, dtype=torch.int32).contiguous()
+    if is_paged:
+        table = block_table.to(device=device, dtype=torch.int32).contiguous()
+    elif cache_batch_idx is None:
+        table = torch.arange(batch, dtype=torch.int32, device=device).reshape(batch, 1)
+    else:
+        table = int32_device(cache_batch_idx, device, "cache_batch_idx").reshape(batch, 1).contiguous()
     num_active_t = _num_active_tensor(num_active, batch, device)
     q = q.contiguous()
     if has_new:
@@ -341,7 +375,8 @@ def flash_attn_with_kvcache(
         q, k_cache, k_new, v_new, row_cache_seqlens, table, num_active_t, sinks,
         nheads_k=nheads_k, softmax_scale=softmax_scale, softcap=float(softcap),
         causal=causal_eff, window_left=left, k_descale=k_descale, v_descale=v_descale,
-        seqlen_add=seqlen_add, return_lse=return_softmax_lse)
+        seqlen_add=seqlen_add, return_lse=return_softmax_lse,
+        v_cache=None if is_paged else v_cache)
     if return_softmax_lse:
-        return out, lse, k_cache
-    return out, k_cache
+        return (out, lse, *cache_operands)
+    return (out, *cache_operands)

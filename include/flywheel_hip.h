@@ -44,7 +44,7 @@ enum fw_dtype {
 
 /* The last error message of the calling thread ("" if none). */
 const char *fw_last_error(void);
-/* ABI version of this header: 1. */
+/* ABI version of this header: 2. */
 int fw_abi_version(void);
 
 /*
@@ -90,6 +90,13 @@ typedef struct fw_decode_params {
   int32_t window_left; /* -1 = unbounded */
   float k_descale, v_descale;
   int32_t split_keys;  /* keys per split-K work item; 0 = heuristic */
+  /* NULL: kv_cache is the merged pool above.  Otherwise the contiguous K/V
+   * cache pair of single-token decode (softmax_attention/decode.py:383-403,
+   * kernels/decode.py:2147-2178): kv_cache = K cache and v_cache = V cache,
+   * both (num_pages = batch_cache, page_size = capacity, nheads_k, head_dim)
+   * bf16, and block_table = cache_batch_idx as a (batch, 1) table
+   * (max_pages 1); the new token goes to [cache_batch_idx[b], cache_seqlens[b]]. */
+  const void *v_cache;
 } fw_decode_params;
 
 size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p);

@@ -168,7 +168,7 @@ def test_anchor_change_known_answer():
                                           return_softmax_lse=True)
     torch.cuda.synchronize()
     np.testing.assert_allclose(out.float().cpu().numpy(), 3.0, atol=1e-2)
-    qs = float(T.bf16(np.float32(1 / math.sqrt(d) * A.LOG2E)))
+    qs = float(np.asarray(T.bf16(np.float32(1 / math.sqrt(d) * A.LOG2E))).reshape(-1)[0])
     expect = 128 * 16 * qs * math.log(2) + math.log(cap // 2)
     np.testing.assert_allclose(lse.cpu().numpy(), expect, rtol=1e-5)
 
@@ -193,3 +193,97 @@ def test_split_k_invariance_and_determinism():
     for _ in range(20):
         o3, l3 = paged_decode(q, pool, None, None, lens, table, None, None, **kw)
         assert torch.equal(o3, o2) and torch.equal(l3, l2)
+
+
+# ---------------------------------------------------------------- contiguous K/V cache pair
+def run_contig(rng, *, batch, batch_cache, nheads, nheads_k, capacity, lengths, append,
+               batch_idx=None, window=(-1, -1), softcap=0.0, sinks=None, num_active=None):
+    """One single-token step over separate (batch_cache, capacity, nheads_k, 128)
+    K/V caches (decode.py:383-403); returns (out, lse, expected k/v codes, oracle
+    out, oracle lse)."""
+    from tests.gpu_util import dev_from_codes, random_codes
+    shape = (batch_cache, capacity, nheads_k, 128)
+    kc, vc = random_codes(rng, shape, torch.bfloat16), random_codes(rng, shape, torch.bfloat16)
+    q = randn(rng, (batch, 1, nheads, 128))
+    lengths = np.asarray(lengths, np.int32)
+    idx = np.arange(batch, dtype=np.int32) if batch_idx is None else np.asarray(batch_idx, np.int32)
+    kw = {}
+    exp_k, exp_v = kc.copy(), vc.copy()
+    if append:
+        kn = random_codes(rng, (batch, 1, nheads_k, 128), torch.bfloat16)
+        vn = random_codes(rng, (batch, 1, nheads_k, 128), torch.bfloat16)
+        kw["k"], kw["v"] = dev_from_codes(kn, torch.bfloat16), dev_from_codes(vn, torch.bfloat16)
+        live = batch if num_active is None else num_active
+        for r in range(live):
+            exp_k[idx[r], lengths[r]] = kn[r, 0]
+            exp_v[idx[r], lengths[r]] = vn[r, 0]
+    k_dev, v_dev = dev_from_codes(kc, torch.bfloat16), dev_from_codes(vc, torch.bfloat16)
+    res = flash_attn_with_kvcache(
+        to_dev_bf16(q), k_dev, v_dev, **kw,
+        cache_seqlens=torch.tensor(lengths, device=DEV),
+        cache_batch_idx=None if batch_idx is None else torch.tensor(idx, device=DEV),
+        window_size=window, softcap=softcap, return_softmax_lse=True, num_active=num_active,
+        learnable_sink=None if sinks is None else torch.tensor(sinks, device=DEV))
+    torch.cuda.synchronize()
+    out, lse, k_out, v_out = res
+    assert k_out is k_dev and v_out is v_dev
+    np.testing.assert_array_equal(codes_of(k_out), exp_k)
+    np.testing.assert_array_equal(codes_of(v_out), exp_v)
+    totals = lengths + (1 if append else 0)
+    ro, rl = A.decode_reference(q, T.bf16_to_f32(exp_k), T.bf16_to_f32(exp_v), totals,
+                                cache_batch_idx=idx, window_size=window, softcap=softcap,
+                                sinks=sinks)
+    return out.float().cpu().numpy(), lse.cpu().numpy(), ro, rl, totals
+
+
+@pytest.mark.parametrize("append", [True, False])
+@pytest.mark.parametrize("with_idx", [True, False])
+def test_contiguous_cache_decode(append, with_idx):
+    announce(f"contiguous decode append={append} batch_idx={with_idx}")
+    rng = np.random.default_rng(7)
+    lengths = [3, 517, 1799, 2047] if append else [1, 517, 2048, 1000]
+    idx = rng.permutation(6)[:4] if with_idx else None
+    out, lse, ro, rl, _ = run_contig(rng, batch=4, batch_cache=6 if with_idx else 4, nheads=8,
+                                     nheads_k=2, capacity=2048, lengths=lengths, append=append,
+                                     batch_idx=idx)
+    assert_close(out, ro)
+    assert_lse(lse, rl)
+
+
+def test_contiguous_cache_boundary_append_window():
+    """test_regression.py:1065-1112: a 255-key window over 512 / 1799 cached keys
+    in cache rows 2 and 0, the append landing on position 1799."""
+    announce("contiguous decode boundary append, window 255")
+    rng = np.random.default_rng(91)
+    out, lse, ro, rl, _ = run_contig(rng, batch=2, batch_cache=3, nheads=4, nheads_k=2,
+                                     capacity=2048, lengths=[512, 1799], append=True,
+                                     batch_idx=[2, 0], window=(255, 0))
+    assert_close(out, ro)
+    assert_lse(lse, rl)
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (255, 0)])
+@pytest.mark.parametrize("nheads,nheads_k", [(8, 1), (8, 2)])
+def test_contiguous_cache_sinks(window, nheads, nheads_k):
+    """test_regression.py:1148-1180: the empty row attends only its sink
+    (out 0, lse = sink)."""
+    announce(f"contiguous decode sinks window={window} h{nheads}/{nheads_k}")
+    rng = np.random.default_rng(29)
+    sinks = rng.uniform(-2.0, 8.0, nheads).astype(np.float32)
+    out, lse, ro, rl, _ = run_contig(rng, batch=3, batch_cache=3, nheads=nheads, nheads_k=nheads_k,
+                                     capacity=1024, lengths=[0, 517, 1024], append=False,
+                                     window=window, sinks=sinks)
+    assert_close(out, ro)
+    assert_lse(lse, rl)
+    np.testing.assert_allclose(lse[0], np.broadcast_to(sinks[:, None], lse[0].shape), atol=1e-5)
+    assert np.abs(out[0]).max() == 0.0
+
+
+def test_contiguous_cache_num_active_softcap():
+    announce("contiguous decode num_active=2 softcap")
+    rng = np.random.default_rng(8)
+    out, lse, ro, rl, _ = run_contig(rng, batch=4, batch_cache=4, nheads=16, nheads_k=4,
+                                     capacity=1024, lengths=[10, 1000, 30, 40], append=True,
+                                     softcap=30.0, num_active=2)
+    assert_close(out[:2], ro[:2])
+    assert_lse(lse[:2], rl[:2])

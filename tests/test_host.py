@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} is declared but not exported"
     assert set(names) == set(N.SIGNATURES), "ctypes bindings and header disagree"
-    assert lib.fw_abi_version() == 1
+    assert lib.fw_abi_version() == 2
 
 
 def test_struct_layouts_match_header_fields():
@@ -168,6 +168,31 @@ def test_flash_attn_with_kvcache_errors():
                                 block_table=table)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         flash_attn_with_kvcache(q, pool, None, **kw)
+
+
+def test_contiguous_cache_errors():
+    """decode.py:383-403 conditions for the contiguous K/V pair."""
+    kc = bf(3, 256, 2, 128)
+    q = bf(2, 1, 4, 128)
+    kw = dict(cache_seqlens=torch.tensor([3, 5], dtype=torch.int32))
+    with pytest.raises(ValueError):  # a merged cache must be paged
+        flash_attn_with_kvcache(q, kc, None, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, kc, bf(3, 128, 2, 128), **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, kc, kc, nheads_k=1, **kw)
+    with pytest.raises(ValueError):  # capacity a multiple of 128
+        flash_attn_with_kvcache(q, bf(3, 200, 2, 128), bf(3, 200, 2, 128), **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, kc, kc, cache_batch_idx=torch.tensor([0, 1, 2]), **kw)
+    with pytest.raises(NotImplementedError):  # fp8 only in a paged pool
+        f8 = kc.to(torch.float8_e4m3fn)
+        flash_attn_with_kvcache(q, f8, f8, **kw)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, kc, kc, bf(2, 1, 2, 128), None, **kw)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_with_kvcache(q, kc, kc, bf(2, 1, 2, 128), bf(2, 1, 2, 128),
+                                cache_batch_idx=torch.tensor([2, 0]), **kw)
 
 
 def test_write_kv_cache_pages_errors():
