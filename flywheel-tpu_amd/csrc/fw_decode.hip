@@ -52,6 +52,7 @@ struct DecodeArgs {
 };
 
 constexpr int kD = 128;
+constexpr float kPsumTrigger = 65536.f;  // lane partial-sum bound of the fast path
 
 // Visible key range of a row: [lo, total) overall; per folded row the causal
 // limit drops by (Sq - 1 - t).
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
       for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
     if (a.softcap_log2 != 0.f) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sc[e] = tanhf(sc[e]) * a.softcap_log2;
+      for (int e = 0; e < 8; ++e) sc[e] = fast_tanh(sc[e]) * a.softcap_log2;
     }
     if (edge) {
 #pragma unroll
@@ -282,29 +283,45 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
         sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
       }
     }
-    float tmax = sc[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sc[e]);
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
-    float psum = 0.f;
+    // Static anchor: exponentiate against the row's anchor m_run; only when a
+    // lane's partial sum overflows 2^16 (a score more than ~13 above the
+    // anchor) or a row meets its first valid key does the wave reduce the row
+    // max across its four lane groups and rescale O and l.
+    float psum;
     uint32_t pw[4];
+    auto exponentiate = [&]() {
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      psum = 0.f;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float p0 = fast_exp2(sc[2 * p] - m_use);
-      const float p1 = fast_exp2(sc[2 * p + 1] - m_use);
-      psum += p0 + p1;
-      pw[p] = pack_bf16(p0, p1);
+      for (int p = 0; p < 4; ++p) {
+        const float p0 = fast_exp2(sc[2 * p] - m_use);
+        const float p1 = fast_exp2(sc[2 * p + 1] - m_use);
+        psum += p0 + p1;
+        pw[p] = pack_bf16(p0, p1);
+      }
+    };
+    exponentiate();
+    bool fresh = false;
+    if (m_run == -INFINITY) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fresh = fresh || sc[e] != -INFINITY;
     }
-    l_run = l_run * alpha + psum;
-    if (__any(alpha != 1.f)) {
+    if (__any(!(psum <= kPsumTrigger) || fresh)) {
+      asm volatile("" ::: "memory");  // a real branch: never if-converted
+      float tmax = sc[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sc[e]);
+      tmax = wave_max_xor(tmax, 16);
+      tmax = wave_max_xor(tmax, 32);
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int c = 0; c < 8; ++c) oacc[c] *= alpha;
+      exponentiate();
     }
+    l_run += psum;
     const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, (u32x4_t){pw[0], pw[1], pw[2], pw[3]});
     // -------- O^T += V^T P^T, 8 tiles of 16 dims; tile c holds dim 8m + c.
     // Word w of a key's V (dims 8n+2w, 8n+2w+1) feeds tiles 2w and 2w+1.
