@@ -200,10 +200,11 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   const size_t vh_off = (size_t)(a.kstep * h + a.vhead) * kD * EB;
   const size_t new_off = ((size_t)b * a.Hk + h) * kD * EB;
   const int last_key = total - 1;
-  // Block-table entries of the whole split, one per lane (a split spans at
-  // most 64 pages); a sub-tile's page is then a readlane, off the load path.
+  // Block-table entries of the whole split, two per lane (a split spans at
+  // most 128 pages); a sub-tile's page is then a readlane, off the load path.
   const int first_page = k_begin / a.P;
-  const int tbl_lane = table[min(first_page + lane, a.max_pages - 1)];
+  const int tbl_lane0 = table[min(first_page + lane, a.max_pages - 1)];
+  const int tbl_lane1 = table[min(first_page + 64 + lane, a.max_pages - 1)];
 
   // Per-lane byte offsets inside a 16-row sub-tile: a load is the sub-tile's
   // uniform page row pointer plus a 32-bit lane offset.
@@ -219,7 +220,9 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const int sbc = min(tb + 16 * sub, last_key) & ~15;  // clamp into valid pages
-      int page = __builtin_amdgcn_readlane(tbl_lane, sbc / a.P - first_page);
+      const int pi = sbc / a.P - first_page;  // wave-uniform, < 128
+      int page = pi < 64 ? __builtin_amdgcn_readlane(tbl_lane0, pi)
+                         : __builtin_amdgcn_readlane(tbl_lane1, pi - 64);
       page = min(max(page, 0), a.num_pages - 1);
       const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
       const uint8_t *vrow = prow + a.vdelta;
@@ -485,12 +488,12 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
 }
 
 // Keys per split-K work item: about 32K items at full capacity, at least 256
-// keys, and at most what one lane-per-page table prefetch covers (64 pages
-// from a 32-key-aligned start: 63*P + gcd(32, P) keys).
+// keys, and at most what the two-entries-per-lane table prefetch covers (128
+// pages from a 32-key-aligned start: 127*P + gcd(32, P) keys).
 static int max_split_keys(int P) {
   int gcd = 32;
   while (P % gcd) gcd >>= 1;
-  return (63 * P + gcd) / 32 * 32;
+  return (127 * P + gcd) / 32 * 32;
 }
 
 static int pick_split(const fw_decode_params *p, int n_qtiles) {
@@ -501,12 +504,21 @@ static int pick_split(const fw_decode_params *p, int n_qtiles) {
   long split = (capacity * items_per_key + 32767) / 32768;
   split = (split + 31) / 32 * 32;
   if (split < 256) split = 256;
-  if (split > 896) split = 896;  // measured optimum for C3 (bf16) and C5 (fp8)
-  if (split > cap_split) split = cap_split;
+  // Every work item writes a (rows x 128) f32 partial; with many query rows
+  // per item (a verify window) longer splits pay for themselves.  Measured:
+  // C3 (4 rows) flat from 896 to 2016 keys, C5 (16 rows) 4.69 TB/s at 896,
+  // 5.05 TB/s at 1792.
+  const int rows = (int)std::min<long>(16, (long)p->seqlen_q * (p->nheads / p->nheads_k));
+  const long cap_rows = rows <= 8 ? 896 : 1792;
+  if (split > cap_rows) split = cap_rows;
+  if (split > cap_split) split = cap_split / 32 * 32;
   // Power-of-two multiples of 32 keys measured ~20% slower on MI355X (C3
-  // decode: 512 or 1024 keys ~4.3 TB/s, 576..960 keys 5.3-5.5 TB/s).
+  // decode: 512 or 1024 keys ~4.3 TB/s, 576..960 keys 5.3-5.5 TB/s; C5 2048
+  // keys 4.16 TB/s, 1792 keys 5.05 TB/s): step up by half when the caps
+  // allow, else down by an eighth.
   const long units = split / 32;
-  if ((units & (units - 1)) == 0 && split * 3 / 2 <= cap_split) split = split * 3 / 2;
+  if (units >= 8 && (units & (units - 1)) == 0)
+    split = split * 3 / 2 <= std::min<long>(cap_rows, cap_split) ? split * 3 / 2 : split * 7 / 8;
   return (int)split;
 }
 
