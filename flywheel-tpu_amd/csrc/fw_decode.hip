@@ -53,6 +53,8 @@ struct DecodeArgs {
 
 constexpr int kD = 128;
 constexpr float kPsumTrigger = 65536.f;  // lane partial-sum bound of the fast path
+constexpr int kStageRow = 132;
+constexpr int kTblPerLane = 4;            // block-table entries a lane prefetches per split           // padded f32 row of the partial-O staging slot
 
 // Visible key range of a row: [lo, total) overall; per folded row the causal
 // limit drops by (Sq - 1 - t).
@@ -121,6 +123,7 @@ template <int KV> constexpr int kDecodeWaves = KV == FW_BF16 ? 2 : 3;
 template <int KV>
 __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(DecodeArgs a) {
   constexpr int EB = KV == FW_BF16 ? 2 : 1;  // bytes per cache element
+  __shared__ __attribute__((aligned(16))) float stage[4][16 * kStageRow];  // partial-O staging
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
   const int g = lane >> 4;
@@ -200,11 +203,13 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   const size_t vh_off = (size_t)(a.kstep * h + a.vhead) * kD * EB;
   const size_t new_off = ((size_t)b * a.Hk + h) * kD * EB;
   const int last_key = total - 1;
-  // Block-table entries of the whole split, two per lane (a split spans at
-  // most 128 pages); a sub-tile's page is then a readlane, off the load path.
+  // Block-table entries of the whole split, kTblPerLane per lane (a split
+  // spans at most 64 * kTblPerLane pages); a sub-tile's page is then a
+  // readlane, off the load path.
   const int first_page = k_begin / a.P;
-  const int tbl_lane0 = table[min(first_page + lane, a.max_pages - 1)];
-  const int tbl_lane1 = table[min(first_page + 64 + lane, a.max_pages - 1)];
+  int tbl_lane[kTblPerLane];
+#pragma unroll
+  for (int t = 0; t < kTblPerLane; ++t) tbl_lane[t] = table[min(first_page + 64 * t + lane, a.max_pages - 1)];
 
   // Per-lane byte offsets inside a 16-row sub-tile: a load is the sub-tile's
   // uniform page row pointer plus a 32-bit lane offset.
@@ -220,9 +225,11 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const int sbc = min(tb + 16 * sub, last_key) & ~15;  // clamp into valid pages
-      const int pi = sbc / a.P - first_page;  // wave-uniform, < 128
-      int page = pi < 64 ? __builtin_amdgcn_readlane(tbl_lane0, pi)
-                         : __builtin_amdgcn_readlane(tbl_lane1, pi - 64);
+      const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
+      int page = __builtin_amdgcn_readlane(tbl_lane[0], pi & 63);
+#pragma unroll
+      for (int t = 1; t < kTblPerLane; ++t)
+        page = (pi >> 6) == t ? __builtin_amdgcn_readlane(tbl_lane[t], pi & 63) : page;
       page = min(max(page, 0), a.num_pages - 1);
       const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
       const uint8_t *vrow = prow + a.vdelta;
@@ -372,18 +379,28 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   const size_t item = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit + s;
-  if (row_ok) {
-    float *po = a.ws_o + (item * 16 + n) * kD;
-    // tile c, reg i -> dim 32g + 8i + c
+  // The (16 rows x 128 dims) f32 partial goes out through a wave-private LDS
+  // slot so that every global store writes two whole 512-byte rows (lane
+  // order = address order); stored straight from the MFMA layout each
+  // instruction would scatter 64 16-byte pieces.  Rows are padded to 132
+  // floats: the 16 rows of one column group land on distinct banks.
+  float *st = stage[threadIdx.x >> 6];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4_t v0 = {oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
-      f32x4_t v1 = {oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]};
-      *(f32x4_t *)(po + 32 * g + 8 * i) = v0;
-      *(f32x4_t *)(po + 32 * g + 8 * i + 4) = v1;
-    }
-    if (g == 0) a.ws_ml[item * 16 + n] = make_float2(m_run, l_run);
+  for (int i = 0; i < 4; ++i) {  // tile c, reg i -> dim 32g + 8i + c
+    const f32x4_t v0 = {oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
+    const f32x4_t v1 = {oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]};
+    *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i) = v0;
+    *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i + 4) = v1;
   }
+  const int rows_valid = min(16, a.Rq - qt * 16);
+  float *po = a.ws_o + item * 16 * kD;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int row = 2 * k + (lane >> 5), col = 4 * (lane & 31);
+    if (row < rows_valid)
+      *(f32x4_t *)(po + row * kD + col) = *(const f32x4_t *)(st + row * kStageRow + col);
+  }
+  if (row_ok && g == 0) a.ws_ml[item * 16 + n] = make_float2(m_run, l_run);
 }
 
 struct CombineArgs {
@@ -488,12 +505,12 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
 }
 
 // Keys per split-K work item: about 32K items at full capacity, at least 256
-// keys, and at most what the two-entries-per-lane table prefetch covers (128
-// pages from a 32-key-aligned start: 127*P + gcd(32, P) keys).
+// keys, and at most what the table prefetch covers (64 * kTblPerLane pages
+// from a 32-key-aligned start: (64 * kTblPerLane - 1) * P + gcd(32, P) keys).
 static int max_split_keys(int P) {
   int gcd = 32;
   while (P % gcd) gcd >>= 1;
-  return (127 * P + gcd) / 32 * 32;
+  return ((64 * kTblPerLane - 1) * P + gcd) / 32 * 32;
 }
 
 static int pick_split(const fw_decode_params *p, int n_qtiles) {
@@ -501,15 +518,16 @@ static int pick_split(const fw_decode_params *p, int n_qtiles) {
   if (p->split_keys > 0) return std::min((p->split_keys + 31) / 32 * 32, cap_split);
   const long capacity = (long)p->max_pages * p->page_size;
   const long items_per_key = (long)p->batch * p->nheads_k * n_qtiles;
-  long split = (capacity * items_per_key + 32767) / 32768;
+  // Every work item writes a (rows x 128) f32 partial; with many query rows
+  // per item (a verify window) fewer, longer splits pay for themselves.
+  // Measured: C3 (4 rows) best at 896 keys; C5 (16 rows) 4.69 TB/s at 896,
+  // 5.11 at 1792, 5.34 at 3584.
+  const int rows = (int)std::min<long>(16, (long)p->seqlen_q * (p->nheads / p->nheads_k));
+  const long target_items = rows <= 8 ? 32768 : 16384;
+  const long cap_rows = rows <= 8 ? 896 : 3584;
+  long split = (capacity * items_per_key + target_items - 1) / target_items;
   split = (split + 31) / 32 * 32;
   if (split < 256) split = 256;
-  // Every work item writes a (rows x 128) f32 partial; with many query rows
-  // per item (a verify window) longer splits pay for themselves.  Measured:
-  // C3 (4 rows) flat from 896 to 2016 keys, C5 (16 rows) 4.69 TB/s at 896,
-  // 5.05 TB/s at 1792.
-  const int rows = (int)std::min<long>(16, (long)p->seqlen_q * (p->nheads / p->nheads_k));
-  const long cap_rows = rows <= 8 ? 896 : 1792;
   if (split > cap_rows) split = cap_rows;
   if (split > cap_split) split = cap_split / 32 * 32;
   // Power-of-two multiples of 32 keys measured ~20% slower on MI355X (C3
