@@ -53,16 +53,25 @@ __global__ __launch_bounds__(256) void fw_append_kernel(
     int P, int num_pages, int max_pages) {
   const int i = blockIdx.x;
   const int nact = num_active ? min(*num_active, B) : B;
-  if (i >= cu[nact]) return;  // rows past the last active request are padding
-  // request r: the last r with cu[r] <= i
-  int lo = 0, hi = nact;  // cu[lo] <= i < cu[hi]
-  while (hi - lo > 1) {
-    int mid = (lo + hi) >> 1;
-    if (cu[mid] <= i) lo = mid; else hi = mid;
+  int r, first;
+  if (cu) {
+    if (i >= cu[nact]) return;  // rows past the last active request are padding
+    // request r: the last r with cu[r] <= i
+    int lo = 0, hi = nact;  // cu[lo] <= i < cu[hi]
+    while (hi - lo > 1) {
+      int mid = (lo + hi) >> 1;
+      if (cu[mid] <= i) lo = mid; else hi = mid;
+    }
+    r = lo;
+    first = cu[r];
+    if (i < first) return;
+  } else {  // T / B tokens per request
+    const int per = T / B;
+    r = i / per;
+    first = r * per;
+    if (r >= nact) return;
   }
-  const int r = lo;
-  if (i < cu[r]) return;
-  const int pos = lens[r] + (i - cu[r]);
+  const int pos = lens[r] + (i - first);
   if (pos < 0 || pos / P >= max_pages) return;
   const int page = table[(size_t)r * max_pages + pos / P];
   if (page < 0 || page >= num_pages) return;

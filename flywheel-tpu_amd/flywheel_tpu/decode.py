@@ -50,11 +50,14 @@ def _num_active_tensor(num_active, batch, device):
     return t.reshape(1).to(device=device, dtype=torch.int32)
 
 
-def append_ragged(kv_cache, k, v, cu_seqlens, cache_seqlens, block_table, num_active, nheads_k):
+def append_ragged(kv_cache, k, v, cu_seqlens, cache_seqlens, block_table, num_active, nheads_k,
+                  batch=None):
     """Packed new tokens k, v (total, nheads_k, head_dim) after each active
-    request's cache_seqlens (kernels/kv_append.py:116-184); in place."""
+    request's cache_seqlens (kernels/kv_append.py:116-184); in place.
+    cu_seqlens None: total // batch tokens per request."""
     total, _, head_dim = k.shape
-    batch = cu_seqlens.shape[0] - 1
+    if cu_seqlens is not None:
+        batch = cu_seqlens.shape[0] - 1
     N.check(N.lib().fw_append_ragged(
         N.ptr(kv_cache), N.ptr(k), N.ptr(v), N.ptr(cu_seqlens), N.ptr(cache_seqlens),
         N.ptr(block_table), N.ptr(num_active), batch, total, nheads_k, head_dim,
@@ -363,9 +366,9 @@ def flash_attn_with_kvcache(
     seqlen_add = 0
     k_new = v_new = None
     if has_new and is_folded:
-        cu = torch.arange(batch + 1, dtype=torch.int32, device=device) * seqlen_q
+        # cu_seqlens None: seqlen_q tokens per row
         append_ragged(k_cache, k.reshape(-1, nheads_k, head_dim), v.reshape(-1, nheads_k, head_dim),
-                      cu, row_cache_seqlens, table, num_active_t, nheads_k)
+                      None, row_cache_seqlens, table, num_active_t, nheads_k, batch=batch)
         seqlen_add = seqlen_q
     elif has_new:
         k_new = k.reshape(batch, nheads_k, head_dim)

@@ -107,7 +107,8 @@ int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream);
  * append_ragged / append_kernel (kernels/kv_append.py:116-184, :32-114).
  * k, v (total_tokens, nheads_k, head_dim) in the pool dtype, packed by
  * cu_seqlens (batch + 1); token t of request r < *num_active goes to row
- * cache_seqlens[r] + t - cu_seqlens[r] of its pages.  Bit-exact copy.
+ * cache_seqlens[r] + t - cu_seqlens[r] of its pages.  cu_seqlens NULL means
+ * total_tokens / batch tokens per request (a verify window).  Bit-exact copy.
  */
 int fw_append_ragged(void *kv_cache, const void *k, const void *v,
                      const int32_t *cu_seqlens, const int32_t *cache_seqlens,
