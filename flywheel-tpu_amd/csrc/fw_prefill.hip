@@ -951,8 +951,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
+    const float m_init = m_run == -INFINITY ? 0.f : -m_run;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
+    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = m_init;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
@@ -992,11 +993,13 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // O/l rescale, exponentiate again).
   auto softmax = [&](int t, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
     const int kb = t * kKT;
+    // the scores arrive as s - anchor (the MFMA accumulated onto -anchor)
+    const float m_qk = m_run == -INFINITY ? 0.f : m_run;
     if (a.softcap_log2 != 0.f) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
+        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e] + m_qk) * a.softcap_log2 - m_qk;
     }
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
@@ -1027,7 +1030,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
         pop[u] = __builtin_bit_cast(bf16x8_t, pw);
       }
     };
-    exponentiate(m_run == -INFINITY ? 0.f : m_run);
+    exponentiate(0.f);
     if (__any(!(psum <= kPsumTrigger) || (m_run == -INFINITY && row_has_key))) {
       asm volatile("" ::: "memory");  // a real branch: never if-converted
       float tmax = -INFINITY;
@@ -1035,11 +1038,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
-      tmax = wave_max_xor(tmax, 32);
+      tmax = wave_max_xor(tmax, 32) + m_qk;
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
       m_run = m_new;
-      exponentiate(m_new == -INFINITY ? 0.f : m_new);
+      exponentiate((m_new == -INFINITY ? 0.f : m_new) - m_qk);
       l_run *= alpha;
 #pragma unroll
       for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
