@@ -763,10 +763,20 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 constexpr int kPPWaves = 8;
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
+constexpr int kPPQBytes = 32 * 128 * 2; // one wave's Q^T operands
+
+// 64 lanes x 16 bytes from base + voff[lane] into LDS at lds_addr + 16 * lane
+// (global_load_lds_dwordx4).  Issued from asm so the compiler does not add a
+// wait for it before every later LDS read: the kernel waits for its own
+// copies (s_waitcnt vmcnt) before the barrier that publishes the buffer.
+__device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
+}
 
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf + kPPWaves * kPPQBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -884,8 +894,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     kbase_p = a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kbase * a.kst);
     vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
   }
-  u32x4_t stg[4];
-  auto fetch_tile = [&](int j) __attribute__((always_inline)) {
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)lds;
+  // Tile t goes from global memory straight into LDS buffer t % 3
+  // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
+  // per instruction); this wave moves key rows 8w .. 8w+7.
+  auto dma_tile = [&](int j, const int buf) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
     int key0 = min((t_begin + j) * kKT + 8 * w, kmax);
     const uint8_t *kp, *vp;
@@ -900,89 +913,103 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       vp = vbase_p + (size_t)key0 * vstB;
     }
     const uint32_t lim = (uint32_t)(kmax - key0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t lr = min(lr0 + 4u * i, lim);
-      const uint32_t c16 = c16b ^ (16u * ((2 * w + i) & 3));
-      stg[i] = *(const u32x4_t *)(kp + (__umul24(lr, kstB) + c16));
-      stg[2 + i] = *(const u32x4_t *)(vp + (__umul24(lr, vstB) + c16));
-    }
+    const uint32_t lra = min(lr0, lim), lrb = min(lr0 + 4u, lim);
+    const uint32_t c16a = c16b ^ (16u * ((2 * w) & 3)), c16c = c16b ^ (16u * ((2 * w + 1) & 3));
+    const uint32_t d = lds0 + (uint32_t)(8 * w * kRowB) + (uint32_t)buf * kTileB;
+    lds_dma16(kp, __umul24(lra, kstB) + c16a, d);
+    lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 3 * kTileB);
+    lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
+    lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 3 * kTileB);
   };
   // LDS: K tiles of buffers 0,1,2 then V tiles of buffers 0,1,2, so every
   // operand read is a per-lane base plus an immediate offset below 64 KiB.
-  FW_LDS uint8_t *const lds_base = (FW_LDS uint8_t *)lds;
-  auto store_tile = [&](int j) __attribute__((always_inline)) {
-    const int bi = j % 3;
-    FW_LDS uint8_t *kdst = lds_base + bi * kTileB;
+  // LDS addresses as 32-bit integers: per-lane parts in registers, buffer and
+  // step offsets as constants, so they fold into the instructions' offset field.
+  // This wave's Q^T operands, in operand order (dim step j: 64 lanes x 16 B),
+  // are read back from LDS by the QK steps instead of occupying 32 VGPRs.
+  const uint32_t qofs = lds0 + 3 * kPPBuf + w * kPPQBytes + 16 * lane;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int o = (8 * w + 4 * i) * kRowB + 16 * lane;
-      *(FW_LDS u32x4_t *)(kdst + o) = stg[i];
-      *(FW_LDS u32x4_t *)(kdst + 3 * kTileB + o) = stg[2 + i];
-    }
-  };
+  for (int j = 0; j < 8; ++j) *(FW_LDS bf16x8_t *)(qofs + 1024 * j) = qop[j];
 
-  auto store_tile_after_fetch = [&](int j) {
-    fetch_tile(j);
-    store_tile(j);
-  };
+
+
 
   // ---- LDS operand addressing (per-lane offsets within a buffer).
-  int kofs[8];
+  uint32_t kofs[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) kofs[j] = n * kRowB + 16 * ((2 * j + g) ^ swz(n));
+  for (int j = 0; j < 8; ++j) kofs[j] = lds0 + n * kRowB + 16 * ((2 * j + g) ^ swz(n));
   const int tr_i = lane & 15, tr_G = lane >> 4;
   const int tr_a = tr_i >> 2, tr_b = tr_i & 3, tr_kg = tr_G >> 1;
   const int tr_lo = 2 * (tr_G & 1) + (tr_b >> 1);
-  int vofs[4][2];
+  uint32_t vofs[4][2];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
-      vofs[c][hh] = 3 * kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
+      vofs[c][hh] = lds0 + 3 * kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
                     16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
   f32x16_t sacc[2];
-  bf16x8_t pops[2][4];
+  bf16x8_t pops[4];  // P^T of the last softmax; zero before the first
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pops[u][e] = (__bf16)0.f;
 
-  auto qk = [&](const int bi) __attribute__((always_inline)) {
-    const FW_LDS uint8_t *buf = lds_base + bi * kTileB;
-    bf16x8_t kop0[8], kop1[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
-    const float m_init = m_run == -INFINITY ? 0.f : -m_run;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = m_init;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
-      sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
+  // One MFMA slot as a software pipeline of 32 steps: PV of tile j-1 (steps
+  // 0-15: u = s/4 key group, c = s%4 dim block; two transposing V reads each)
+  // then QK of tile j (steps 16-31: dim step (s-16)/2, key half (s-16)%2; one
+  // K read each).  The operand reads of step s+kPipe are issued right after
+  // the MFMA of step s: a wave that issues a burst of LDS reads between two
+  // MFMAs stalls its own MFMA issue (measured 50-55 cycles per MFMA against
+  // 35-38 when reads and MFMAs alternate).
+  // The operands of the first kPipe PV steps (V of tile j-1, whose buffer is
+  // complete) are read before the barrier that opens the MFMA slot.
+  constexpr int kPipe = 3;
+  bf16x8_t opr[32], qr[8];
+  auto rd = [&](const int st, const uint32_t bufq, const uint32_t bufp) __attribute__((always_inline)) {
+    if (st < 16) {
+      const int u = st >> 2, c = st & 3;
+      const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (FW_LDS v4i16_t *)(vofs[c][0] + bufp + 16 * u * kRowB));
+      const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (FW_LDS v4i16_t *)(vofs[c][1] + bufp + (16 * u + 8) * kRowB));
+      opr[st] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      const int j = (st - 16) >> 1, hh = (st - 16) & 1;
+      if (hh == 0) qr[j] = *(const FW_LDS bf16x8_t *)(qofs + 1024 * j);
+      opr[st] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(kofs[j] + bufq + 32 * kRowB * hh));
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
   };
-
-  auto pv = [&](const int bi, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
-    const FW_LDS uint8_t *buf = lds_base + bi * kTileB;
-    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
+  auto mslot_pre = [&](const int bp) __attribute__((always_inline)) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (FW_LDS v4i16_t *)(buf + vofs[c][0] + 16 * u * kRowB));
-        const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (FW_LDS v4i16_t *)(buf + vofs[c][1] + (16 * u + 8) * kRowB));
-        dst[c] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
+    for (int st = 0; st < kPipe; ++st) rd(st, 0, bp * kTileB);
+  };
+  auto mslot = [&](const int bq, const int bp, const bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
+    const uint32_t bufq = bq * kTileB, bufp = bp * kTileB;
+    const float m_init = m_run == -INFINITY ? 0.f : -m_run;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 32; ++st) {
+      if (st < 16) {
+        const int u = st >> 2, c = st & 3;
+        oacc[c] = mfma32(opr[st], pop[u], oacc[c]);
+      } else if (st < 18) {
+        // both key halves start from the anchor block; the second MFMA
+        // overwrites it in place
+        if (st == 16) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sacc[1][e] = m_init;
+          sacc[0] = mfma32(opr[st], qr[0], sacc[1]);
+        } else {
+          sacc[1] = mfma32(opr[st], qr[0], sacc[1]);
+        }
+      } else {
+        const int j = (st - 16) >> 1, hh = (st - 16) & 1;
+        sacc[hh] = mfma32(opr[st], qr[j], sacc[hh]);
       }
-    };
-    bf16x8_t vop[2][4];
-    read_v(0, vop[0]);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
+      if (st + kPipe < 32) rd(st + kPipe, bufq, bufp);
+      __builtin_amdgcn_sched_barrier(0);  // MFMA, then the reads of step st+kPipe
     }
   };
 
@@ -995,12 +1022,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     const int kb = t * kKT;
     // the scores arrive as s - anchor (the MFMA accumulated onto -anchor)
     const float m_qk = m_run == -INFINITY ? 0.f : m_run;
-    if (a.softcap_log2 != 0.f) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e] + m_qk) * a.softcap_log2 - m_qk;
-    }
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
     bool row_has_key = true;
@@ -1066,38 +1087,70 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // slots earlier) and fetches its rows of tile j+2+grp: group 0 carries key
   // rows 0-31 of each tile, group 1 rows 32-63.
   if (T > 0) {
-    store_tile_after_fetch(0);
-    if (grp == 1 && T > 1) store_tile_after_fetch(1);
-    if (1 + grp < T) fetch_tile(1 + grp);
+    // buffers 1 and 2 start as zeros (read by the spare PV of slot 0 and QK of
+    // slot T before any tile lands there)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t o = lds0 + kTileB + 16u * (tid + 512u * i);
+      *(FW_LDS u32x4_t *)(o) = u32x4_t{0, 0, 0, 0};
+      *(FW_LDS u32x4_t *)(o + 3 * kTileB) = u32x4_t{0, 0, 0, 0};
+    }
+    __syncthreads();
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    // Tile 0 from every wave; group 1 also starts its rows of tile 1 here
+    // (group 0 issues those at the start of its first MFMA slot).
+    dma_tile(0, 0);
+    if (grp == 1 && T > 1) dma_tile(1, 1);
+    if (grp == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     slot_barrier();  // tile 0 complete
     if (grp == 1) slot_barrier();
+    mslot_pre(2);  // the first PV multiplies P = 0 into zeroed buffer 2
     // Unrolled by three so every buffer index is a compile-time constant.
     auto body = [&](const int j, const auto bi, const auto pi) __attribute__((always_inline)) {
+      // The address registers are opaque to the optimiser here, so the
+      // per-buffer constants stay in the LDS instructions' offset fields
+      // instead of being hoisted into one register per buffer and step.
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) asm volatile("" : "+v"(kofs[jj]));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(vofs[c][0]), "+v"(vofs[c][1]));
       constexpr int B = decltype(bi)::value;
       constexpr int P = decltype(pi)::value;
-      if (j < T && wave_needs(j)) qk(B);
-      if (j >= 1 && wave_needs(j - 1)) pv((B + 2) % 3, pops[P ^ 1]);
+      // One code path for every slot (a branchy variant made the compiler
+      // copy all 64 O registers at each join): the PV of slot 0 multiplies
+      // P = 0 into a zeroed buffer, the QK of slot T reads a stale but finite
+      // tile and is never used, and tiles outside a wave's rows are fully
+      // masked by the softmax, so their P is 0.
+      // MFMA slot at raised priority: the other wave of this SIMD is in its
+      // softmax slot and would otherwise win issue whenever it is the older.
+      // Tile t's buffer is free from slot 2t-2 and must be complete at the
+      // end of slot 2t-1: group 0 issues its rows at the start of M(t-1) and
+      // waits at the end of S(t-1); group 1 issues in S(t-2) and waits at the
+      // end of M(t-1).
+      if (grp == 0 && j + 1 < T) dma_tile(j + 1, (B + 1) % 3);
+      __builtin_amdgcn_s_setprio(2);
+      mslot(B, (B + 2) % 3, pops);
+      __builtin_amdgcn_s_setprio(0);
+      if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
-      if (j + 1 + grp < T) store_tile(j + 1 + grp);
-      if (j + 2 + grp < T) fetch_tile(j + 2 + grp);
-      if (j < T && wave_needs(j)) softmax(t_begin + j, pops[P]);
+      if (grp == 1 && j + 2 < T) dma_tile(j + 2, (B + 2) % 3);
+      if (j < T) softmax(t_begin + j, pops);
+      mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
+      if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    for (int j = 0; j <= T; j += 6) {
+    for (int j = 0; j <= T; j += 3) {
       body(j, I0(), I0());
       if (j + 1 > T) break;
-      body(j + 1, I1(), I1());
+      body(j + 1, I1(), I0());
       if (j + 2 > T) break;
       body(j + 2, I2(), I0());
-      if (j + 3 > T) break;
-      body(j + 3, I0(), I1());
-      if (j + 4 > T) break;
-      body(j + 4, I1(), I0());
-      if (j + 5 > T) break;
-      body(j + 5, I2(), I1());
     }
     if (grp == 0) slot_barrier();
   }
