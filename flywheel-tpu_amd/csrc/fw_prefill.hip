@@ -763,7 +763,6 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 constexpr int kPPWaves = 8;
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
-constexpr int kPPQBytes = 32 * 128 * 2; // one wave's Q^T operands
 
 // 64 lanes x 16 bytes from base + voff[lane] into LDS at lds_addr + 16 * lane
 // (global_load_lds_dwordx4).  Issued from asm so the compiler does not add a
@@ -776,7 +775,7 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
 
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf + kPPWaves * kPPQBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -849,24 +848,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   const bool row_ok = qrow < sq_len;
   const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
 
-  // ------------------------------------------------------------ Q^T operand
-  bf16x8_t qop[8];
-  {
-    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
-                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    u32x4_t raw[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
-    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
-      qop[j] = __builtin_bit_cast(bf16x8_t, o);
-    }
-  }
-
   f32x16_t oacc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
@@ -921,15 +902,31 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
     lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 3 * kTileB);
   };
+  // Tile 0's copy goes out before the Q loads so the two latencies overlap.
+  if (T > 0) dma_tile(0, 0);
+
+  // ------------------------------------------------------------ Q^T operand
+  bf16x8_t qop[8];
+  {
+    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
+                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
+    u32x4_t raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
+      qop[j] = __builtin_bit_cast(bf16x8_t, o);
+    }
+  }
+
   // LDS: K tiles of buffers 0,1,2 then V tiles of buffers 0,1,2, so every
   // operand read is a per-lane base plus an immediate offset below 64 KiB.
   // LDS addresses as 32-bit integers: per-lane parts in registers, buffer and
   // step offsets as constants, so they fold into the instructions' offset field.
-  // This wave's Q^T operands, in operand order (dim step j: 64 lanes x 16 B),
-  // are read back from LDS by the QK steps instead of occupying 32 VGPRs.
-  const uint32_t qofs = lds0 + 3 * kPPBuf + w * kPPQBytes + 16 * lane;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) *(FW_LDS bf16x8_t *)(qofs + 1024 * j) = qop[j];
 
 
 
@@ -977,7 +974,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       opr[st] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
     } else {
       const int j = (st - 16) >> 1, hh = (st - 16) & 1;
-      if (hh == 0) qr[j] = *(const FW_LDS bf16x8_t *)(qofs + 1024 * j);
+      if (hh == 0) qr[j] = qop[j];
       opr[st] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(kofs[j] + bufq + 32 * kRowB * hh));
     }
   };
@@ -1101,7 +1098,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     using S2 = std::integral_constant<int, 2>;
     // Tile 0 from every wave; group 1 also starts its rows of tile 1 here
     // (group 0 issues those at the start of its first MFMA slot).
-    dma_tile(0, 0);
     if (grp == 1 && T > 1) dma_tile(1, 1);
     if (grp == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1168,18 +1164,33 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       M = Mn;
     }
   }
-  if (!row_ok) return;
   const bool any = Lsum > 0.f && l_run > 0.f;
   const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
-  uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
+  // O goes out as whole 256-byte rows: each wave stages its 32 rows in its own
+  // 8 KiB of LDS (16-byte chunks XOR-swizzled by row), then every lane stores
+  // 16 contiguous bytes.  All LDS reads of the loop finished at its last
+  // barrier.
+  {
+    const uint32_t wbase = lds0 + (uint32_t)w * 8192u;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
-                          pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
-      *(u32x2_t *)(op + 32 * c + 8 * rr + 4 * g) = wv;
+      for (int rr = 0; rr < 4; ++rr) {
+        const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
+                            pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
+        *(FW_LDS u32x2_t *)(wbase + n * kRowB + 16 * ((4 * c + rr) ^ (n & 15)) + 8 * g) = wv;
+      }
+    const int cc = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      const u32x4_t v = *(const FW_LDS u32x4_t *)(wbase + r * kRowB + 16 * (cc ^ (r & 15)));
+      const int grow = q0 + 32 * w + r;
+      if (grow < sq_len)
+        *(u32x4_t *)(a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + grow) * a.ost + 8 * cc) = v;
     }
+  }
+  if (!row_ok) return;
   if (a.lse && g == 0) {
     a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] =
         Lsum > 0.f ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
