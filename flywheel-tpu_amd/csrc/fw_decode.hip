@@ -442,22 +442,34 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
   const size_t item0 = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit;
   float M = -INFINITY, Lsum = 0.f;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // The loads of up to kBatch splits are issued before any of them is used
+  // (one memory latency per batch instead of one per split).
+  constexpr int kBatch = 8;
   if (valid) {
-#pragma unroll 2
-    for (int s = grp; s < nsp; s += 4) {
-      const float2 ml = a.ws_ml[(item0 + s) * 16 + row];
-      const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
-      const f32x4_t v0 = *(const f32x4_t *)po, v1 = *(const f32x4_t *)(po + 4);
-      if (ml.x == -INFINITY) continue;
-      const float Mn = fmaxf(M, ml.x);
-      const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml.x - Mn);
+    for (int s0 = grp; s0 < nsp; s0 += 4 * kBatch) {
+      float2 ml[kBatch];
+      f32x4_t v0[kBatch], v1[kBatch];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[e] = acc[e] * c_old + v0[e] * c_new;
-        acc[4 + e] = acc[4 + e] * c_old + v1[e] * c_new;
+      for (int i = 0; i < kBatch; ++i) {
+        const int s = min(s0 + 4 * i, nsp - 1);
+        ml[i] = a.ws_ml[(item0 + s) * 16 + row];
+        const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
+        v0[i] = *(const f32x4_t *)po;
+        v1[i] = *(const f32x4_t *)(po + 4);
       }
-      Lsum = Lsum * c_old + ml.y * c_new;
-      M = Mn;
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (s0 + 4 * i >= nsp || ml[i].x == -INFINITY) continue;
+        const float Mn = fmaxf(M, ml[i].x);
+        const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml[i].x - Mn);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] = acc[e] * c_old + v0[i][e] * c_new;
+          acc[4 + e] = acc[4 + e] * c_old + v1[i][e] * c_new;
+        }
+        Lsum = Lsum * c_old + ml[i].y * c_new;
+        M = Mn;
+      }
     }
   }
 #pragma unroll
