@@ -1187,7 +1187,8 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       const u32x4_t v = *(const FW_LDS u32x4_t *)(wbase + r * kRowB + 16 * (cc ^ (r & 15)));
       const int grow = q0 + 32 * w + r;
       if (grow < sq_len)
-        *(u32x4_t *)(a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + grow) * a.ost + 8 * cc) = v;
+        // non-temporal: whole rows that no later launch step re-reads here
+        __builtin_nontemporal_store(v, (u32x4_t *)(a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + grow) * a.ost + 8 * cc));
     }
   }
   if (!row_ok) return;
