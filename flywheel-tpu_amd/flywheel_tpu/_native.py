@@ -65,6 +65,18 @@ class PrefillParams(ctypes.Structure):
     ]
 
 
+class RotaryParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _c_p), ("y", _c_p), ("cos_table", _c_p), ("sin_table", _c_p),
+        ("cu_seqlens", _c_p), ("kv_cu", _c_p), ("kv_lens", _c_p), ("num_active", _c_p),
+        ("x_stride_b", _i64), ("x_stride_h", _i64), ("x_stride_t", _i64),
+        ("y_stride_b", _i64), ("y_stride_h", _i64), ("y_stride_t", _i64),
+        ("batch_rows", _i32), ("nheads", _i32), ("ntokens", _i32), ("head_dim", _i32),
+        ("table_rows", _i32), ("table_f32", _i32), ("interleaved", _i32),
+        ("pos_offset", _i32), ("nseq", _i32),
+    ]
+
+
 # name -> (restype, argtypes); the full exported surface of include/flywheel_hip.h
 SIGNATURES = {
     "fw_last_error": (ctypes.c_char_p, []),
@@ -77,6 +89,7 @@ SIGNATURES = {
                                                _i32, _i32, _i32, _i32, _i32, _c_p]),
     "fw_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(PrefillParams)]),
     "fw_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillParams), _c_p]),
+    "fw_rotary": (ctypes.c_int, [ctypes.POINTER(RotaryParams), _c_p]),
 }
 
 

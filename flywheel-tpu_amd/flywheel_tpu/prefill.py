@@ -24,12 +24,7 @@ from .inputs import (
     resolve_scale,
 )
 from .kv_layout import resolve_merged_kv_heads
-
-_ROTARY_MSG = (
-    "fused RoPE (rotary_cos / rotary_sin) is not implemented on this backend;"
-    " rotate q / k before the call."
-)
-
+from . import rotary as R
 
 def _check_bf16(*ts):
     if not all(t.dtype == torch.bfloat16 for t in ts):
@@ -107,7 +102,7 @@ def flash_attn_func(
     j <= i + seqlen_k - seqlen_q.  Rows with no reachable key return out 0 and
     lse -inf (or the sink).  lse (batch, nheads, seqlen_q) f32.
     """
-    del interpret, rotary_interleaved
+    del interpret
     window_size = check_common_kwargs(
         window_size, dropout_p=dropout_p, softcap=softcap, alibi_slopes=alibi_slopes,
         deterministic=deterministic, return_attn_probs=return_attn_probs)
@@ -121,8 +116,6 @@ def flash_attn_func(
             "heads_outer_fold is a forward-only head-major layout; it supports fused RoPE"
             " only as Q-only rotation (rotary_k=False) and no return_softmax_lse."
         )
-    if has_rotary:
-        raise NotImplementedError(_ROTARY_MSG)
     q, k, v = as_tensor(q), as_tensor(k), as_tensor(v)
     if token_major:
         if head_dim is None:
@@ -165,9 +158,21 @@ def flash_attn_func(
             raise ValueError(f"k / v must match q's batch and head_dim; got {k.shape=}, {v.shape=}.")
     if nheads_k <= 0 or nheads % nheads_k:
         raise ValueError(f"{nheads=} must be a multiple of {nheads_k=}.")
+    tables = R.check_tables(rotary_cos, rotary_sin, head_dim=d, dtype=q.dtype,
+                            rotate_k=rotary_k, interleaved=rotary_interleaved,
+                            kv_len_bound=seqlen_k)
+    if tables is not None and seqlen_q > seqlen_k:
+        raise ValueError("RoPE prefill requires seqlen_q <= seqlen_k.")
     _check_bf16(q, k, v)
     N.require_device(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if tables is not None:
+        # rotary.py:118-120: Q at seqlen_k - seqlen_q + i, K at i.
+        q = R.rotate(q, tables, rotary_interleaved, strides=qs, batch_rows=batch,
+                     nheads=nheads, ntokens=seqlen_q, pos_offset=seqlen_k - seqlen_q)
+        if rotary_k:
+            k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
+                         nheads=nheads_k, ntokens=seqlen_k)
     softmax_scale = resolve_scale(softmax_scale, d)
     sinks = check_sinks(learnable_sink, nheads, q.device)
     out = torch.empty_like(q)
@@ -228,7 +233,7 @@ def flash_attn_varlen_func(
     guard_replay_unroll are accepted for compatibility (tiles are chosen by
     this backend).
     """
-    del interpret, rotary_interleaved
+    del interpret
     window_size = check_common_kwargs(
         window_size, dropout_p=dropout_p, softcap=softcap, alibi_slopes=alibi_slopes,
         deterministic=deterministic, return_attn_probs=return_attn_probs)
@@ -241,8 +246,6 @@ def flash_attn_varlen_func(
             )
         if bs[0] % 128 or bs[1] % 128:
             raise ValueError(f"block_q and block_kv must be multiples of 128; got {bs!r}.")
-    if rotary_cos is not None or rotary_sin is not None:
-        raise NotImplementedError(_ROTARY_MSG)
     for name, bound in (("max_seqlen_q", max_seqlen_q), ("max_seqlen_k", max_seqlen_k)):
         if isinstance(bound, torch.Tensor):
             bound = int(bound)
@@ -275,6 +278,10 @@ def flash_attn_varlen_func(
         if seqused_k is None:
             raise ValueError("block_table needs seqused_k, the (batch,) kv length of each"
                              " sequence (its new tokens included).")
+        if rotary_cos is not None and rotary_k:
+            raise NotImplementedError(
+                "a paged KV cache holds K already rotated; pass rotary_k=False to rotate Q"
+                " only.")
         if q.ndim != 3:
             raise ValueError(f"with block_table, q must be (nheads, total_q, headdim); got"
                              f" {tuple(q.shape)=}.")
@@ -302,17 +309,34 @@ def flash_attn_varlen_func(
             raise ValueError(f"page_size must be a multiple of 16; got {k.shape[1]}.")
         if q.dtype != torch.bfloat16:
             raise NotImplementedError(f"q must be bfloat16; got {q.dtype}.")
+        tables = R.check_tables(rotary_cos, rotary_sin, head_dim=d, dtype=q.dtype,
+                                rotate_k=rotary_k, interleaved=rotary_interleaved,
+                                kv_len_bound=int(max_seqlen_k))
+        if tables is not None and (num_active is None or isinstance(num_active, int)):
+            cu_h, used_h = cu, as_tensor(seqused_k)
+            if isinstance(num_active, int) and not (cu.is_cuda or used_h.is_cuda):
+                # prefill.py:570-577: inactive sequences hold no rows, kv length 0.
+                cu_h = torch.where(torch.arange(batch + 1) <= num_active, cu, cu[num_active])
+                used_h = torch.where(torch.arange(batch) < num_active, used_h, 0)
+            R.check_packed_lengths(cu_h, used_h, tables[0].shape[0])
         N.require_device(q, k)
         device = q.device
         bt = as_tensor(block_table)
         if bt.ndim != 2 or bt.shape[0] != batch or bt.is_floating_point():
             raise ValueError(f"block_table must be (batch={batch}, max_pages) int; got"
                              f" {tuple(bt.shape)} {bt.dtype}.")
+        cu_dev = int32_device(cu, device, "cu_seqlens_q")
+        used_dev = int32_device(seqused_k, device, "seqused_k", (batch,))
+        active = _num_active_tensor(num_active, batch, device)
+        q = q.contiguous()
+        if tables is not None:
+            q = R.rotate(q, tables, rotary_interleaved, strides=(0, total_q * d, d),
+                         batch_rows=1, nheads=nheads, ntokens=total_q, cu=cu_dev,
+                         kv_lens=used_dev, num_active=active)
         out, lse = paged_prefill(
-            q.contiguous(), k, int32_device(cu, device, "cu_seqlens_q"),
-            int32_device(seqused_k, device, "seqused_k", (batch,)),
+            q, k, cu_dev, used_dev,
             bt.to(device=device, dtype=torch.int32).contiguous(),
-            _num_active_tensor(num_active, batch, device),
+            active,
             check_sinks(learnable_sink, nheads, device),
             nheads_k=nkv, softmax_scale=resolve_scale(softmax_scale, d), softcap=float(softcap),
             causal=causal, window_size=window_size,
@@ -356,10 +380,24 @@ def flash_attn_varlen_func(
         raise ValueError(f"v must match k's shape; got {k.shape=}, {v.shape=}.")
     if nkv <= 0 or nheads % nkv:
         raise ValueError(f"{nheads=} must be a multiple of nheads_k={nkv}.")
+    tables = R.check_tables(rotary_cos, rotary_sin, head_dim=d, dtype=q.dtype,
+                            rotate_k=rotary_k, interleaved=rotary_interleaved,
+                            kv_len_bound=int(max_seqlen_k))
+    if tables is not None:
+        R.check_packed_lengths(cu_q, torch.diff(cu_k.to(torch.int64)), tables[0].shape[0])
     _check_bf16(q, k, v)
     N.require_device(q, k, v)
     device = q.device
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    cu_q_dev = int32_device(cu_q, device, "cu_seqlens_q")
+    cu_k_dev = int32_device(cu_k, device, "cu_seqlens_k")
+    if tables is not None:
+        # rotary.py:148-156: Q at len_k - len_q + local, K at local.
+        q = R.rotate(q, tables, rotary_interleaved, strides=qs,
+                     batch_rows=1, nheads=nheads, ntokens=total_q, cu=cu_q_dev, kv_cu=cu_k_dev)
+        if rotary_k:
+            k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=1,
+                         nheads=nkv, ntokens=total_k, cu=cu_k_dev)
     out = torch.empty_like(q)
     lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
            if return_softmax_lse else None)
@@ -368,8 +406,7 @@ def flash_attn_varlen_func(
                  seqlen_q=total_q, seqlen_k=total_k, causal=causal, window_size=window_size,
                  softmax_scale=resolve_scale(softmax_scale, d), softcap=softcap,
                  sinks=check_sinks(learnable_sink, nheads, device),
-                 cu_q=int32_device(cu_q, device, "cu_seqlens_q"),
-                 cu_k=int32_device(cu_k, device, "cu_seqlens_k"),
+                 cu_q=cu_q_dev, cu_k=cu_k_dev,
                  max_seqlen_q=int(max_seqlen_q))
     if return_softmax_lse:
         return out, lse

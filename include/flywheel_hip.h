@@ -184,6 +184,49 @@ typedef struct fw_prefill_params {
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);
 int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
 
+/*
+ * RoPE on bf16 rows at their prefill positions, in f32 with one rounding to
+ * bf16.  Replaces the reference's fused rotation of staged Q / K tiles:
+ * prepare_rotary (softmax_attention/rotary.py:27-167: positions and the packed
+ * cos/sin plane) and rotate_tile (rotary.py:170-215), applied by
+ * fwd_blocks.rotate_staged / rotate_gqa_folded_q (fwd_blocks.py:260-303).
+ * Element (b, h, t, d) of x is at x + b*x_stride_b + h*x_stride_h +
+ * t*x_stride_t + d (elements), likewise y; y may alias x.
+ * cos, sin   (table_rows, head_dim / 2), bf16 or f32 (table_f32).
+ * interleaved = 0 pairs dims (i, i + head_dim/2) with table column i;
+ * interleaved = 1 pairs dims (2i, 2i+1) with column i.
+ * Position of token t: dense (cu_seqlens NULL): t + pos_offset.  Packed
+ * (cu_seqlens, batch + 1 boundaries): t - cu_seqlens[s] + base(s) for the
+ * sequence s holding t, where base(s) = kv_len(s) - q_len(s) when kv_lens
+ * (batch, e.g. seqused_k) or kv_cu (batch + 1, cu_seqlens_k) is given, else 0;
+ * tokens past cu_seqlens[batch] (or cu_seqlens[*num_active] when num_active
+ * is given, prefill.py:570-577) use position 0.  Positions are clamped to
+ * [0, table_rows - 1] (the API layer checks the lengths first).
+ */
+typedef struct fw_rotary_params {
+  const void *x;
+  void *y;
+  const void *cos_table;
+  const void *sin_table;
+  const int32_t *cu_seqlens;
+  const int32_t *kv_cu;
+  const int32_t *kv_lens;
+  const int32_t *num_active; /* optional (1,): sequences >= it hold no rows */
+  int64_t x_stride_b, x_stride_h, x_stride_t;
+  int64_t y_stride_b, y_stride_h, y_stride_t;
+  int32_t batch_rows;   /* size of the b index (1 for packed layouts) */
+  int32_t nheads;
+  int32_t ntokens;
+  int32_t head_dim;     /* 128 */
+  int32_t table_rows;
+  int32_t table_f32;
+  int32_t interleaved;
+  int32_t pos_offset;
+  int32_t nseq;         /* batch of cu_seqlens (packed) */
+} fw_rotary_params;
+
+int fw_rotary(const fw_rotary_params *p, fw_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

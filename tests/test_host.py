@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts_match_header_fields():
     text = open(HEADER).read()
-    for struct, cls in (("fw_decode_params", N.DecodeParams), ("fw_prefill_params", N.PrefillParams)):
+    for struct, cls in (("fw_decode_params", N.DecodeParams), ("fw_prefill_params", N.PrefillParams),
+                        ("fw_rotary_params", N.RotaryParams)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         fields = []
@@ -75,6 +76,11 @@ def test_capi_validation_status_codes():
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED  # fp8 only for a paged pool
     assert lib.fw_append_ragged(None, None, None, None, None, None, None, 1, 0, 2, 128, 16, 1, 1,
                                 7, None) == N.FW_ERR_NOT_IMPLEMENTED
+    r = N.RotaryParams()
+    r.head_dim, r.table_rows = 64, 8
+    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED
+    r.head_dim = 128
+    assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
 
 
 def bf(*shape):
@@ -107,6 +113,52 @@ def test_flash_attn_func_errors():
         flash_attn_func(q, k, k, heads_outer_fold=1)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         flash_attn_func(q, k, k, causal=True)
+
+
+def test_rotary_argument_errors():
+    """rotary.py:56-97, 113-114; prefill.py:480-485 (paged K arrives rotated)."""
+    q, k = bf(1, 4, 8, 128), bf(1, 2, 16, 128)
+    tab = torch.zeros(16, 64)
+    with pytest.raises(ValueError, match="together"):
+        flash_attn_func(q, k, k, rotary_cos=tab)
+    with pytest.raises(ValueError, match="rotary_k=False needs"):
+        flash_attn_func(q, k, k, rotary_k=False)
+    with pytest.raises(ValueError, match="static bool"):
+        flash_attn_func(q, k, k, rotary_cos=tab, rotary_sin=tab, rotary_interleaved=1)
+    with pytest.raises(ValueError, match="partial rotary"):
+        flash_attn_func(q, k, k, rotary_cos=tab[:, :32], rotary_sin=tab[:, :32])
+    with pytest.raises(ValueError, match="divisible by 16"):
+        flash_attn_func(q, k, k, rotary_cos=tab[:, :4], rotary_sin=tab[:, :4])
+    with pytest.raises(ValueError, match="dtype"):
+        flash_attn_func(q, k, k, rotary_cos=tab.double(), rotary_sin=tab.double())
+    with pytest.raises(ValueError, match="shorter"):
+        flash_attn_func(q, k, k, rotary_cos=tab[:15], rotary_sin=tab[:15])
+    with pytest.raises(ValueError, match="seqlen_q <= seqlen_k"):
+        flash_attn_func(bf(1, 4, 20, 128), k, k, rotary_cos=tab, rotary_sin=tab)
+    with pytest.raises(NotImplementedError, match="heads_outer_fold"):
+        flash_attn_func(bf(4, 1, 8, 128), bf(2, 1, 16, 128), bf(2, 1, 16, 128),
+                        heads_outer_fold=True, rotary_cos=tab, rotary_sin=tab)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_func(q, k, k, rotary_cos=tab, rotary_sin=tab.to(torch.float32))
+    qp, kp = bf(4, 10, 128), bf(2, 10, 128)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    with pytest.raises(ValueError, match="len_q <= len_k"):  # second sequence: 6 q rows, 2 keys
+        flash_attn_varlen_func(qp, kp, kp, cu, torch.tensor([0, 8, 10], dtype=torch.int32), 6, 8,
+                               rotary_cos=tab, rotary_sin=tab)
+    with pytest.raises(ValueError, match="shorter"):
+        flash_attn_varlen_func(qp, kp, kp, cu, cu, 6, 17, rotary_cos=tab, rotary_sin=tab)
+    pool, table = bf(8, 16, 4, 128), torch.zeros(2, 4, dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match="rotary_k=False"):
+        flash_attn_varlen_func(qp, pool, None, cu, None, 6, 16, block_table=table,
+                               seqused_k=torch.tensor([4, 6]), rotary_cos=tab, rotary_sin=tab)
+    with pytest.raises(ValueError, match="len_q <= len_k"):
+        flash_attn_varlen_func(qp, pool, None, cu, None, 6, 16, block_table=table,
+                               seqused_k=torch.tensor([4, 5]), rotary_cos=tab, rotary_sin=tab,
+                               rotary_k=False)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attn_varlen_func(qp, pool, None, cu, None, 6, 16, block_table=table,
+                               seqused_k=torch.tensor([4, 6]), rotary_cos=tab, rotary_sin=tab,
+                               rotary_k=False, num_active=1)
 
 
 def test_flash_attn_varlen_func_errors():
