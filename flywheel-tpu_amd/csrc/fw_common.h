@@ -42,6 +42,19 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Columns i .. i + 3 (i a multiple of 4) of a RoPE table held as f32 or bf16,
+// one vector load.
+template <bool F32>
+__device__ __forceinline__ void rope_load4(const void *t, size_t i, float (&v)[4]) {
+  if constexpr (F32) {
+    const f32x4_t x = *(const f32x4_t *)((const float *)t + i);
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+  } else {
+    const u32x2_t x = *(const u32x2_t *)((const uint16_t *)t + i);
+    v[0] = bf16_lo(x[0]); v[1] = bf16_hi(x[0]); v[2] = bf16_lo(x[1]); v[3] = bf16_hi(x[1]);
+  }
+}
+
 __device__ __forceinline__ uint16_t to_bf16(float a) {
   __bf16 r = (__bf16)a;
   return __builtin_bit_cast(uint16_t, r);

@@ -45,7 +45,72 @@ struct PrefillArgs {
   int B, H, Hk, G, Sq, Sk, n_qt, P, max_pages, num_pages, CH;
   int causal, wl, wr;
   float qscale, softcap_log2, v_descale;
+  const void *rcos, *rsin;  // fused Q RoPE tables, or null
+  int rrows, rf32, ril;
 };
+
+// RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7, at table
+// row tb / 64, in f32 with one rounding to bf16 (rotary.py:170-215).  Both
+// partners of every pair are in the lane: dims d and d + 64 are words j and
+// j + 4 (halves), dims 2i and 2i + 1 one packed word (interleaved).
+template <bool F32>
+__device__ __forceinline__ void rope_q_words(const PrefillArgs &a, size_t tb, int g,
+                                             u32x4_t (&raw)[8]) {
+#pragma clang fp contract(off)
+  if (!a.ril) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float c[4], sn[4];
+        rope_load4<F32>(a.rcos, tb + 16 * j + 8 * g + 4 * hf, c);
+        rope_load4<F32>(a.rsin, tb + 16 * j + 8 * g + 4 * hf, sn);
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const int e = 2 * hf + e2;
+          const float ca = c[2 * e2], cb = c[2 * e2 + 1], sa = sn[2 * e2], sb = sn[2 * e2 + 1];
+          const float la = bf16_lo(raw[j][e]), lb = bf16_hi(raw[j][e]);
+          const float ha = bf16_lo(raw[j + 4][e]), hb = bf16_hi(raw[j + 4][e]);
+          raw[j][e] = pack_bf16(la * ca - ha * sa, lb * cb - hb * sb);
+          raw[j + 4][e] = pack_bf16(ha * ca + la * sa, hb * cb + lb * sb);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float c[4], sn[4];
+      rope_load4<F32>(a.rcos, tb + 8 * j + 4 * g, c);
+      rope_load4<F32>(a.rsin, tb + 8 * j + 4 * g, sn);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_lo(raw[j][e]), x1 = bf16_hi(raw[j][e]);
+        raw[j][e] = pack_bf16(x0 * c[e] - x1 * sn[e], x1 * c[e] + x0 * sn[e]);
+      }
+    }
+  }
+}
+
+// One lane's Q^T operand: dims 16j + 8g .. 16j + 8g + 7 (j = 0..7) of the row
+// at qp, rotated at position pos when RoPE tables are given, then scaled by qs
+// and rounded to bf16.
+__device__ __forceinline__ void load_q_operand(const PrefillArgs &a, const uint16_t *qp, int g,
+                                               float qs, int pos, bf16x8_t (&qop)[8]) {
+  u32x4_t raw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+  if (a.rcos) {
+    const size_t tb = (size_t)min(max(pos, 0), a.rrows - 1) * 64;
+    if (a.rf32) rope_q_words<true>(a, tb, g, raw);
+    else rope_q_words<false>(a, tb, g, raw);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
+    qop[j] = __builtin_bit_cast(bf16x8_t, o);
+  }
+}
 
 // 8 bf16 of one K/V row (dims 8c .. 8c+7).
 template <int KV>
@@ -175,17 +240,8 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    u32x4_t raw[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
     const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
-      qop[j] = __builtin_bit_cast(bf16x8_t, o);
-    }
+    load_q_operand(a, qp, g, qs, qrow + off, qop);
   }
 
   f32x16_t oacc[4];
@@ -471,17 +527,8 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    u32x4_t raw[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
     const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
-      qop[j] = __builtin_bit_cast(bf16x8_t, o);
-    }
+    load_q_operand(a, qp, g, qs, qrow + off, qop);
   }
 
   f32x16_t oacc[4];
@@ -910,17 +957,8 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    u32x4_t raw[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
     const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
-      qop[j] = __builtin_bit_cast(bf16x8_t, o);
-    }
+    load_q_operand(a, qp, g, qs, qrow + off, qop);
   }
 
   // LDS: K tiles of buffers 0,1,2 then V tiles of buffers 0,1,2, so every
@@ -1329,6 +1367,13 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.qscale = p->softcap > 0.f ? sm / p->softcap : sm * kLog2e;
   a.softcap_log2 = p->softcap > 0.f ? p->softcap * kLog2e : 0.f;
   a.v_descale = p->v_descale;
+  a.rcos = p->rotary_cos;
+  a.rsin = p->rotary_sin;
+  a.rrows = p->rotary_rows;
+  a.rf32 = p->rotary_f32 ? 1 : 0;
+  a.ril = p->rotary_interleaved ? 1 : 0;
+  FW_REQUIRE(!p->rotary_cos || (p->rotary_sin && p->rotary_rows > 0), FW_ERR_VALUE,
+             "rotary_cos needs rotary_sin and rotary_rows > 0");
   hipStream_t s = (hipStream_t)stream;
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,

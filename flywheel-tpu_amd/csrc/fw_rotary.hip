@@ -22,10 +22,6 @@ struct RotaryArgs {
   int rows_b, H, T, table_rows, table_f32, interleaved, pos_offset, nseq;
 };
 
-__device__ __forceinline__ float table_at(const void *t, int f32, size_t i) {
-  return f32 ? ((const float *)t)[i] : bf16_lo(((const uint16_t *)t)[i]);
-}
-
 __device__ __forceinline__ int token_position(const RotaryArgs &a, int t) {
   if (!a.cu) return t + a.pos_offset;
   const int nseq = a.num_active ? min(max(*a.num_active, 0), a.nseq) : a.nseq;
@@ -44,17 +40,52 @@ __device__ __forceinline__ int token_position(const RotaryArgs &a, int t) {
   return local + base;
 }
 
+// Thread i's two 8-dim chunks (dims 8i.. and 64 + 8i..) rotated at table row
+// tb / 64.
+template <bool F32>
+__device__ __forceinline__ void rope_rows(const RotaryArgs &a, size_t tb, int i, const float (&xl)[8],
+                                          const float (&xh)[8], float (&yl)[8], float (&yh)[8]) {
+  if (!a.interleaved) {  // pair (d, d + 64) with column d
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      float c[4], s[4];
+      rope_load4<F32>(a.cosv, tb + 8 * i + 4 * hf, c);
+      rope_load4<F32>(a.sinv, tb + 8 * i + 4 * hf, s);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 4 * hf + e;
+        yl[d] = xl[d] * c[e] - xh[d] * s[e];
+        yh[d] = xh[d] * c[e] + xl[d] * s[e];
+      }
+    }
+  } else {  // pairs (2j, 2j+1) with column j, in both 8-dim chunks
+    float c0[4], s0[4], c1[4], s1[4];
+    rope_load4<F32>(a.cosv, tb + 4 * i, c0);
+    rope_load4<F32>(a.sinv, tb + 4 * i, s0);
+    rope_load4<F32>(a.cosv, tb + 32 + 4 * i, c1);
+    rope_load4<F32>(a.sinv, tb + 32 + 4 * i, s1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      yl[2 * e] = xl[2 * e] * c0[e] - xl[2 * e + 1] * s0[e];
+      yl[2 * e + 1] = xl[2 * e + 1] * c0[e] + xl[2 * e] * s0[e];
+      yh[2 * e] = xh[2 * e] * c1[e] - xh[2 * e + 1] * s1[e];
+      yh[2 * e + 1] = xh[2 * e + 1] * c1[e] + xh[2 * e] * s1[e];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
-  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-  const long row = gid >> 3;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t row = gid >> 3;
   const int i = gid & 7;
-  if (row >= (long)a.rows_b * a.H * a.T) return;
-  const int t = row % a.T;
-  const int h = (row / a.T) % a.H;
-  const int b = row / ((long)a.T * a.H);
+  if (row >= (uint32_t)a.rows_b * a.H * a.T) return;
+  const uint32_t bh = row / (uint32_t)a.T;
+  const int t = row - bh * a.T;
+  const int b = bh / (uint32_t)a.H;
+  const int h = bh - (uint32_t)b * a.H;
   const int pos = min(max(token_position(a, t), 0), a.table_rows - 1);
-  const uint16_t *xr = a.x + b * a.xsb + h * a.xsh + (size_t)t * a.xst;
-  uint16_t *yr = a.y + b * a.ysb + h * a.ysh + (size_t)t * a.yst;
+  const uint16_t *xr = a.x + (size_t)b * a.xsb + (size_t)h * a.xsh + (size_t)t * a.xst;
+  uint16_t *yr = a.y + (size_t)b * a.ysb + (size_t)h * a.ysh + (size_t)t * a.yst;
   const u32x4_t lo = *(const u32x4_t *)(xr + 8 * i), hi = *(const u32x4_t *)(xr + 64 + 8 * i);
   float xl[8], xh[8];
 #pragma unroll
@@ -64,27 +95,8 @@ __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
   }
   const size_t tb = (size_t)pos * 64;  // table row (head_dim / 2 columns)
   float yl[8], yh[8];
-  if (!a.interleaved) {  // pair (d, d + 64) with column d
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float c = table_at(a.cosv, a.table_f32, tb + 8 * i + e);
-      const float s = table_at(a.sinv, a.table_f32, tb + 8 * i + e);
-      yl[e] = xl[e] * c - xh[e] * s;
-      yh[e] = xh[e] * c + xl[e] * s;
-    }
-  } else {  // pairs (2j, 2j+1) with column j, in both 8-dim chunks
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float c0 = table_at(a.cosv, a.table_f32, tb + 4 * i + e);
-      const float s0 = table_at(a.sinv, a.table_f32, tb + 4 * i + e);
-      const float c1 = table_at(a.cosv, a.table_f32, tb + 32 + 4 * i + e);
-      const float s1 = table_at(a.sinv, a.table_f32, tb + 32 + 4 * i + e);
-      yl[2 * e] = xl[2 * e] * c0 - xl[2 * e + 1] * s0;
-      yl[2 * e + 1] = xl[2 * e + 1] * c0 + xl[2 * e] * s0;
-      yh[2 * e] = xh[2 * e] * c1 - xh[2 * e + 1] * s1;
-      yh[2 * e + 1] = xh[2 * e + 1] * c1 + xh[2 * e] * s1;
-    }
-  }
+  if (a.table_f32) rope_rows<true>(a, tb, i, xl, xh, yl, yh);
+  else rope_rows<false>(a, tb, i, xl, xh, yl, yh);
   u32x4_t ol, oh;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -128,6 +140,7 @@ extern "C" int fw_rotary(const fw_rotary_params *p, fw_stream_t stream) {
   a.nseq = p->nseq;
   const long threads = (long)a.rows_b * a.H * a.T * 8;
   if (threads == 0) return FW_OK;
+  FW_REQUIRE(threads < (1l << 32), FW_ERR_VALUE, "%ld rows exceed one launch", threads / 8);
   fw_rotary_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
   return check_launch("fw_rotary_kernel");
 }

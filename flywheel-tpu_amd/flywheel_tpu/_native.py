@@ -62,6 +62,8 @@ class PrefillParams(ctypes.Structure):
         ("softmax_scale", _f32), ("softcap", _f32),
         ("causal", _i32), ("window_left", _i32), ("window_right", _i32),
         ("k_descale", _f32), ("v_descale", _f32),
+        ("rotary_cos", _c_p), ("rotary_sin", _c_p),
+        ("rotary_rows", _i32), ("rotary_f32", _i32), ("rotary_interleaved", _i32),
     ]
 
 

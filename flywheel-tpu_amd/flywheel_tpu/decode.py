@@ -20,6 +20,7 @@ implementation only:
 import torch
 
 from . import _native as N
+from . import rotary as R
 from .inputs import (
     as_tensor,
     check_common_kwargs,
@@ -102,11 +103,12 @@ def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_acti
 
 def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active, sinks, *,
                   nheads_k, softmax_scale, softcap, causal, window_size, k_descale, v_descale,
-                  max_seqlen_q, return_lse, token_major_q):
+                  max_seqlen_q, return_lse, token_major_q, q_rotary=None):
     """The paged varlen forward (kernels/fwd_paged.py:1351-1491).
 
     q is (total_q, nheads, D) when token_major_q, else head-major
-    (nheads, total_q, D); out has q's layout; lse is (nheads, total_q)."""
+    (nheads, total_q, D); out has q's layout; lse is (nheads, total_q).
+    q_rotary: None or (tables, interleaved) for the fused Q RoPE."""
     if token_major_q:
         total_q, nheads, head_dim = q.shape
         qs_h, qs_t = head_dim, nheads * head_dim
@@ -132,11 +134,13 @@ def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active,
     p.softmax_scale, p.softcap = softmax_scale, softcap
     p.causal, p.window_left, p.window_right = int(causal), left, right
     p.k_descale, p.v_descale = k_descale, v_descale
+    keep = None if q_rotary is None else R.set_q_rotary(p, *q_rotary, q.device)
     lib = N.lib()
     nbytes = lib.fw_prefill_workspace_bytes(p)
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = N.ptr(ws), ws.numel()
     N.check(lib.fw_prefill(p, N.stream_of(q)))
+    del keep
     return out, lse
 
 

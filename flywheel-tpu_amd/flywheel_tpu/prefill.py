@@ -42,7 +42,7 @@ def _split_token_major(x, head_dim):
 
 def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads, nheads_k,
                  head_dim, seqlen_q, seqlen_k, causal, window_size, softmax_scale, softcap,
-                 sinks, cu_q=None, cu_k=None, max_seqlen_q=0):
+                 sinks, cu_q=None, cu_k=None, max_seqlen_q=0, q_rotary=None):
     left, right = effective_window(causal, window_size)
     p = N.PrefillParams()
     p.kv_mode = mode
@@ -59,6 +59,7 @@ def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads,
     p.softmax_scale, p.softcap = softmax_scale, float(softcap)
     p.causal, p.window_left, p.window_right = int(causal), left, right
     p.k_descale, p.v_descale = 1.0, 1.0
+    keep = None if q_rotary is None else R.set_q_rotary(p, *q_rotary, q.device)
     lib = N.lib()
     nbytes = lib.fw_prefill_workspace_bytes(p)
     ws = None
@@ -66,6 +67,7 @@ def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads,
         ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         p.workspace, p.workspace_bytes = N.ptr(ws), nbytes
     N.check(lib.fw_prefill(p, N.stream_of(q)))
+    del keep
 
 
 def flash_attn_func(
@@ -166,13 +168,11 @@ def flash_attn_func(
     _check_bf16(q, k, v)
     N.require_device(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    if tables is not None:
-        # rotary.py:118-120: Q at seqlen_k - seqlen_q + i, K at i.
-        q = R.rotate(q, tables, rotary_interleaved, strides=qs, batch_rows=batch,
-                     nheads=nheads, ntokens=seqlen_q, pos_offset=seqlen_k - seqlen_q)
-        if rotary_k:
-            k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
-                         nheads=nheads_k, ntokens=seqlen_k)
+    if tables is not None and rotary_k:
+        # rotary.py:118-120: K at i; Q (at seqlen_k - seqlen_q + i) is rotated
+        # by the kernel as it loads it.
+        k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
+                     nheads=nheads_k, ntokens=seqlen_k)
     softmax_scale = resolve_scale(softmax_scale, d)
     sinks = check_sinks(learnable_sink, nheads, q.device)
     out = torch.empty_like(q)
@@ -182,7 +182,8 @@ def flash_attn_func(
                  ls=(nheads * seqlen_q, seqlen_q), batch=batch, nheads=nheads,
                  nheads_k=nheads_k, head_dim=d, seqlen_q=seqlen_q, seqlen_k=seqlen_k,
                  causal=causal, window_size=window_size, softmax_scale=softmax_scale,
-                 softcap=softcap, sinks=sinks)
+                 softcap=softcap, sinks=sinks,
+                 q_rotary=None if tables is None else (tables, rotary_interleaved))
     if return_softmax_lse:
         return out, lse
     return out
@@ -329,10 +330,6 @@ def flash_attn_varlen_func(
         used_dev = int32_device(seqused_k, device, "seqused_k", (batch,))
         active = _num_active_tensor(num_active, batch, device)
         q = q.contiguous()
-        if tables is not None:
-            q = R.rotate(q, tables, rotary_interleaved, strides=(0, total_q * d, d),
-                         batch_rows=1, nheads=nheads, ntokens=total_q, cu=cu_dev,
-                         kv_lens=used_dev, num_active=active)
         out, lse = paged_prefill(
             q, k, cu_dev, used_dev,
             bt.to(device=device, dtype=torch.int32).contiguous(),
@@ -342,7 +339,8 @@ def flash_attn_varlen_func(
             causal=causal, window_size=window_size,
             k_descale=descale_scalar(k_descale, "k_descale"),
             v_descale=descale_scalar(v_descale, "v_descale"),
-            max_seqlen_q=int(max_seqlen_q), return_lse=return_softmax_lse, token_major_q=False)
+            max_seqlen_q=int(max_seqlen_q), return_lse=return_softmax_lse, token_major_q=False,
+            q_rotary=None if tables is None else (tables, rotary_interleaved))
         return (out, lse) if return_softmax_lse else out
     if seqused_k is not None or num_active is not None:
         raise ValueError("seqused_k and num_active describe a paged KV cache and need"
@@ -391,13 +389,11 @@ def flash_attn_varlen_func(
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     cu_q_dev = int32_device(cu_q, device, "cu_seqlens_q")
     cu_k_dev = int32_device(cu_k, device, "cu_seqlens_k")
-    if tables is not None:
-        # rotary.py:148-156: Q at len_k - len_q + local, K at local.
-        q = R.rotate(q, tables, rotary_interleaved, strides=qs,
-                     batch_rows=1, nheads=nheads, ntokens=total_q, cu=cu_q_dev, kv_cu=cu_k_dev)
-        if rotary_k:
-            k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=1,
-                         nheads=nkv, ntokens=total_k, cu=cu_k_dev)
+    if tables is not None and rotary_k:
+        # rotary.py:148-156: K at local; Q (at len_k - len_q + local) is rotated
+        # by the kernel as it loads it.
+        k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=1,
+                     nheads=nkv, ntokens=total_k, cu=cu_k_dev)
     out = torch.empty_like(q)
     lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
            if return_softmax_lse else None)
@@ -407,7 +403,8 @@ def flash_attn_varlen_func(
                  softmax_scale=resolve_scale(softmax_scale, d), softcap=softcap,
                  sinks=check_sinks(learnable_sink, nheads, device),
                  cu_q=cu_q_dev, cu_k=cu_k_dev,
-                 max_seqlen_q=int(max_seqlen_q))
+                 max_seqlen_q=int(max_seqlen_q),
+                 q_rotary=None if tables is None else (tables, rotary_interleaved))
     if return_softmax_lse:
         return out, lse
     return out

@@ -4,9 +4,10 @@ Restates the reference's prepare_rotary contract
 (flywheel_tpu/softmax_attention/rotary.py:27-167) and the rotation of
 rotate_tile (rotary.py:170-215): tables (seqlen_ro, head_dim / 2) in q's dtype
 or float32, full-head rotation only, f32 arithmetic rounded once to bf16, K at
-positions 0..len_k-1 and Q at len_k-len_q..len_k-1 of each sequence.  The
-rotated rows go to a fresh buffer on the device (fw_rotary) which the attention
-kernel then reads; q and k themselves are never modified.
+positions 0..len_k-1 and Q at len_k-len_q..len_k-1 of each sequence.  Q is
+rotated by the prefill kernels as they load it (the fused path); K, when it is
+rotated, goes to a fresh buffer (fw_rotary) which the kernel then reads.  q and
+k themselves are never modified.
 """
 
 import torch
@@ -55,6 +56,21 @@ def check_packed_lengths(cu_q, k_lens, table_rows):
     k_lens = k_lens.to(torch.int64)
     if not bool(((q_lens >= 0) & (k_lens >= q_lens) & (k_lens <= table_rows)).all()):
         raise ValueError("RoPE requires 0 <= len_q <= len_k <= rotary table length.")
+
+
+def set_q_rotary(p, tables, interleaved, device):
+    """Fills the fused Q-RoPE fields of a PrefillParams (the prefill kernels
+    rotate Q as they load it, at position i + kv_len - q_len of each row).
+    Returns the device tables, to be kept alive until the launch is queued."""
+    if tables is None:
+        return None
+    cos = tables[0].to(device).contiguous()
+    sin = tables[1].to(device).contiguous()
+    p.rotary_cos, p.rotary_sin = N.ptr(cos), N.ptr(sin)
+    p.rotary_rows = cos.shape[0]
+    p.rotary_f32 = int(cos.dtype == torch.float32)
+    p.rotary_interleaved = int(interleaved)
+    return cos, sin
 
 
 def rotate(x, tables, interleaved, *, strides, batch_rows, nheads, ntokens, pos_offset=0,

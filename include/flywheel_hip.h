@@ -44,7 +44,7 @@ enum fw_dtype {
 
 /* The last error message of the calling thread ("" if none). */
 const char *fw_last_error(void);
-/* ABI version of this header: 2. */
+/* ABI version of this header: 3. */
 int fw_abi_version(void);
 
 /*
@@ -179,6 +179,14 @@ typedef struct fw_prefill_params {
   float softmax_scale, softcap;
   int32_t causal, window_left, window_right;
   float k_descale, v_descale;
+  /* Fused Q RoPE (rotary.py:170-215 applied to Q, prefill.py:150-160), or
+   * rotary_cos NULL for none: tables (rotary_rows, head_dim / 2), f32 when
+   * rotary_f32 else bf16; query row i of a sequence sits at position
+   * i + kv_len - q_len.  Q is rotated in f32 and rounded to bf16 before its
+   * scaling, as a separately rotated Q would be.  K is not rotated here. */
+  const void *rotary_cos;
+  const void *rotary_sin;
+  int32_t rotary_rows, rotary_f32, rotary_interleaved;
 } fw_prefill_params;
 
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);
