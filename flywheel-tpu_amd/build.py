@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "flywheel_tpu", "lib")
 LIB = os.path.join(OUT_DIR, "libflywheel_hip.so")
-SOURCES = ["fw_cache.hip", "fw_decode.hip", "fw_prefill.hip", "fw_rotary.hip"]
+SOURCES = ["fw_cache.hip", "fw_decode.hip", "fw_prefill.hip", "fw_rotary.hip", "fw_backward.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",

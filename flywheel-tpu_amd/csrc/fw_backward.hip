@@ -1,0 +1,575 @@
+// Dense flash-attention backward on gfx950 MFMA (bf16 in, f32 accumulate).
+//
+// The reference's flash_attn_bwd (flywheel_tpu/softmax_attention/kernels/
+// bwd.py:463-840, bwd_pipeline.py:401-570) recomputes, per (q tile, kv tile):
+//   p  = exp2(q_s k^T - lse_log2)    q_s = bf16(q * scale * log2 e), the
+//                                    forward's rounded scaled q
+//   dp = dout v^T,  ds = p (dp - delta),  delta = rowsum(dout * out)
+//   dv += p^T dout,  dk += scale ds^T q,  dq += scale ds k
+// Here that work is split into three launches, all deterministic:
+//   fw_bwd_prep_kernel   lse_log2 and delta per query row (bwd.py:685-720)
+//   fw_bwd_dkv_kernel    one workgroup per 128 keys of one KV head (and one
+//                        chunk of its query heads); K and V live in registers,
+//                        q tiles stream through LDS; dk, dv in registers
+//   fw_bwd_dq_kernel     one workgroup per 128 query rows of one head; q and
+//                        dout live in registers, kv tiles stream through LDS
+//   fw_bwd_reduce_kernel sums the per-chunk dk / dv partials when a KV head's
+//                        query heads were split over workgroups
+// Every product is a 32x32x16 bf16 MFMA whose lane index is the row that owns
+// the accumulator (keys in the dk/dv kernel, query rows in the dq kernel), so
+// the softmax statistics of a lane are per-lane values and P / dS feed the
+// next MFMA straight from the accumulator registers (the reduction index of
+// that MFMA is permuted to match, and its LDS operand is read in the same
+// permuted order from a transposed copy).
+#include "fw_common.h"
+
+namespace fw {
+
+namespace {
+
+constexpr int kBT = 64;     // rows per streamed tile (keys or query rows)
+constexpr int kBS = 136;    // row-major tile stride (bf16): conflict-free ds_read_b128
+constexpr int kTS = 68;     // transposed tile stride (bf16)
+constexpr int kRowTileB = kBT * kBS * 2;  // 17 KiB
+constexpr int kTrTileB = 128 * kTS * 2;   // 17 KiB
+
+struct BwdArgs {
+  const uint16_t *q, *k, *v, *o, *dout;
+  const float *lse;
+  uint16_t *dq, *dk, *dv;
+  float *lse2, *delta;     // (B, H, Sq) workspace
+  float *dk_part, *dv_part;  // (split, B, Hk, Sk, 128) workspace, or null
+  int64_t qsb, qsh, qst, ksb, ksh, kst, vsb, vsh, vst, lsb, lsh;
+  int B, H, Hk, G, Sq, Sk, split;
+  float scale, qscale;
+};
+
+__device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *(const u32x4_t *)p; }
+
+// ------------------------------------------------------------------ prep
+// 16 lanes per query row, 8 dims each: delta = sum(out * dout) in f32 and
+// lse_log2 = lse * log2 e (+inf for a row with no visible key, so that
+// exp2(s - lse_log2) = 0 there, bwd_pipeline.py:120-123).
+__global__ __launch_bounds__(256) void fw_bwd_prep_kernel(BwdArgs a) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t row = gid >> 4;
+  const int c = gid & 15;
+  const uint32_t rows = (uint32_t)a.B * a.H * a.Sq;
+  if (row >= rows) return;
+  const uint32_t bh = row / (uint32_t)a.Sq;
+  const int t = row - bh * a.Sq;
+  const int b = bh / (uint32_t)a.H;
+  const int h = bh - (uint32_t)b * a.H;
+  const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)t * a.qst + 8 * c;
+  const u32x4_t o = ld16(a.o + base), d = ld16(a.dout + base);
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc += bf16_lo(o[e]) * bf16_lo(d[e]);
+    acc += bf16_hi(o[e]) * bf16_hi(d[e]);
+  }
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (c == 0) {
+    const float l = a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + t];
+    a.delta[row] = acc;
+    a.lse2[row] = l == -INFINITY ? INFINITY : l * kLog2e;
+  }
+}
+
+// Scaled, rounded copy of 8 q values (the forward's q_s).
+__device__ __forceinline__ u32x4_t scale_words(const u32x4_t x, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = pack_bf16(bf16_lo(x[e]) * s, bf16_hi(x[e]) * s);
+  return r;
+}
+
+// A transposed-tile operand: row (dim) r, reduction rows 16u + 4g .. + 3 and
+// 16u + 8 + 4g .. + 3 of the streamed tile, matching the order in which an
+// accumulator's values 8(u&1) .. 8(u&1)+7 of sub-tile u>>1 are packed.
+__device__ __forceinline__ bf16x8_t tr_operand(const uint16_t *T, int r, int u, int g) {
+  const uint16_t *p = T + r * kTS + 16 * u + 4 * g;
+  const u32x2_t lo = *(const u32x2_t *)p;
+  const u32x2_t hi = *(const u32x2_t *)(p + 8);
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+}
+
+// Stores rows 2(sr+16p) and 2(sr+16p)+1 (p = 0, 1), dims 8sc .. 8sc+7, of a
+// 64-row tile held in x[2p], x[2p+1]: row-major into R (optional) and
+// transposed, rows in pairs, into T (optional).
+__device__ __forceinline__ void store_pairs(uint16_t *R, uint16_t *T, const u32x4_t (&x)[4],
+                                            int sr, int sc) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int rp = sr + 16 * p;
+    if (R) {
+      *(u32x4_t *)(R + (2 * rp) * kBS + 8 * sc) = x[2 * p];
+      *(u32x4_t *)(R + (2 * rp + 1) * kBS + 8 * sc) = x[2 * p + 1];
+    }
+    if (T) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t x0 = x[2 * p][e], x1 = x[2 * p + 1][e];
+        *(uint32_t *)(T + (8 * sc + 2 * e) * kTS + 2 * rp) = perm_lo(x0, x1);
+        *(uint32_t *)(T + (8 * sc + 2 * e + 1) * kTS + 2 * rp) = perm_hi(x0, x1);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dk, dv
+// Workgroup = 4 waves = 128 keys of KV head hk (wave w: keys k0 + 32w + n);
+// it walks query heads [h0, h0 + G / split) of the group and, per head, the
+// query tiles that can see its keys.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kRowTileB + 2 * kTrTileB + 2 * kBT * 4];
+  uint16_t *Qs = (uint16_t *)smem;                            // q_s rows
+  uint16_t *Ds = (uint16_t *)(smem + kRowTileB);              // dout rows
+  uint16_t *Qt = (uint16_t *)(smem + 2 * kRowTileB);          // q^T (raw)
+  uint16_t *Dt = (uint16_t *)(smem + 2 * kRowTileB + kTrTileB);  // dout^T
+  float *Ls = (float *)(smem + 2 * kRowTileB + 2 * kTrTileB);   // lse_log2
+  float *Dl = Ls + kBT;                                         // delta
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  const int k0 = blockIdx.x * 128;
+  int z = blockIdx.y;
+  const int sp = z % a.split;
+  z /= a.split;
+  const int hk = z % a.Hk;
+  const int b = z / a.Hk;
+  const int chunk = a.G / a.split;
+  const int off = a.Sk - a.Sq;
+
+  const int key = k0 + 32 * w + n;
+  const bool key_ok = key < a.Sk;
+  bf16x8_t kop[8], vop[8];
+  {
+    const int kr = key_ok ? key : 0;
+    const uint16_t *kp = a.k + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kr * a.kst;
+    const uint16_t *vp = a.v + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kr * a.vst;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x4_t kx = ld16(kp + 16 * j + 8 * g), vx = ld16(vp + 16 * j + 8 * g);
+      const u32x4_t z4 = {0, 0, 0, 0};
+      kop[j] = __builtin_bit_cast(bf16x8_t, key_ok ? kx : z4);
+      vop[j] = __builtin_bit_cast(bf16x8_t, key_ok ? vx : z4);
+    }
+  }
+  f32x16_t dkacc[4], dvacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dkacc[c][e] = dvacc[c][e] = 0.f;
+
+  // First query row that sees key k0 (causal: q + off >= key).
+  const int q_first = CAUSAL ? max(0, k0 - off) : 0;
+  const int t_begin = q_first / kBT;
+  const int t_end = (a.Sq + kBT - 1) / kBT;
+  const int kw0 = k0 + 32 * w;  // wave's first key
+  const int sc = tid & 15, sr = tid >> 4;
+  u32x4_t qx[4], dx[4];
+  float lx = 0.f, dl = 0.f;
+
+  for (int hi = 0; hi < chunk; ++hi) {
+    const int h = hk * a.G + sp * chunk + hi;
+    const size_t qbase = (size_t)b * a.qsb + (size_t)h * a.qsh;
+    const size_t sbase = ((size_t)b * a.H + h) * a.Sq;
+    auto gload = [&](int t) {
+      const int qb = t * kBT;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int q = min(qb + 2 * (sr + 16 * p) + r, a.Sq - 1);
+          qx[2 * p + r] = ld16(a.q + qbase + (size_t)q * a.qst + 8 * sc);
+          dx[2 * p + r] = ld16(a.dout + qbase + (size_t)q * a.qst + 8 * sc);
+        }
+      if (tid < kBT) {
+        const int q = qb + tid;
+        lx = q < a.Sq ? a.lse2[sbase + q] : INFINITY;
+        dl = q < a.Sq ? a.delta[sbase + q] : 0.f;
+      }
+    };
+    if (t_begin < t_end) gload(t_begin);
+    for (int t = t_begin; t < t_end; ++t) {
+      __syncthreads();  // the previous tile's LDS reads are done
+      {
+        u32x4_t qsx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qsx[i] = scale_words(qx[i], a.qscale);
+        store_pairs(Qs, nullptr, qsx, sr, sc);
+        store_pairs(nullptr, Qt, qx, sr, sc);
+        store_pairs(Ds, Dt, dx, sr, sc);
+        if (tid < kBT) {
+          Ls[tid] = lx;
+          Dl[tid] = dl;
+        }
+      }
+      __syncthreads();
+      if (t + 1 < t_end) gload(t + 1);
+      const int qb = t * kBT;
+      // causal: no row of this tile sees any key of the wave
+      if (CAUSAL && qb + kBT - 1 + off < kw0) continue;
+      if (kw0 >= a.Sk) continue;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        f32x16_t sacc, dpacc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
+        {
+          bf16x8_t qa[8], da[8];
+          const uint16_t *qr = Qs + (32 * st + n) * kBS + 8 * g;
+          const uint16_t *dr = Ds + (32 * st + n) * kBS + 8 * g;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            qa[j] = __builtin_bit_cast(bf16x8_t, ld16(qr + 16 * j));
+            da[j] = __builtin_bit_cast(bf16x8_t, ld16(dr + 16 * j));
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            sacc = mfma32(qa[j], kop[j], sacc);    // S[q][key]
+            dpacc = mfma32(da[j], vop[j], dpacc);  // dP[q][key]
+          }
+        }
+        // value e: query row qb + 32st + 8(e>>2) + 4g + (e&3), key `key`
+        bf16x8_t pop[2], dsop[2];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          const int r0 = 32 * st + 8 * blk + 4 * g;
+          const f32x4_t l4 = *(const f32x4_t *)(Ls + r0);
+          const f32x4_t d4 = *(const f32x4_t *)(Dl + r0);
+          float pv[4], dv4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * blk + i;
+            const bool vis = !CAUSAL || qb + r0 + i + off >= key;
+            const float p = vis ? fast_exp2(sacc[e] - l4[i]) : 0.f;
+            pv[i] = p;
+            dv4[i] = p * (dpacc[e] - d4[i]);
+          }
+          // values 8(u&1) .. 8(u&1)+7 form the operand of k-step u = 2st + (blk >> 1)
+          const int u = blk >> 1, half = blk & 1;
+          u32x4_t pw = __builtin_bit_cast(u32x4_t, pop[u]);
+          u32x4_t dw = __builtin_bit_cast(u32x4_t, dsop[u]);
+          pw[2 * half] = pack_bf16(pv[0], pv[1]);
+          pw[2 * half + 1] = pack_bf16(pv[2], pv[3]);
+          dw[2 * half] = pack_bf16(dv4[0], dv4[1]);
+          dw[2 * half + 1] = pack_bf16(dv4[2], dv4[3]);
+          pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+          dsop[u] = __builtin_bit_cast(bf16x8_t, dw);
+        }
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) {
+          const int u = 2 * st + uu;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            dvacc[c] = mfma32(tr_operand(Dt, n + 32 * c, u, g), pop[uu], dvacc[c]);
+            dkacc[c] = mfma32(tr_operand(Qt, n + 32 * c, u, g), dsop[uu], dkacc[c]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---------------------------------------------------------------- store
+  if (!key_ok) return;
+  if (a.split == 1) {
+    uint16_t *kp = a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst;
+    uint16_t *vp = a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d = 32 * c + 8 * rr + 4 * g;
+        const f32x16_t &K = dkacc[c];
+        const f32x16_t &V = dvacc[c];
+        *(u32x2_t *)(kp + d) = u32x2_t{pack_bf16(K[4 * rr] * a.scale, K[4 * rr + 1] * a.scale),
+                                       pack_bf16(K[4 * rr + 2] * a.scale, K[4 * rr + 3] * a.scale)};
+        *(u32x2_t *)(vp + d) = u32x2_t{pack_bf16(V[4 * rr], V[4 * rr + 1]),
+                                       pack_bf16(V[4 * rr + 2], V[4 * rr + 3])};
+      }
+  } else {
+    const size_t row = ((((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key) * 128;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d = 32 * c + 8 * rr + 4 * g;
+        *(f32x4_t *)(a.dk_part + row + d) =
+            f32x4_t{dkacc[c][4 * rr], dkacc[c][4 * rr + 1], dkacc[c][4 * rr + 2], dkacc[c][4 * rr + 3]};
+        *(f32x4_t *)(a.dv_part + row + d) =
+            f32x4_t{dvacc[c][4 * rr], dvacc[c][4 * rr + 1], dvacc[c][4 * rr + 2], dvacc[c][4 * rr + 3]};
+      }
+  }
+}
+
+// 16 lanes per key row, 8 dims each: dk = scale * sum of partials, dv = sum.
+__global__ __launch_bounds__(256) void fw_bwd_reduce_kernel(BwdArgs a) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t row = gid >> 4;
+  const int c = gid & 15;
+  const uint32_t rows = (uint32_t)a.B * a.Hk * a.Sk;
+  if (row >= rows) return;
+  const uint32_t bh = row / (uint32_t)a.Sk;
+  const int key = row - bh * a.Sk;
+  const int b = bh / (uint32_t)a.Hk;
+  const int hk = bh - (uint32_t)b * a.Hk;
+  float sk[8] = {}, sv[8] = {};
+  for (int s = 0; s < a.split; ++s) {
+    const size_t base = ((size_t)s * rows + row) * 128 + 8 * c;
+    const f32x4_t k0 = *(const f32x4_t *)(a.dk_part + base), k1 = *(const f32x4_t *)(a.dk_part + base + 4);
+    const f32x4_t v0 = *(const f32x4_t *)(a.dv_part + base), v1 = *(const f32x4_t *)(a.dv_part + base + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sk[e] += k0[e]; sk[4 + e] += k1[e];
+      sv[e] += v0[e]; sv[4 + e] += v1[e];
+    }
+  }
+  u32x4_t ko, vo;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    ko[e] = pack_bf16(sk[2 * e] * a.scale, sk[2 * e + 1] * a.scale);
+    vo[e] = pack_bf16(sv[2 * e], sv[2 * e + 1]);
+  }
+  *(u32x4_t *)(a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst + 8 * c) = ko;
+  *(u32x4_t *)(a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst + 8 * c) = vo;
+}
+
+// ------------------------------------------------------------------ dq
+// Workgroup = 4 waves = 128 query rows of head h (wave w: rows q0 + 32w + n);
+// kv tiles of 64 keys stream through LDS as K rows, V rows and K^T.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kRowTileB + kTrTileB];
+  uint16_t *Ks = (uint16_t *)smem;
+  uint16_t *Vs = (uint16_t *)(smem + kRowTileB);
+  uint16_t *Kt = (uint16_t *)(smem + 2 * kRowTileB);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  const int n_qt = (a.Sq + 127) / 128;
+  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
+  const int q0 = qt * 128;
+  const int off = a.Sk - a.Sq;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < a.Sq;
+
+  bf16x8_t qop[8], dop[8];
+  float l2 = INFINITY, dl = 0.f;
+  {
+    const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)(row_ok ? qrow : 0) * a.qst;
+    const float qs = row_ok ? a.qscale : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
+      const u32x4_t d = ld16(a.dout + base + 16 * j + 8 * g);
+      dop[j] = __builtin_bit_cast(bf16x8_t, row_ok ? d : u32x4_t{0, 0, 0, 0});
+    }
+    if (row_ok) {
+      const size_t s = ((size_t)b * a.H + h) * a.Sq + qrow;
+      l2 = a.lse2[s];
+      dl = a.delta[s];
+    }
+  }
+  f32x16_t dqacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqacc[c][e] = 0.f;
+
+  // visible keys of a row: [0, hi)
+  auto row_hi = [&](int r) { return CAUSAL ? min(a.Sk, r + off + 1) : a.Sk; };
+  const int last_row = min(q0 + 127, a.Sq - 1);
+  const int wg_hi = row_hi(last_row);
+  const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
+  const int w_last = min(q0 + 32 * w + 31, a.Sq - 1);
+  const int w_hi = q0 + 32 * w < a.Sq ? row_hi(w_last) : 0;
+  const int r_hi = row_hi(qrow);
+
+  const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
+  const size_t vbase = (size_t)b * a.vsb + (size_t)hk * a.vsh;
+  const int sc = tid & 15, sr = tid >> 4;
+  u32x4_t kx[4], vx[4];
+  auto gload = [&](int t) {
+    const int kb = t * kBT, kmax = a.Sk - 1;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int kk = min(kb + 2 * (sr + 16 * p) + r, kmax);
+        kx[2 * p + r] = ld16(a.k + kbase + (size_t)kk * a.kst + 8 * sc);
+        vx[2 * p + r] = ld16(a.v + vbase + (size_t)kk * a.vst + 8 * sc);
+      }
+  };
+  if (t_end > 0) gload(0);
+  for (int t = 0; t < t_end; ++t) {
+    __syncthreads();
+    store_pairs(Ks, Kt, kx, sr, sc);
+    store_pairs(Vs, nullptr, vx, sr, sc);
+    __syncthreads();
+    if (t + 1 < t_end) gload(t + 1);
+    const int kb = t * kBT;
+    if (kb >= w_hi) continue;  // no row of the wave sees this tile
+    const bool full = kb + kBT <= row_hi(q0 + 32 * w);
+    bf16x8_t dsop[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x16_t sacc, dpacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
+      {
+        bf16x8_t ka[8], va[8];
+        const uint16_t *kr = Ks + (32 * st + n) * kBS + 8 * g;
+        const uint16_t *vr = Vs + (32 * st + n) * kBS + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
+          va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sacc = mfma32(ka[j], qop[j], sacc);    // S^T[key][q]
+          dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
+        }
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        u32x4_t dw;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          float dsv[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int e = 8 * u2 + 2 * e2 + i;
+            const int kk = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+            const bool vis = full || kk < r_hi;
+            const float p = vis ? fast_exp2(sacc[e] - l2) : 0.f;
+            dsv[i] = p * (dpacc[e] - dl);
+          }
+          dw[e2] = pack_bf16(dsv[0], dsv[1]);
+        }
+        dsop[2 * st + u2] = __builtin_bit_cast(bf16x8_t, dw);
+      }
+    }
+    // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dqacc[c] = mfma32(tr_operand(Kt, n + 32 * c, u, g), dsop[u], dqacc[c]);
+  }
+
+  if (!row_ok) return;
+  uint16_t *dp = a.dq + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qrow * a.qst;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const f32x16_t &Q = dqacc[c];
+      *(u32x2_t *)(dp + 32 * c + 8 * rr + 4 * g) =
+          u32x2_t{pack_bf16(Q[4 * rr] * a.scale, Q[4 * rr + 1] * a.scale),
+                  pack_bf16(Q[4 * rr + 2] * a.scale, Q[4 * rr + 3] * a.scale)};
+    }
+}
+
+// Query heads of one KV head are split over `split` workgroups when the
+// (batch, kv head, key tile) grid alone would leave CUs idle.
+int pick_split(const fw_attn_bwd_params *p) {
+  const int G = p->nheads / p->nheads_k;
+  const long base = (long)p->batch * p->nheads_k * ceil_div(p->seqlen_k, 128);
+  int split = 1;
+  while (split < G && base * split < 512) {
+    int nxt = split + 1;
+    while (G % nxt) ++nxt;
+    split = nxt;
+  }
+  return split;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p) {
+  if (p->nheads_k <= 0 || p->nheads % p->nheads_k) return 0;
+  const size_t rows = (size_t)p->batch * p->nheads * p->seqlen_q;
+  size_t bytes = 2 * align256(rows * 4);
+  const int split = pick_split(p);
+  if (split > 1) bytes += 2 * align256((size_t)split * p->batch * p->nheads_k * p->seqlen_k * 128 * 4);
+  return bytes;
+}
+
+extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
+  FW_REQUIRE(p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 backward takes head_dim 128; got %d", p->head_dim);
+  FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
+             "nheads (%d) must be a multiple of nheads_k (%d)", p->nheads, p->nheads_k);
+  FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
+             "batch, seqlen_q and seqlen_k must be positive");
+  FW_REQUIRE(p->q && p->k && p->v && p->out && p->dout && p->lse && p->dq && p->dk && p->dv,
+             FW_ERR_VALUE, "q, k, v, out, dout, lse, dq, dk and dv are required");
+  const size_t need = fw_attn_bwd_workspace_bytes(p);
+  FW_REQUIRE(p->workspace && p->workspace_bytes >= need, FW_ERR_VALUE,
+             "workspace of %zu bytes is smaller than the %zu needed", p->workspace_bytes, need);
+  FW_REQUIRE((long)p->batch * p->nheads * p->seqlen_q * 16 < (1l << 32) &&
+                 (long)p->batch * p->nheads_k * p->seqlen_k * 16 < (1l << 32),
+             FW_ERR_VALUE, "too many rows for one launch");
+  BwdArgs a;
+  a.q = (const uint16_t *)p->q;
+  a.k = (const uint16_t *)p->k;
+  a.v = (const uint16_t *)p->v;
+  a.o = (const uint16_t *)p->out;
+  a.dout = (const uint16_t *)p->dout;
+  a.lse = p->lse;
+  a.dq = (uint16_t *)p->dq;
+  a.dk = (uint16_t *)p->dk;
+  a.dv = (uint16_t *)p->dv;
+  const size_t rows = (size_t)p->batch * p->nheads * p->seqlen_q;
+  uint8_t *ws = (uint8_t *)p->workspace;
+  a.lse2 = (float *)ws;
+  a.delta = (float *)(ws + align256(rows * 4));
+  a.split = pick_split(p);
+  a.dk_part = a.dv_part = nullptr;
+  if (a.split > 1) {
+    const size_t part = align256((size_t)a.split * p->batch * p->nheads_k * p->seqlen_k * 128 * 4);
+    a.dk_part = (float *)(ws + 2 * align256(rows * 4));
+    a.dv_part = (float *)(ws + 2 * align256(rows * 4) + part);
+  }
+  a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qst = p->q_stride_t;
+  a.ksb = p->k_stride_b; a.ksh = p->k_stride_h; a.kst = p->k_stride_t;
+  a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.vst = p->v_stride_t;
+  a.lsb = p->lse_stride_b; a.lsh = p->lse_stride_h;
+  a.B = p->batch;
+  a.H = p->nheads;
+  a.Hk = p->nheads_k;
+  a.G = p->nheads / p->nheads_k;
+  a.Sq = p->seqlen_q;
+  a.Sk = p->seqlen_k;
+  a.scale = p->softmax_scale;
+  a.qscale = p->softmax_scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+
+  fw_bwd_prep_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a);  // 16 rows per block
+  int st = check_launch("fw_bwd_prep_kernel");
+  if (st != FW_OK) return st;
+  const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split);
+  if (p->causal) fw_bwd_dkv_kernel<true><<<gkv, 256, 0, s>>>(a);
+  else fw_bwd_dkv_kernel<false><<<gkv, 256, 0, s>>>(a);
+  st = check_launch("fw_bwd_dkv_kernel");
+  if (st != FW_OK) return st;
+  if (a.split > 1) {
+    const long thr = (long)p->batch * p->nheads_k * p->seqlen_k * 16;
+    fw_bwd_reduce_kernel<<<(unsigned)((thr + 255) / 256), 256, 0, s>>>(a);
+    st = check_launch("fw_bwd_reduce_kernel");
+    if (st != FW_OK) return st;
+  }
+  const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads);
+  if (p->causal) fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
+  else fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
+  return check_launch("fw_bwd_dq_kernel");
+}

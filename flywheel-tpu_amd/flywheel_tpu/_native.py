@@ -67,6 +67,21 @@ class PrefillParams(ctypes.Structure):
     ]
 
 
+class AttnBwdParams(ctypes.Structure):
+    _fields_ = [
+        ("q", _c_p), ("k", _c_p), ("v", _c_p), ("out", _c_p), ("dout", _c_p), ("lse", _c_p),
+        ("dq", _c_p), ("dk", _c_p), ("dv", _c_p),
+        ("workspace", _c_p), ("workspace_bytes", ctypes.c_size_t),
+        ("q_stride_b", _i64), ("q_stride_h", _i64), ("q_stride_t", _i64),
+        ("k_stride_b", _i64), ("k_stride_h", _i64), ("k_stride_t", _i64),
+        ("v_stride_b", _i64), ("v_stride_h", _i64), ("v_stride_t", _i64),
+        ("lse_stride_b", _i64), ("lse_stride_h", _i64),
+        ("batch", _i32), ("nheads", _i32), ("nheads_k", _i32), ("head_dim", _i32),
+        ("seqlen_q", _i32), ("seqlen_k", _i32),
+        ("softmax_scale", _f32), ("causal", _i32),
+    ]
+
+
 class RotaryParams(ctypes.Structure):
     _fields_ = [
         ("x", _c_p), ("y", _c_p), ("cos_table", _c_p), ("sin_table", _c_p),
@@ -92,6 +107,8 @@ SIGNATURES = {
     "fw_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(PrefillParams)]),
     "fw_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillParams), _c_p]),
     "fw_rotary": (ctypes.c_int, [ctypes.POINTER(RotaryParams), _c_p]),
+    "fw_attn_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnBwdParams)]),
+    "fw_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _c_p]),
 }
 
 

@@ -1,0 +1,63 @@
+"""Gradients of flash_attn_func through the gfx950 backward kernels.
+
+Mirrors the reference's differentiation rules (flywheel_tpu/softmax_attention/
+autograd.py:27-109): the dense MHA / GQA / MQA forward with a causal or full
+mask has a backward (flash_attn_bwd, kernels/bwd.py:463); every other
+configuration runs its forward and raises NotImplementedError, naming the
+feature, only when a gradient is requested.  lse carries no gradient of its own.
+"""
+
+import torch
+
+from . import _native as N
+
+
+def attn_bwd(q, k, v, out, dout, lse, *, qs, ks, ls, batch, nheads, nheads_k, seqlen_q,
+             seqlen_k, softmax_scale, causal):
+    """fw_attn_bwd: (dq, dk, dv) laid out like q, k, v (all contiguous)."""
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    p = N.AttnBwdParams()
+    p.q, p.k, p.v, p.out, p.dout, p.lse = (N.ptr(t) for t in (q, k, v, out, dout, lse))
+    p.dq, p.dk, p.dv = N.ptr(dq), N.ptr(dk), N.ptr(dv)
+    p.q_stride_b, p.q_stride_h, p.q_stride_t = qs
+    p.k_stride_b, p.k_stride_h, p.k_stride_t = ks
+    p.v_stride_b, p.v_stride_h, p.v_stride_t = ks
+    p.lse_stride_b, p.lse_stride_h = ls
+    p.batch, p.nheads, p.nheads_k, p.head_dim = batch, nheads, nheads_k, 128
+    p.seqlen_q, p.seqlen_k = seqlen_q, seqlen_k
+    p.softmax_scale, p.causal = softmax_scale, int(causal)
+    lib = N.lib()
+    nbytes = lib.fw_attn_bwd_workspace_bytes(p)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    p.workspace, p.workspace_bytes = N.ptr(ws), ws.numel()
+    N.check(lib.fw_attn_bwd(p, N.stream_of(q)))
+    return dq, dk, dv
+
+
+class FlashAttnFunction(torch.autograd.Function):
+    """forward(q, k, v, spec) -> (out, lse); spec holds the launch closure, the
+    geometry for the backward and, for forward-only configurations, the
+    message the backward raises (autograd.py:75-109, variant.py:365-384)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, spec):
+        out, lse = spec["run"](q, k, v)
+        ctx.spec = spec
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, unused_dlse):
+        spec = ctx.spec
+        if spec["forward_only"]:
+            raise NotImplementedError(spec["forward_only"])
+        q, k, v, out, lse = ctx.saved_tensors
+        g = spec["geometry"]
+        dq, dk, dv = attn_bwd(q, k, v, out, dout.contiguous(), lse, **g)
+        return dq, dk, dv, None
+
+
+def needs_grad(*tensors):
+    return torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)

@@ -24,6 +24,7 @@ from .inputs import (
     resolve_scale,
 )
 from .kv_layout import resolve_merged_kv_heads
+from . import backward as B
 from . import rotary as R
 
 def _check_bf16(*ts):
@@ -167,23 +168,52 @@ def flash_attn_func(
         raise ValueError("RoPE prefill requires seqlen_q <= seqlen_k.")
     _check_bf16(q, k, v)
     N.require_device(q, k, v)
+    grad = B.needs_grad(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    if tables is not None and rotary_k:
-        # rotary.py:118-120: K at i; Q (at seqlen_k - seqlen_q + i) is rotated
-        # by the kernel as it loads it.
-        k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
-                     nheads=nheads_k, ntokens=seqlen_k)
     softmax_scale = resolve_scale(softmax_scale, d)
     sinks = check_sinks(learnable_sink, nheads, q.device)
-    out = torch.empty_like(q)
-    lse = (torch.empty((batch, nheads, seqlen_q), dtype=torch.float32, device=q.device)
-           if return_softmax_lse else None)
-    _run_prefill(N.FW_KV_DENSE, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
-                 ls=(nheads * seqlen_q, seqlen_q), batch=batch, nheads=nheads,
-                 nheads_k=nheads_k, head_dim=d, seqlen_q=seqlen_q, seqlen_k=seqlen_k,
-                 causal=causal, window_size=window_size, softmax_scale=softmax_scale,
-                 softcap=softcap, sinks=sinks,
-                 q_rotary=None if tables is None else (tables, rotary_interleaved))
+    lse_shape = (batch, nheads, seqlen_q)
+
+    def run(q, k, v, with_lse):
+        if tables is not None and rotary_k:
+            # rotary.py:118-120: K at i; Q (at seqlen_k - seqlen_q + i) is
+            # rotated by the kernel as it loads it.
+            k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
+                         nheads=nheads_k, ntokens=seqlen_k)
+        out = torch.empty_like(q)
+        lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if with_lse else None
+        _run_prefill(N.FW_KV_DENSE, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+                     ls=(nheads * seqlen_q, seqlen_q), batch=batch, nheads=nheads,
+                     nheads_k=nheads_k, head_dim=d, seqlen_q=seqlen_q, seqlen_k=seqlen_k,
+                     causal=causal, window_size=window_size, softmax_scale=softmax_scale,
+                     softcap=softcap, sinks=sinks,
+                     q_rotary=None if tables is None else (tables, rotary_interleaved))
+        return out, lse
+
+    if not grad:
+        out, lse = run(q, k, v, return_softmax_lse)
+    else:
+        # prefill.py:250-297 and variant.py:365-384: which configurations have
+        # a backward; the others raise when a gradient is requested.
+        reason = None
+        if heads_outer_fold or tables is not None or sinks is not None:
+            what = ("Fused RoPE" if tables is not None else
+                    "heads_outer_fold" if heads_outer_fold else "learnable_sink")
+            reason = f"{what} is forward-only; backward is unsupported."
+        else:
+            unsupported = ("window_size" if window_size != (-1, -1) else
+                           "softcap" if softcap != 0.0 else None)
+            if unsupported:
+                reason = (f"The backward kernel does not support {unsupported}; that"
+                          " configuration is forward-only.")
+        spec = {
+            "run": lambda q, k, v: run(q, k, v, True),
+            "forward_only": reason,
+            "geometry": dict(qs=qs, ks=ks, ls=(nheads * seqlen_q, seqlen_q), batch=batch,
+                             nheads=nheads, nheads_k=nheads_k, seqlen_q=seqlen_q,
+                             seqlen_k=seqlen_k, softmax_scale=softmax_scale, causal=causal),
+        }
+        out, lse = B.FlashAttnFunction.apply(q, k, v, spec)
     if return_softmax_lse:
         return out, lse
     return out

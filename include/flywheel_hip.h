@@ -193,6 +193,40 @@ size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);
 int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
 
 /*
+ * Dense flash-attention backward: dq, dk, dv (bf16) from q, k, v, out, dout
+ * (bf16) and the forward's lse (f32, natural log).  Replaces flash_attn_bwd
+ * (softmax_attention/kernels/bwd.py:463-840): the lse_log2 / delta
+ * preparation (bwd.py:685-720) and the dk / dv / dq recurrences of
+ * bwd_pipeline.py:401-570 (p = exp2(q_s k - lse_log2) from the forward's
+ * rounded scaled q, ds = p (dp - delta), dk = scale ds^T q, dv = p^T dout,
+ * dq = scale ds k).  MHA and GQA / MQA; causal (bottom-right, offset
+ * seqlen_k - seqlen_q) or full mask; the backward supports nothing else of the
+ * forward (variant.py:365-384).  Element (b, h, t, d) of q, out, dout and dq is
+ * at b*q_stride_b + h*q_stride_h + t*q_stride_t + d; k and dk use the k
+ * strides, v and dv the v strides; lse (b, h, t) at b*lse_stride_b +
+ * h*lse_stride_h + t.  Deterministic: no atomics.  The workspace (its size
+ * from fw_attn_bwd_workspace_bytes) holds f32 row statistics and, when the
+ * query heads of one KV head are split over workgroups, f32 dk / dv partials.
+ */
+typedef struct fw_attn_bwd_params {
+  const void *q, *k, *v, *out, *dout;
+  const float *lse;
+  void *dq, *dk, *dv;
+  void *workspace;
+  size_t workspace_bytes;
+  int64_t q_stride_b, q_stride_h, q_stride_t;
+  int64_t k_stride_b, k_stride_h, k_stride_t;
+  int64_t v_stride_b, v_stride_h, v_stride_t;
+  int64_t lse_stride_b, lse_stride_h;
+  int32_t batch, nheads, nheads_k, head_dim, seqlen_q, seqlen_k;
+  float softmax_scale;
+  int32_t causal;
+} fw_attn_bwd_params;
+
+size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p);
+int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream);
+
+/*
  * RoPE on bf16 rows at their prefill positions, in f32 with one rounding to
  * bf16.  Replaces the reference's fused rotation of staged Q / K tiles:
  * prepare_rotary (softmax_attention/rotary.py:27-167: positions and the packed

@@ -1,0 +1,95 @@
+"""GPU parity of the dense backward (flash_attn_func under torch.autograd)
+against oracle/backward.py, with the reference's tolerance rule
+(test_prefill.py:301-333): max |grad - ref| <= 3 * max |bf16_ref - ref| + atol,
+where ref is the float64 backward from the forward's rounded scaled q and
+bf16_ref rounds out, p, dp and ds to bf16 as a bf16 computation would."""
+
+import numpy as np
+import pytest
+import torch
+
+from flywheel_tpu import flash_attn_func
+from oracle import backward as OB
+from tests.gpu_util import DEV, announce, randn, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def head_major(x):  # (B, S, H, D) <-> (B, H, S, D)
+    return np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+
+
+def check_grads(got, q, k, v, do, causal, what):
+    ref = OB.attention_bwd_ref(q, k, v, do, causal=causal, round_scaled_q=True)
+    coarse = OB.attention_bwd_ref(q, k, v, do, causal=causal, round_scaled_q=True,
+                                  bf16_intermediates=True)
+    for name, g, r, c in zip(("dq", "dk", "dv"), got, ref, coarse):
+        err = np.abs(g - r).max()
+        bound = 3 * np.abs(c - r).max() + 2 * np.abs(r + 0.3 - 0.3 - r).max() + 1e-4
+        print(f"{what} {name}: max err {err:.3e} bound {bound:.3e} |ref| {np.abs(r).max():.3e}")
+        assert err <= bound, f"{what} {name}: {err} > {bound}"
+
+
+def run(q, k, v, do, causal, token_major=False):
+    b, sq, h, d = q.shape
+    hk = k.shape[2]
+    if token_major:
+        tens = [to_dev_bf16(x.reshape(x.shape[0], x.shape[1], -1)).requires_grad_() for x in (q, k, v)]
+        out = flash_attn_func(*tens, causal=causal, token_major=True, head_dim=d)
+        out.backward(to_dev_bf16(do.reshape(b, sq, h * d)))
+        torch.cuda.synchronize()
+        return [t.grad.float().cpu().numpy().reshape(t.shape[0], t.shape[1], -1, d) for t in tens]
+    tens = [to_dev_bf16(head_major(x)).requires_grad_() for x in (q, k, v)]
+    out = flash_attn_func(*tens, causal=causal)
+    out.backward(to_dev_bf16(head_major(do)))
+    torch.cuda.synchronize()
+    return [head_major(t.grad.float().cpu().numpy()) for t in tens]
+
+
+@pytest.mark.parametrize(
+    "b,h,hk,sq,sk,causal",
+    [
+        (1, 4, 4, 128, 128, True),
+        (2, 4, 2, 200, 333, True),
+        (1, 4, 1, 333, 200, True),   # leading rows see no key
+        (1, 8, 2, 300, 300, False),
+        (1, 2, 2, 64, 1000, False),
+        (1, 16, 2, 520, 520, True),  # query heads of a KV head split over workgroups
+    ],
+)
+def test_flash_attn_func_backward(b, h, hk, sq, sk, causal):
+    what = f"bwd b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+    announce(what)
+    rng = np.random.default_rng(60)
+    q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
+    do = randn(rng, (b, sq, h, 128))
+    check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
+
+
+def test_backward_token_major_and_repeat():
+    announce("bwd token-major, bitwise repeat")
+    rng = np.random.default_rng(61)
+    q, k, v = randn(rng, (2, 150, 4, 128)), randn(rng, (2, 150, 2, 128)), randn(rng, (2, 150, 2, 128))
+    do = randn(rng, (2, 150, 4, 128))
+    g1 = run(q, k, v, do, True, token_major=True)
+    check_grads(g1, q, k, v, do, True, "token-major")
+    g2 = run(q, k, v, do, True, token_major=True)
+    for a, b_ in zip(g1, g2):
+        np.testing.assert_array_equal(a, b_)
+
+
+def test_backward_forward_only_configurations_raise():
+    """autograd.py:75-109, variant.py:365-384: the forward runs, the backward
+    names the unsupported feature."""
+    announce("bwd forward-only raises")
+    rng = np.random.default_rng(62)
+    x = lambda *s: to_dev_bf16(randn(rng, s)).requires_grad_()
+    q, k, v = x(1, 2, 64, 128), x(1, 2, 64, 128), x(1, 2, 64, 128)
+    for kw, msg in ((dict(window_size=(8, 0)), "window_size"), (dict(softcap=5.0), "softcap"),
+                    (dict(learnable_sink=torch.zeros(2, device=DEV)), "learnable_sink")):
+        out = flash_attn_func(q, k, v, causal=True, **kw)
+        with pytest.raises(NotImplementedError, match=msg):
+            out.sum().backward()
+    # no gradient requested: the same calls run as plain forwards
+    with torch.no_grad():
+        flash_attn_func(q, k, v, causal=True, window_size=(8, 0))

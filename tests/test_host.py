@@ -39,7 +39,8 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header_fields():
     text = open(HEADER).read()
     for struct, cls in (("fw_decode_params", N.DecodeParams), ("fw_prefill_params", N.PrefillParams),
-                        ("fw_rotary_params", N.RotaryParams)):
+                        ("fw_rotary_params", N.RotaryParams),
+                        ("fw_attn_bwd_params", N.AttnBwdParams)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         fields = []
