@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
   const int t_begin = q_first / kBT;
   const int t_end = (a.Sq + kBT - 1) / kBT;
   const int kw0 = k0 + 32 * w;  // wave's first key
-  const int sc = tid & 15, sr = tid >> 4;
+  const int sr = tid & 15, sc = tid >> 4;  // rows vary fastest: conflict-free transposed stores
   u32x4_t qx[4], dx[4];
   float lx = 0.f, dl = 0.f;
 
@@ -213,24 +213,32 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
       // causal: no row of this tile sees any key of the wave
       if (CAUSAL && qb + kBT - 1 + off < kw0) continue;
       if (kw0 >= a.Sk) continue;
+      // every row of the tile sees every key of the wave (rows past Sq have
+      // lse_log2 = +inf, so p = 0 there without a mask)
+      const bool full = !CAUSAL || qb + off >= kw0 + 31;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         f32x16_t sacc, dpacc;
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
         {
-          bf16x8_t qa[8], da[8];
+          // operands read two steps ahead of their MFMAs (a few registers live)
           const uint16_t *qr = Qs + (32 * st + n) * kBS + 8 * g;
           const uint16_t *dr = Ds + (32 * st + n) * kBS + 8 * g;
+          bf16x8_t qa[3], da[3];
+          qa[0] = __builtin_bit_cast(bf16x8_t, ld16(qr));
+          da[0] = __builtin_bit_cast(bf16x8_t, ld16(dr));
+          qa[1] = __builtin_bit_cast(bf16x8_t, ld16(qr + 16));
+          da[1] = __builtin_bit_cast(bf16x8_t, ld16(dr + 16));
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            qa[j] = __builtin_bit_cast(bf16x8_t, ld16(qr + 16 * j));
-            da[j] = __builtin_bit_cast(bf16x8_t, ld16(dr + 16 * j));
-          }
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            sacc = mfma32(qa[j], kop[j], sacc);    // S[q][key]
-            dpacc = mfma32(da[j], vop[j], dpacc);  // dP[q][key]
+            if (j + 2 < 8) {
+              qa[(j + 2) % 3] = __builtin_bit_cast(bf16x8_t, ld16(qr + 16 * (j + 2)));
+              da[(j + 2) % 3] = __builtin_bit_cast(bf16x8_t, ld16(dr + 16 * (j + 2)));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            sacc = mfma32(qa[j % 3], kop[j], sacc);    // S[q][key]
+            dpacc = mfma32(da[j % 3], vop[j], dpacc);  // dP[q][key]
           }
         }
         // value e: query row qb + 32st + 8(e>>2) + 4g + (e&3), key `key`
@@ -244,7 +252,7 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * blk + i;
-            const bool vis = !CAUSAL || qb + r0 + i + off >= key;
+            const bool vis = full || qb + r0 + i + off >= key;
             const float p = vis ? fast_exp2(sacc[e] - l4[i]) : 0.f;
             pv[i] = p;
             dv4[i] = p * (dpacc[e] - d4[i]);
@@ -391,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 
   const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
   const size_t vbase = (size_t)b * a.vsb + (size_t)hk * a.vsh;
-  const int sc = tid & 15, sr = tid >> 4;
+  const int sr = tid & 15, sc = tid >> 4;  // rows vary fastest: conflict-free transposed stores
   u32x4_t kx[4], vx[4];
   auto gload = [&](int t) {
     const int kb = t * kBT, kmax = a.Sk - 1;
