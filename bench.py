@@ -1,6 +1,7 @@
 """Benchmark of the softmax-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c2|c3|c4|c5|all|bwd|rope|copy]
 
 Workloads (inputs synthetic, seeded, resident in HBM
 before the timed region):
@@ -13,6 +14,8 @@ before the timed region):
       -> TFLOP/s
   c5  fp8 e4m3 paged decode with a 4-token verify window, B=128,
       ctx U[4096, 65536] -> HBM GB/s
+Extras (not in "all"): bwd (c2's shape through the dense backward), rope (c2
+with fused RoPE tables), copy (calibration of the HBM byte counters).
 The printed JSON line's headline is c2; with
 --workload all (the default) c3/c4/c5 follow in "also".  Each carries
 "roofline" (events on the launch stream) and "cpu_baseline" (the NumPy oracle on
@@ -317,8 +320,77 @@ def workload_copy(args, device):
                 cpu=None)
 
 
+def _c2_inputs(device):
+    b, h, hk, s, d = 1, 32, 4, 4096, 128
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    return (b, h, hk, s, d), gen, q, k, v
+
+
+def workload_bwd(args, device):
+    """c2's shape through the dense backward (fw_attn_bwd: row statistics, dk/dv,
+    dq), inputs (q, k, v, out, lse, dout) resident; FLOPs counted as 2.5x the
+    forward's (the five backward products; the kernels also recompute two)."""
+    from flywheel_tpu import flash_attn_func
+    from flywheel_tpu.backward import attn_bwd
+    (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device)
+    do = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    out, lse = flash_attn_func(q, k, v, causal=True, return_softmax_lse=True)
+    kw = dict(qs=(h * s * d, s * d, d), ks=(hk * s * d, s * d, d), ls=(h * s, s), batch=b,
+              nheads=h, nheads_k=hk, seqlen_q=s, seqlen_k=s, softmax_scale=d ** -0.5, causal=True)
+    flops = 2.5 * 4.0 * s * s * h * d / 2 * b
+    ms = timed(lambda: attn_bwd(q, k, v, out, do, lse, **kw), args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    def cpu():
+        from oracle import backward as OB
+        rng = np.random.default_rng(0)
+        heads = 2  # sample: 2 query heads of one KV head, full 4096 causal
+        x = lambda n: rng.standard_normal((1, s, n, d), dtype=np.float32)
+        qc, kc, vc, dc = x(heads), x(1), x(1), x(heads)
+        with cpu_limits():
+            t = cpu_time(lambda: OB.attention_bwd_ref(qc, kc, vc, dc, causal=True), min_rounds=1)
+        return {"value": round(2.5 * 4.0 * s * s * heads * d / 2 / t / 1e12, 5), "unit": "TFLOP/s",
+                "cores": CPU_THREADS, "kind": "port",
+                "sample": "oracle.backward.attention_bwd_ref (float64), 2 of 32 heads at full"
+                          " 4096 causal"}
+
+    return dict(
+        name="bwd", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_func backward (dq, dk, dv), causal GQA", "batch": b,
+                "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "kernel": "fw_bwd_prep + fw_bwd_dkv + fw_bwd_reduce + fw_bwd_dq (whole backward)",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=cpu)
+
+
+def workload_rope(args, device):
+    """c2 with fused RoPE (f32 tables, Q rotated in the kernel, K by fw_rotary)."""
+    from flywheel_tpu import flash_attn_func
+    (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device)
+    ang = torch.rand((s, d // 2), generator=gen, device=device) * 6.283
+    cos, sin = ang.cos(), ang.sin()
+    flops = 4.0 * s * s * h * d / 2 * b
+    ms = timed(lambda: flash_attn_func(q, k, v, causal=True, rotary_cos=cos, rotary_sin=sin),
+               args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(
+        name="rope", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_func causal GQA prefill with fused RoPE on Q and K",
+                "batch": b, "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "kernel": "fw_rotary (K) + fw_prefill_pp_kernel<DENSE> (Q rotated on load)",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=None)
+
+
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
-EXTRA = {"copy": workload_copy}
+EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope}
 
 
 def main():
