@@ -926,9 +926,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // Tile t goes from global memory straight into LDS buffer t % 3
   // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
   // per instruction); this wave moves key rows 8w .. 8w+7.
-  auto dma_tile = [&](int j, const int buf) __attribute__((always_inline)) {
+  auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
-    int key0 = min((t_begin + j) * kKT + 8 * w, kmax);
+    int key0 = min((t_begin + j) * kKT + 8 * wv, kmax);
     const uint8_t *kp, *vp;
     if constexpr (MODE == FW_KV_PAGED) {
       key0 &= ~7;  // an 8-row group never straddles a page (P % 16 == 0)
@@ -942,15 +942,15 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
     const uint32_t lim = (uint32_t)(kmax - key0);
     const uint32_t lra = min(lr0, lim), lrb = min(lr0 + 4u, lim);
-    const uint32_t c16a = c16b ^ (16u * ((2 * w) & 3)), c16c = c16b ^ (16u * ((2 * w + 1) & 3));
-    const uint32_t d = lds0 + (uint32_t)(8 * w * kRowB) + (uint32_t)buf * kTileB;
+    const uint32_t c16a = c16b ^ (16u * ((2 * wv) & 3)), c16c = c16b ^ (16u * ((2 * wv + 1) & 3));
+    const uint32_t d = lds0 + (uint32_t)(8 * wv * kRowB) + (uint32_t)buf * kTileB;
     lds_dma16(kp, __umul24(lra, kstB) + c16a, d);
     lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 3 * kTileB);
     lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
     lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 3 * kTileB);
   };
   // Tile 0's copy goes out before the Q loads so the two latencies overlap.
-  if (T > 0) dma_tile(0, 0);
+  if (T > 0) dma_tile(0, 0, w);
 
   // ------------------------------------------------------------ Q^T operand
   bf16x8_t qop[8];
@@ -1134,10 +1134,12 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
-    // Tile 0 from every wave; group 1 also starts its rows of tile 1 here
-    // (group 0 issues those at the start of its first MFMA slot).
-    if (grp == 1 && T > 1) dma_tile(1, 1);
-    if (grp == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    // Tile 0 from every wave; group 1 also starts all rows of tile 1 here.
+    if (grp == 1 && T > 1) {
+      dma_tile(1, 1, w - 4);
+      dma_tile(1, 1, w);
+    }
+    if (grp == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     slot_barrier();  // tile 0 complete
     if (grp == 1) slot_barrier();
@@ -1161,19 +1163,19 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       // MFMA slot at raised priority: the other wave of this SIMD is in its
       // softmax slot and would otherwise win issue whenever it is the older.
       // Tile t's buffer is free from slot 2t-2 and must be complete at the
-      // end of slot 2t-1: group 0 issues its rows at the start of M(t-1) and
-      // waits at the end of S(t-1); group 1 issues in S(t-2) and waits at the
-      // end of M(t-1).
-      if (grp == 0 && j + 1 < T) dma_tile(j + 1, (B + 1) % 3);
+      // end of slot 2t-1: group 1 issues all of its rows in S(t-2) and waits
+      // at the end of M(t-1), so group 0's MFMA slots issue no copies.
       __builtin_amdgcn_s_setprio(2);
       mslot(B, (B + 2) % 3, pops);
       __builtin_amdgcn_s_setprio(0);
       if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
-      if (grp == 1 && j + 2 < T) dma_tile(j + 2, (B + 2) % 3);
+      if (grp == 1 && j + 2 < T) {
+        dma_tile(j + 2, (B + 2) % 3, w - 4);
+        dma_tile(j + 2, (B + 2) % 3, w);
+      }
       if (j < T) softmax(t_begin + j, pops);
       mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
-      if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
     };
     using I0 = std::integral_constant<int, 0>;
