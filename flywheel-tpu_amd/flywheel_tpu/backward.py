@@ -58,6 +58,29 @@ class FlashAttnFunction(torch.autograd.Function):
         return dq, dk, dv, None
 
 
+class ForwardOnlyFunction(torch.autograd.Function):
+    """A forward with no backward: the gradient request raises the message
+    (autograd.py:75-109, forward_only_attn).  holder carries the launch
+    closure in and lse (not differentiable) out."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, holder):
+        out, holder["lse"] = holder["run"](q, k, v)
+        ctx.msg = holder["msg"]
+        return out
+
+    @staticmethod
+    def backward(ctx, unused_dout):
+        raise NotImplementedError(ctx.msg)
+
+
+def forward_only(run, msg, q, k, v):
+    """(out, lse) of run(q, k, v) as an autograd node whose backward raises."""
+    holder = {"run": run, "msg": msg}
+    out = ForwardOnlyFunction.apply(q, k, v, holder)
+    return out, holder["lse"]
+
+
 def needs_grad(*tensors):
     return torch.is_grad_enabled() and any(
         isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)

@@ -27,6 +27,10 @@ from .kv_layout import resolve_merged_kv_heads
 from . import backward as B
 from . import rotary as R
 
+# prefill.py:940-950: the varlen kernels have no backward.
+_VARLEN_FORWARD_ONLY = "flash_attn_varlen_func is forward-only; backward is unsupported."
+
+
 def _check_bf16(*ts):
     if not all(t.dtype == torch.bfloat16 for t in ts):
         raise NotImplementedError(
@@ -104,6 +108,14 @@ def flash_attn_func(
     seqlen, d).  causal is bottom-right aligned: query i sees key j iff
     j <= i + seqlen_k - seqlen_q.  Rows with no reachable key return out 0 and
     lse -inf (or the sink).  lse (batch, nheads, seqlen_q) f32.
+
+    rotary_cos / rotary_sin: (seqlen_ro >= seqlen_k, d / 2) tables in q's dtype
+    or float32; K is rotated at positions 0..seqlen_k-1, Q at seqlen_k -
+    seqlen_q + i (rotary_k=False: Q only), in f32 with one rounding to bf16
+    (rotary.py:27-215).  Gradients (torch.autograd) cover MHA / GQA / MQA with
+    a causal or full mask; window_size, softcap, RoPE, heads_outer_fold and
+    learnable_sink run forward and raise NotImplementedError when a gradient
+    is requested (autograd.py:27-109).
     """
     del interpret
     window_size = check_common_kwargs(
@@ -262,7 +274,9 @@ def flash_attn_varlen_func(
     cu_seqlens_k None, seqused_k (batch,) each sequence's kv length.  Padding q
     rows return out 0, lse -inf; lse is (nheads, total_q).  block_sizes and
     guard_replay_unroll are accepted for compatibility (tiles are chosen by
-    this backend).
+    this backend).  RoPE tables as in flash_attn_func, positions per sequence
+    (Q at len_k - len_q + i); a paged cache takes rotary_k=False.  No backward:
+    a gradient request raises NotImplementedError (prefill.py:940-950).
     """
     del interpret
     window_size = check_common_kwargs(
@@ -360,17 +374,23 @@ def flash_attn_varlen_func(
         used_dev = int32_device(seqused_k, device, "seqused_k", (batch,))
         active = _num_active_tensor(num_active, batch, device)
         q = q.contiguous()
-        out, lse = paged_prefill(
-            q, k, cu_dev, used_dev,
-            bt.to(device=device, dtype=torch.int32).contiguous(),
-            active,
-            check_sinks(learnable_sink, nheads, device),
-            nheads_k=nkv, softmax_scale=resolve_scale(softmax_scale, d), softcap=float(softcap),
-            causal=causal, window_size=window_size,
-            k_descale=descale_scalar(k_descale, "k_descale"),
-            v_descale=descale_scalar(v_descale, "v_descale"),
-            max_seqlen_q=int(max_seqlen_q), return_lse=return_softmax_lse, token_major_q=False,
-            q_rotary=None if tables is None else (tables, rotary_interleaved))
+        sinks = check_sinks(learnable_sink, nheads, device)
+        bt_dev = bt.to(device=device, dtype=torch.int32).contiguous()
+        kd, vd = descale_scalar(k_descale, "k_descale"), descale_scalar(v_descale, "v_descale")
+
+        def run_paged(q, k, unused_v):
+            return paged_prefill(
+                q, k, cu_dev, used_dev, bt_dev, active, sinks,
+                nheads_k=nkv, softmax_scale=resolve_scale(softmax_scale, d),
+                softcap=float(softcap), causal=causal, window_size=window_size,
+                k_descale=kd, v_descale=vd, max_seqlen_q=int(max_seqlen_q),
+                return_lse=return_softmax_lse, token_major_q=False,
+                q_rotary=None if tables is None else (tables, rotary_interleaved))
+
+        if B.needs_grad(q, k):
+            out, lse = B.forward_only(run_paged, _VARLEN_FORWARD_ONLY, q, k, None)
+        else:
+            out, lse = run_paged(q, k, None)
         return (out, lse) if return_softmax_lse else out
     if seqused_k is not None or num_active is not None:
         raise ValueError("seqused_k and num_active describe a paged KV cache and need"
@@ -416,6 +436,7 @@ def flash_attn_varlen_func(
     _check_bf16(q, k, v)
     N.require_device(q, k, v)
     device = q.device
+    grad = B.needs_grad(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     cu_q_dev = int32_device(cu_q, device, "cu_seqlens_q")
     cu_k_dev = int32_device(cu_k, device, "cu_seqlens_k")
@@ -424,17 +445,25 @@ def flash_attn_varlen_func(
         # by the kernel as it loads it.
         k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=1,
                      nheads=nkv, ntokens=total_k, cu=cu_k_dev)
-    out = torch.empty_like(q)
-    lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
-           if return_softmax_lse else None)
-    _run_prefill(N.FW_KV_VARLEN, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
-                 ls=(0, total_q), batch=batch, nheads=nheads, nheads_k=nkv, head_dim=d,
-                 seqlen_q=total_q, seqlen_k=total_k, causal=causal, window_size=window_size,
-                 softmax_scale=resolve_scale(softmax_scale, d), softcap=softcap,
-                 sinks=check_sinks(learnable_sink, nheads, device),
-                 cu_q=cu_q_dev, cu_k=cu_k_dev,
-                 max_seqlen_q=int(max_seqlen_q),
-                 q_rotary=None if tables is None else (tables, rotary_interleaved))
+    sinks = check_sinks(learnable_sink, nheads, device)
+
+    def run_packed(q, k, v):
+        out = torch.empty_like(q)
+        lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
+               if return_softmax_lse else None)
+        _run_prefill(N.FW_KV_VARLEN, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+                     ls=(0, total_q), batch=batch, nheads=nheads, nheads_k=nkv, head_dim=d,
+                     seqlen_q=total_q, seqlen_k=total_k, causal=causal,
+                     window_size=window_size, softmax_scale=resolve_scale(softmax_scale, d),
+                     softcap=softcap, sinks=sinks, cu_q=cu_q_dev, cu_k=cu_k_dev,
+                     max_seqlen_q=int(max_seqlen_q),
+                     q_rotary=None if tables is None else (tables, rotary_interleaved))
+        return out, lse
+
+    if grad:
+        out, lse = B.forward_only(run_packed, _VARLEN_FORWARD_ONLY, q, k, v)
+    else:
+        out, lse = run_packed(q, k, v)
     if return_softmax_lse:
         return out, lse
     return out

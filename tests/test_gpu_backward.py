@@ -93,3 +93,27 @@ def test_backward_forward_only_configurations_raise():
     # no gradient requested: the same calls run as plain forwards
     with torch.no_grad():
         flash_attn_func(q, k, v, causal=True, window_size=(8, 0))
+
+
+def test_varlen_is_forward_only():
+    """prefill.py:940-950: flash_attn_varlen_func (packed and paged) runs its
+    forward and raises when a gradient is requested."""
+    announce("varlen forward-only")
+    from flywheel_tpu import flash_attn_varlen_func
+    rng = np.random.default_rng(63)
+    q = to_dev_bf16(randn(rng, (4, 40, 128))).requires_grad_()
+    k = to_dev_bf16(randn(rng, (2, 40, 128))).requires_grad_()
+    v = to_dev_bf16(randn(rng, (2, 40, 128)))
+    cu = torch.tensor([0, 15, 40], dtype=torch.int32, device=DEV)
+    out = flash_attn_varlen_func(q, k, v, cu, cu, 25, 25, causal=True)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        out.sum().backward()
+    with torch.no_grad():
+        ref = flash_attn_varlen_func(q, k, v, cu, cu, 25, 25, causal=True)
+    torch.testing.assert_close(out.detach(), ref, rtol=0, atol=0)
+    pool = torch.zeros(4, 16, 4, 128, dtype=torch.bfloat16, device=DEV)
+    table = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32, device=DEV)
+    out = flash_attn_varlen_func(q, pool, None, cu, None, 25, 32, causal=True, block_table=table,
+                                 seqused_k=torch.tensor([20, 30], dtype=torch.int32, device=DEV))
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        out.sum().backward()

@@ -77,6 +77,16 @@ def test_capi_validation_status_codes():
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED  # fp8 only for a paged pool
     assert lib.fw_append_ragged(None, None, None, None, None, None, None, 1, 0, 2, 128, 16, 1, 1,
                                 7, None) == N.FW_ERR_NOT_IMPLEMENTED
+    bw = N.AttnBwdParams()
+    bw.head_dim, bw.nheads, bw.nheads_k, bw.batch, bw.seqlen_q, bw.seqlen_k = 64, 4, 2, 1, 8, 8
+    assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_NOT_IMPLEMENTED
+    bw.head_dim, bw.nheads = 128, 3
+    assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_VALUE  # heads not a multiple of nheads_k
+    bw.nheads = 4
+    assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_VALUE  # no tensors, no workspace
+    assert lib.fw_attn_bwd_workspace_bytes(bw) >= 2 * 4 * 8 * 4  # row statistics
+    bw.nheads, bw.nheads_k, bw.seqlen_k = 16, 2, 520  # few key tiles: heads split, partials
+    assert lib.fw_attn_bwd_workspace_bytes(bw) > 2 * 2 * 520 * 128 * 4
     r = N.RotaryParams()
     r.head_dim, r.table_rows = 64, 8
     assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED
