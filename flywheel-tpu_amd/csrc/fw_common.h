@@ -90,6 +90,42 @@ __device__ __forceinline__ float fast_tanh(float x) {
   return 1.0f - 2.0f * __builtin_amdgcn_rcpf(t + 1.0f);
 }
 
+// softcap_log2 * tanh(x) for the scores of a wave (sc: an array of floats or
+// of float vectors, read and written through sc[i][e] / sc[e]).  When every
+// |x| of the wave is at most kTanhPolyBound the odd Taylor polynomial through
+// x^7 is used (truncation < 4.3e-7 there; four full-rate FMAs per score),
+// otherwise fast_tanh (two transcendentals); the choice is wave-uniform.
+constexpr float kTanhPolyBound = 0.3f;
+__device__ __forceinline__ float tanh_poly_scaled(float x, float c0, float c1, float c2, float c3) {
+  const float x2 = x * x;
+  float p = fmaf(x2, c3, c2);
+  p = fmaf(x2, p, c1);
+  p = fmaf(x2, p, c0);
+  return x * p;
+}
+template <int N, int M, typename Acc>
+__device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int e = 0; e < M; ++e) amax = fmaxf(amax, fabsf(sc[i][e]));
+  if (__any(amax > kTanhPolyBound)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int e = 0; e < M; ++e) sc[i][e] = fast_tanh(sc[i][e]) * softcap_log2;
+  } else {
+    // tanh x = x (1 - x^2/3 + 2x^4/15 - 17x^6/315 + ...), scaled by softcap_log2
+    const float c0 = softcap_log2, c1 = softcap_log2 * (-1.f / 3.f);
+    const float c2 = softcap_log2 * (2.f / 15.f), c3 = softcap_log2 * (-17.f / 315.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int e = 0; e < M; ++e) sc[i][e] = tanh_poly_scaled(sc[i][e], c0, c1, c2, c3);
+  }
+}
+
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }

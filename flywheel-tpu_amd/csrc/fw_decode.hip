@@ -277,15 +277,12 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
       for (int j = 0; j < 4; ++j) sacc[sub] = mfma16(k_operand<KV>(tl.krow[sub], j), qop[j], sacc[sub]);
     }
     // -------- online softmax on this lane's 8 (row n, key) scores
+    if (a.softcap_log2 != 0.f) softcap_scores<2, 4>(sacc, a.softcap_log2);
     float sc[8];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
-    if (a.softcap_log2 != 0.f) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sc[e] = fast_tanh(sc[e]) * a.softcap_log2;
-    }
     if (edge) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {

@@ -321,12 +321,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
       }
     }
     // ---------------- online softmax (log2 units), lane = query row n
-    if (a.softcap_log2 != 0.f) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
-    }
+    if (a.softcap_log2 != 0.f) softcap_scores<2, 16>(sacc, a.softcap_log2);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
     if (!full) {
@@ -648,12 +643,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
   // exponentiate again.  All exp2 arguments on the fast path are <= 16.
   auto softmax_pv = [&](int t, const FW_LDS uint8_t *buf, f32x16_t (&sacc)[2]) {
     const int kb = t * kKT;
-    if (a.softcap_log2 != 0.f) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[st][e] = fast_tanh(sacc[st][e]) * a.softcap_log2;
-    }
+    if (a.softcap_log2 != 0.f) softcap_scores<2, 16>(sacc, a.softcap_log2);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
     bool row_has_key = true;
