@@ -210,11 +210,12 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
       __syncthreads();
       if (t + 1 < t_end) gload(t + 1);
       const int qb = t * kBT;
-      // causal: no row of this tile sees any key of the wave
-      if (CAUSAL && qb + kBT - 1 + off < kw0) continue;
-      if (kw0 >= a.Sk) continue;
-      // every row of the tile sees every key of the wave (rows past Sq have
-      // lse_log2 = +inf, so p = 0 there without a mask)
+      // One code path for every tile (a skip here would make the compiler copy
+      // all dk / dv accumulators at the join): a tile whose rows see none of
+      // the wave's keys is fully masked, so its p and ds are 0; keys past Sk
+      // are zero rows whose results are never stored.  full: every row of the
+      // tile sees every key of the wave (rows past Sq have lse_log2 = +inf, so
+      // p = 0 there without a mask).
       const bool full = !CAUSAL || qb + off >= kw0 + 31;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
@@ -393,8 +394,6 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
   const int last_row = min(q0 + 127, a.Sq - 1);
   const int wg_hi = row_hi(last_row);
   const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
-  const int w_last = min(q0 + 32 * w + 31, a.Sq - 1);
-  const int w_hi = q0 + 32 * w < a.Sq ? row_hi(w_last) : 0;
   const int r_hi = row_hi(qrow);
 
   const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
@@ -420,7 +419,8 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
     __syncthreads();
     if (t + 1 < t_end) gload(t + 1);
     const int kb = t * kBT;
-    if (kb >= w_hi) continue;  // no row of the wave sees this tile
+    // One code path for every tile (no skip: the join would copy every dq
+    // accumulator); keys no row of the wave sees are masked to p = 0.
     const bool full = kb + kBT <= row_hi(q0 + 32 * w);
     bf16x8_t dsop[4];
 #pragma unroll
