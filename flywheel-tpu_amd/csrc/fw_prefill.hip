@@ -47,6 +47,7 @@ struct PrefillArgs {
   float qscale, softcap_log2, v_descale;
   const void *rcos, *rsin;  // fused Q RoPE tables, or null
   int rrows, rf32, ril;
+  int seqused_plus_q;  // paged: kv length = seqused_k + the sequence's q length
 };
 
 // RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7, at table
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
       kbase = a.cu_k[seq];
       sk_len = a.cu_k[seq + 1] - kbase;
     } else {
-      sk_len = a.seqused_k[seq];
+      sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
     }
   }
   const int hk = h / a.G;
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
       kbase = a.cu_k[seq];
       sk_len = a.cu_k[seq + 1] - kbase;
     } else {
-      sk_len = a.seqused_k[seq];
+      sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
     }
   }
   const int hk = h / a.G;
@@ -860,7 +861,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       kbase = a.cu_k[seq];
       sk_len = a.cu_k[seq + 1] - kbase;
     } else {
-      sk_len = a.seqused_k[seq];
+      sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
     }
   }
   const int hk = h / a.G;
@@ -1331,6 +1332,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.cu_q = p->cu_seqlens_q;
   a.cu_k = p->cu_seqlens_k;
   a.seqused_k = p->seqused_k;
+  a.seqused_plus_q = p->seqused_k_excludes_q ? 1 : 0;
   a.table = p->block_table;
   a.sinks = p->sinks;
   a.sched = (const int32_t *)p->workspace;

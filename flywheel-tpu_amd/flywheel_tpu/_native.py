@@ -64,6 +64,7 @@ class PrefillParams(ctypes.Structure):
         ("k_descale", _f32), ("v_descale", _f32),
         ("rotary_cos", _c_p), ("rotary_sin", _c_p),
         ("rotary_rows", _i32), ("rotary_f32", _i32), ("rotary_interleaved", _i32),
+        ("seqused_k_excludes_q", _i32),
     ]
 
 

@@ -44,7 +44,7 @@ enum fw_dtype {
 
 /* The last error message of the calling thread ("" if none). */
 const char *fw_last_error(void);
-/* ABI version of this header: 3. */
+/* ABI version of this header: 4. */
 int fw_abi_version(void);
 
 /*
@@ -187,6 +187,10 @@ typedef struct fw_prefill_params {
   const void *rotary_cos;
   const void *rotary_sin;
   int32_t rotary_rows, rotary_f32, rotary_interleaved;
+  /* Paged: when nonzero, seqused_k holds each sequence's kv length before its
+   * q rows were appended (the cache lengths of a chunked prefill), and the kv
+   * length is seqused_k[s] + cu_seqlens_q[s+1] - cu_seqlens_q[s]. */
+  int32_t seqused_k_excludes_q;
 } fw_prefill_params;
 
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} is declared but not exported"
     assert set(names) == set(N.SIGNATURES), "ctypes bindings and header disagree"
-    assert lib.fw_abi_version() == 3
+    assert lib.fw_abi_version() == 4
 
 
 def test_struct_layouts_match_header_fields():
