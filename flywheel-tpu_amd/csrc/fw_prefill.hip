@@ -813,7 +813,7 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
 
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * kPPBuf];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kPPBuf];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -914,7 +914,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)lds;
-  // Tile t goes from global memory straight into LDS buffer t % 3
+  // Tile t goes from global memory straight into LDS buffer t % 4
   // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
   // per instruction); this wave moves key rows 8w .. 8w+7.
   auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
@@ -936,9 +936,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     const uint32_t c16a = c16b ^ (16u * ((2 * wv) & 3)), c16c = c16b ^ (16u * ((2 * wv + 1) & 3));
     const uint32_t d = lds0 + (uint32_t)(8 * wv * kRowB) + (uint32_t)buf * kTileB;
     lds_dma16(kp, __umul24(lra, kstB) + c16a, d);
-    lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 3 * kTileB);
+    lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 4 * kTileB);
     lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
-    lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 3 * kTileB);
+    lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 4 * kTileB);
   };
   // Tile 0's copy goes out before the Q loads so the two latencies overlap.
   if (T > 0) dma_tile(0, 0, w);
@@ -972,7 +972,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
-      vofs[c][hh] = lds0 + 3 * kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
+      vofs[c][hh] = lds0 + 4 * kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
                     16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
 
   f32x16_t sacc[2];
@@ -1113,29 +1113,26 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // slots earlier) and fetches its rows of tile j+2+grp: group 0 carries key
   // rows 0-31 of each tile, group 1 rows 32-63.
   if (T > 0) {
-    // buffers 1 and 2 start as zeros (read by the spare PV of slot 0 and QK of
+    // buffers 1-3 start as zeros (read by the spare PV of slot 0 and the QK of
     // slot T before any tile lands there)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 6; ++i) {
       const uint32_t o = lds0 + kTileB + 16u * (tid + 512u * i);
       *(FW_LDS u32x4_t *)(o) = u32x4_t{0, 0, 0, 0};
-      *(FW_LDS u32x4_t *)(o + 3 * kTileB) = u32x4_t{0, 0, 0, 0};
+      *(FW_LDS u32x4_t *)(o + 4 * kTileB) = u32x4_t{0, 0, 0, 0};
     }
     __syncthreads();
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    // Tile 0 from every wave; group 1 also starts all rows of tile 1 here.
-    if (grp == 1 && T > 1) {
-      dma_tile(1, 1, w - 4);
+    // Tile 0 from every wave (issued before the Q loads); tile 1 likewise here.
+    if (T > 1) {
       dma_tile(1, 1, w);
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    if (grp == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     slot_barrier();  // tile 0 complete
     if (grp == 1) slot_barrier();
-    mslot_pre(2);  // the first PV multiplies P = 0 into zeroed buffer 2
-    // Unrolled by three so every buffer index is a compile-time constant.
+    mslot_pre(3);  // the first PV multiplies P = 0 into zeroed buffer 3
+    // Unrolled by four so every buffer index is a compile-time constant.
     auto body = [&](const int j, const auto bi, const auto pi) __attribute__((always_inline)) {
       // The address registers are opaque to the optimiser here, so the
       // per-buffer constants stay in the LDS instructions' offset fields
@@ -1153,31 +1150,39 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       // masked by the softmax, so their P is 0.
       // MFMA slot at raised priority: the other wave of this SIMD is in its
       // softmax slot and would otherwise win issue whenever it is the older.
-      // Tile t's buffer is free from slot 2t-2 and must be complete at the
-      // end of slot 2t-1: group 1 issues all of its rows in S(t-2) and waits
-      // at the end of M(t-1), so group 0's MFMA slots issue no copies.
+      // Four buffers: tile t+2 lands where tile t-2 was, free from slot 2t;
+      // each wave copies its own rows of it in its S(t) slot (slot 2t+1 for
+      // group 0, 2t+2 for group 1) and both are complete at the end of slot
+      // 2t+3 (group 0 waits at the end of S(t+1), group 1 at the end of
+      // M(t+1)), one slot before the first QK that reads it.  No MFMA slot
+      // issues copies.
       __builtin_amdgcn_s_setprio(2);
-      mslot(B, (B + 2) % 3, pops);
+      mslot(B, (B + 3) % 4, pops);
       __builtin_amdgcn_s_setprio(0);
       if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
-      if (grp == 1 && j + 2 < T) {
-        dma_tile(j + 2, (B + 2) % 3, w - 4);
-        dma_tile(j + 2, (B + 2) % 3, w);
-      }
+      const bool copy = j + 2 < T;
+      if (copy) dma_tile(j + 2, (B + 2) % 4, w);
       if (j < T) softmax(t_begin + j, pops);
       mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
+      if (grp == 0) {
+        if (copy) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // tile j+1 in
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
       slot_barrier();
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    for (int j = 0; j <= T; j += 3) {
+    using I3 = std::integral_constant<int, 3>;
+    for (int j = 0; j <= T; j += 4) {
       body(j, I0(), I0());
       if (j + 1 > T) break;
       body(j + 1, I1(), I0());
       if (j + 2 > T) break;
       body(j + 2, I2(), I0());
+      if (j + 3 > T) break;
+      body(j + 3, I3(), I0());
     }
     if (grp == 0) slot_barrier();
   }
