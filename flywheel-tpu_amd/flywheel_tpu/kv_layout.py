@@ -4,6 +4,14 @@ odd KV head count with one zero head."""
 
 import torch
 
+# Values the reference exports for its callers (config.py:40, :89; core/tpu.py:18):
+# pages here need only be a multiple of 16 (the kernels walk 16-key sub-tiles);
+# the block-size list and lane width keep the reference's values, and block sizes
+# built from them are accepted (tiles are chosen by this backend).
+PAGE_SIZE_MULTIPLE = 16
+FWD_BLOCKS = (2048, 1024, 512, 256, 128)
+NUM_LANES = 128
+
 MERGED_KV_DTYPES = (torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2)
 
 

@@ -273,3 +273,19 @@ def test_write_kv_cache_pages_errors():
 def test_package_surface():
     assert set(flywheel_tpu.__all__) >= {"flash_attn_func", "flash_attn_varlen_func",
                                          "flash_attn_with_kvcache"}
+
+
+def test_internal_exports_warn():
+    """flywheel_tpu/__init__.py:35-60: the names tpu-inference reads, each
+    access a FutureWarning; anything else an AttributeError."""
+    with pytest.warns(FutureWarning):
+        assert flywheel_tpu.PAGE_SIZE_MULTIPLE == 16
+    with pytest.warns(FutureWarning):
+        assert flywheel_tpu.FWD_BLOCKS[-1] % 128 == 0
+    with pytest.warns(FutureWarning):
+        assert flywheel_tpu.NUM_LANES == 128
+    with pytest.warns(FutureWarning):
+        mch = flywheel_tpu.merged_cache_heads
+    assert mch(8, torch.bfloat16) == 16 and mch(3, torch.float8_e4m3fn) == 8
+    with pytest.raises(AttributeError):
+        flywheel_tpu.not_an_export
