@@ -881,7 +881,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   const int w_last = min(w_first + 31, sq_len - 1);
   const bool w_any = w_first <= w_last;
   const int w_lo = w_any ? row_lo(w_first) : 0;
-  const int w_hi = w_any ? row_hi(w_last) : 0;
   const int qrow = q0 + 32 * w + n;
   const bool row_ok = qrow < sq_len;
   const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
@@ -1096,10 +1095,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
     l_run += psum;
   };
-  auto wave_needs = [&](int j) {
-    const int kb = (t_begin + j) * kKT;
-    return w_any && kb < w_hi && kb + kKT > w_lo;
-  };
   // End of slot: this wave's LDS reads and writes are complete, then all
   // waves meet (the register-staged global loads stay in flight).
   auto slot_barrier = [&]() {
@@ -1133,7 +1128,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     if (grp == 1) slot_barrier();
     mslot_pre(3);  // the first PV multiplies P = 0 into zeroed buffer 3
     // Unrolled by four so every buffer index is a compile-time constant.
-    auto body = [&](const int j, const auto bi, const auto pi) __attribute__((always_inline)) {
+    auto body = [&](const int j, const auto bi) __attribute__((always_inline)) {
       // The address registers are opaque to the optimiser here, so the
       // per-buffer constants stay in the LDS instructions' offset fields
       // instead of being hoisted into one register per buffer and step.
@@ -1142,7 +1137,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(vofs[c][0]), "+v"(vofs[c][1]));
       constexpr int B = decltype(bi)::value;
-      constexpr int P = decltype(pi)::value;
       // One code path for every slot (a branchy variant made the compiler
       // copy all 64 O registers at each join): the PV of slot 0 multiplies
       // P = 0 into a zeroed buffer, the QK of slot T reads a stale but finite
@@ -1176,13 +1170,13 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     for (int j = 0; j <= T; j += 4) {
-      body(j, I0(), I0());
+      body(j, I0());
       if (j + 1 > T) break;
-      body(j + 1, I1(), I0());
+      body(j + 1, I1());
       if (j + 2 > T) break;
-      body(j + 2, I2(), I0());
+      body(j + 2, I2());
       if (j + 3 > T) break;
-      body(j + 3, I3(), I0());
+      body(j + 3, I3());
     }
     if (grp == 0) slot_barrier();
   }
