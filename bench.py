@@ -270,7 +270,7 @@ def workload_c4(args, device):
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                   "traffic": read_traffic("c4"),
-                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_kernel<PAGED> (softcap; whole step)",
+                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_pp_kernel<PAGED, softcap> (whole step)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=None)
 

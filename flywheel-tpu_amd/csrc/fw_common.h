@@ -96,15 +96,19 @@ __device__ __forceinline__ float fast_tanh(float x) {
 // x^7 is used (truncation < 4.3e-7 there; four full-rate FMAs per score),
 // otherwise fast_tanh (two transcendentals); the choice is wave-uniform.
 constexpr float kTanhPolyBound = 0.3f;
-__device__ __forceinline__ float tanh_poly_scaled(float x, float c0, float c1, float c2, float c3) {
+template <bool ANCHOR>
+__device__ __forceinline__ float tanh_poly_scaled(float x, float c0, float c1, float c2, float c3,
+                                                  float anchor) {
   const float x2 = x * x;
   float p = fmaf(x2, c3, c2);
   p = fmaf(x2, p, c1);
   p = fmaf(x2, p, c0);
-  return x * p;
+  return ANCHOR ? fmaf(x, p, -anchor) : x * p;
 }
-template <int N, int M, typename Acc>
-__device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2) {
+// With ANCHOR, writes softcap_log2 * tanh(x) - anchor instead (the last
+// multiply becomes an FMA).
+template <int N, int M, bool ANCHOR = false, typename Acc>
+__device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2, float anchor = 0.f) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -114,7 +118,9 @@ __device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
 #pragma unroll
-      for (int e = 0; e < M; ++e) sc[i][e] = fast_tanh(sc[i][e]) * softcap_log2;
+      for (int e = 0; e < M; ++e)
+        sc[i][e] = ANCHOR ? fmaf(fast_tanh(sc[i][e]), softcap_log2, -anchor)
+                          : fast_tanh(sc[i][e]) * softcap_log2;
   } else {
     // tanh x = x (1 - x^2/3 + 2x^4/15 - 17x^6/315 + ...), scaled by softcap_log2
     const float c0 = softcap_log2, c1 = softcap_log2 * (-1.f / 3.f);
@@ -122,7 +128,8 @@ __device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
 #pragma unroll
-      for (int e = 0; e < M; ++e) sc[i][e] = tanh_poly_scaled(sc[i][e], c0, c1, c2, c3);
+      for (int e = 0; e < M; ++e)
+        sc[i][e] = tanh_poly_scaled<ANCHOR>(sc[i][e], c0, c1, c2, c3, anchor);
   }
 }
 

@@ -8,9 +8,8 @@
 // fwd_blocks.qk / online_softmax / pv (fwd_blocks.py:812-942), and the
 // schedule tables of schedule.py:617-717.
 //
-// Three forward kernels share one argument block and the q-tile schedule:
-//   fw_prefill_pp_kernel     bf16 K/V, no softcap: 8 waves, ping-pong schedule
-//   fw_prefill_kernel        bf16 K/V with softcap: 4 waves, two per CU
+// Two forward kernels share one argument block and the q-tile schedule:
+//   fw_prefill_pp_kernel     bf16 K/V: 8 waves, ping-pong schedule
 //   fw_prefill_staged_kernel fp8 paged pools: K/V widened to bf16 in registers
 // In all of them a wave owns 32 query rows, each lane one row, and computes
 //   S^T (32 keys x 32 rows) = K x Q^T        (Q^T resident in registers)
@@ -438,351 +437,6 @@ constexpr int kTileB = kKT * kRowB;        // 16 KiB per K or V tile
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define FW_LDS __attribute__((address_space(3)))
 
-// bf16 K/V with softcap: 4 waves = 128 rows, two workgroups per CU, two LDS
-// buffers (tile t computes from one while tile t+1 is fetched into registers
-// and stored into the other), one barrier per tile.
-template <int MODE>
-__global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
-  // Two buffers of [K tile | V tile], two objects so the compiler can prove a
-  // store into one never aliases operand reads from the other.
-  __shared__ __attribute__((aligned(1024))) uint8_t lds0[2 * kTileB];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds1[2 * kTileB];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int n = lane & 31;
-  const int g = lane >> 5;
-
-  // ------------------------------------------------------------ tile decode
-  int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
-  if constexpr (MODE == FW_KV_DENSE) {
-    const int nbh = a.B * a.H;
-    const int bid = blockIdx.x;
-    int qt, bh;
-    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
-      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
-      qt = a.n_qt - 1 - wi / hx;
-      bh = x * hx + wi % hx;
-    } else {
-      qt = a.n_qt - 1 - bid / nbh;
-      bh = bid % nbh;
-    }
-    b = bh / a.H;
-    h = bh % a.H;
-    q0 = qt * kQT;
-    sq_len = a.Sq;
-    sk_len = a.Sk;
-  } else {
-    if ((int)blockIdx.x >= a.sched[0]) return;
-    seq = a.sched[1 + 2 * blockIdx.x];
-    q0 = a.sched[2 + 2 * blockIdx.x];
-    h = blockIdx.y;
-    if (seq < 0) {  // packed padding rows: out 0, lse -inf
-      const int r0 = q0 + w * 32 + n;
-      if (r0 < a.Sq) {
-        uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
-        for (int d = g * 64; d < g * 64 + 64; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
-        if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
-      }
-      return;
-    }
-    qtok0 = a.cu_q[seq];
-    sq_len = a.cu_q[seq + 1] - qtok0;
-    if constexpr (MODE == FW_KV_VARLEN) {
-      kbase = a.cu_k[seq];
-      sk_len = a.cu_k[seq + 1] - kbase;
-    } else {
-      sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
-    }
-  }
-  const int hk = h / a.G;
-  const int off = sk_len - sq_len;  // bottom-right alignment
-  auto row_hi = [&](int r) {
-    const int p = r + off;
-    return a.wr >= 0 ? min(sk_len, p + a.wr + 1) : sk_len;
-  };
-  auto row_lo = [&](int r) {
-    const int p = r + off;
-    return a.wl >= 0 ? max(0, p - a.wl) : 0;
-  };
-  const int last_row = min(q0 + kQT, sq_len) - 1;
-  const int wg_lo = row_lo(q0);
-  const int wg_hi = row_hi(last_row);
-  const int w_first = q0 + 32 * w;
-  const int w_last = min(w_first + 31, sq_len - 1);
-  const bool w_any = w_first <= w_last;
-  const int w_lo = w_any ? row_lo(w_first) : 0;
-  const int w_hi = w_any ? row_hi(w_last) : 0;
-  const int qrow = q0 + 32 * w + n;
-  const bool row_ok = qrow < sq_len;
-  const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
-
-  // ------------------------------------------------------------ Q^T operand
-  bf16x8_t qop[8];
-  {
-    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
-                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
-    load_q_operand(a, qp, g, qs, qrow + off, qop);
-  }
-
-  f32x16_t oacc[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  const int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
-  const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
-
-  // ---- global -> LDS: wave w fills rows 16w .. 16w+15 of the K and V tiles,
-  // four rows (1 KiB) per instruction; lane l takes local row l/16 + 4i
-  // (LDS row 16w + 4i + l/16) and physical chunk l % 16, which holds logical
-  // chunk (l % 16) ^ swz(row) = (l % 16) ^ 4(l/16) ^ i.
-  // The row group's base address is wave-uniform (scalar registers); lanes add
-  // a 32-bit offset min(local row, last valid row) * row stride + chunk, so the
-  // clamp at the end of the sequence costs one v_min per row.
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const uint32_t lr0 = lane >> 4;
-  const uint32_t c16b = 16u * ((lane & 15) ^ (lr0 << 2));
-  uint32_t kstB, vstB;
-  const uint8_t *kbase_p = nullptr, *vbase_p = nullptr;
-  if constexpr (MODE == FW_KV_PAGED) {
-    kstB = vstB = (uint32_t)a.CH * 256u;
-  } else {
-    kstB = 2u * (uint32_t)a.kst;
-    vstB = 2u * (uint32_t)a.vst;
-    kbase_p = a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kbase * a.kst);
-    vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
-  }
-  // global -> registers (asynchronous loads, they never block issue); the
-  // chunks land in LDS later through store_tile with conflict-free
-  // ds_write_b128.  (global_load_lds stalls the issuing wave on this GPU.)
-  u32x4_t stg[8];
-  auto fetch_tile = [&](int t) {
-    const int kmax = sk_len - 1;
-    int key0 = min(t * kKT + 16 * wu, kmax);
-    const uint8_t *kp, *vp;
-    if constexpr (MODE == FW_KV_PAGED) {
-      key0 &= ~15;  // a 16-row group never straddles a page (P % 16 == 0)
-      int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
-      page = min(max(page, 0), a.num_pages - 1);
-      kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
-      vp = kp + 256;
-    } else {
-      kp = kbase_p + (size_t)key0 * kstB;
-      vp = vbase_p + (size_t)key0 * vstB;
-    }
-    const uint32_t lim = (uint32_t)(kmax - key0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lr = min(lr0 + 4u * i, lim);
-      const uint32_t c16 = c16b ^ (16u * i);
-      stg[i] = *(const u32x4_t *)(kp + (__umul24(lr, kstB) + c16));
-      stg[4 + i] = *(const u32x4_t *)(vp + (__umul24(lr, vstB) + c16));
-    }
-  };
-  auto store_tile = [&](FW_LDS uint8_t *kdst, FW_LDS uint8_t *vdst) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int off = (16 * w + 4 * i) * kRowB + 16 * lane;
-      *(FW_LDS u32x4_t *)(kdst + off) = stg[i];
-      *(FW_LDS u32x4_t *)(vdst + off) = stg[4 + i];
-    }
-  };
-
-  // ---- LDS operand addressing.  Every read is a per-lane base plus a
-  // compile-time offset (buffer, sub-tile, k-step).
-  // K (A of S^T): row r = 32st + n, physical chunk (2j+g) ^ swz(n): one base
-  // per step j.
-  int kofs[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kofs[j] = n * kRowB + 16 * ((2 * j + g) ^ swz(n));
-  // V (A of O^T, ds_read_b64_tr_b16): 16-lane group G covers dims
-  // 32c + 16(G&1) .. +15 for keys 16u + 8hh + 4(G>>1) + a; lane 4a+b points at
-  // dims +4b..+4b+3, i.e. logical chunk 4c + lo, lo = 2(G&1) + (b>>1).  With
-  // key & 15 = 8hh + 4kg + a the physical chunk is
-  // 4(c ^ a) + (lo ^ kg ^ 2hh): one base per (c, hh).
-  const int tr_i = lane & 15, tr_G = lane >> 4;
-  const int tr_a = tr_i >> 2, tr_b = tr_i & 3, tr_kg = tr_G >> 1;
-  const int tr_lo = 2 * (tr_G & 1) + (tr_b >> 1);
-  int vofs[4][2];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-      vofs[c][hh] = kTileB + (4 * tr_kg + tr_a) * kRowB + 64 * (c ^ tr_a) +
-                    16 * (tr_lo ^ tr_kg ^ (2 * hh)) + 8 * (tr_b & 1);
-
-  // ---- S^T = K Q^T for one tile: two 32-key sub-tiles; sub-tile 1's K
-  // operands are read while sub-tile 0's MFMAs run.
-  auto qk = [&](const FW_LDS uint8_t *buf, f32x16_t (&sacc)[2]) {
-    bf16x8_t kop0[8], kop1[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      kop0[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j]));
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[0][e] = sacc[1][e] = 0.f;
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kop1[j] = __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(buf + kofs[j] + 32 * kRowB));
-      sacc[0] = mfma32(kop0[j], qop[j], sacc[0]);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sacc[1] = mfma32(kop1[j], qop[j], sacc[1]);
-    __builtin_amdgcn_s_setprio(0);
-  };
-
-  // ---- online softmax (log2 units, lane = query row n) and O^T += V^T P^T.
-  // The anchor m_run is static: a tile is exponentiated against the current
-  // anchor, and only when that overflows the lane's partial row sum (> 2^16,
-  // i.e. a score more than ~11 above the anchor) or a row sees its first valid
-  // key does the wave take the slow path: row max, new anchor, O/l rescale,
-  // exponentiate again.  All exp2 arguments on the fast path are <= 16.
-  auto softmax_pv = [&](int t, const FW_LDS uint8_t *buf, f32x16_t (&sacc)[2]) {
-    const int kb = t * kKT;
-    if (a.softcap_log2 != 0.f) softcap_scores<2, 16>(sacc, a.softcap_log2);
-    const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
-                      kb + kKT <= sk_len;
-    bool row_has_key = true;
-    if (!full) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
-        }
-      row_has_key = max(r_lo, kb) < min(r_hi, kb + kKT);
-    }
-    bf16x8_t pop[4];
-    float psum;
-    auto exponentiate = [&](float m_use) {
-      psum = 0.f;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        u32x4_t pw;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e] - m_use);
-          const float p1 = fast_exp2(sacc[u >> 1][8 * (u & 1) + 2 * e + 1] - m_use);
-          psum += p0 + p1;
-          pw[e] = pack_bf16(p0, p1);
-        }
-        pop[u] = __builtin_bit_cast(bf16x8_t, pw);
-      }
-    };
-    exponentiate(m_run == -INFINITY ? 0.f : m_run);
-    if (__any(!(psum <= kPsumTrigger) || (m_run == -INFINITY && row_has_key))) {
-      asm volatile("" ::: "memory");  // a real branch: never if-converted
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[st][e]);
-      tmax = wave_max_xor(tmax, 32);
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      exponentiate(m_new == -INFINITY ? 0.f : m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
-    }
-    l_run += psum;
-    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles
-    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const FW_LDS uint8_t *src = buf + vofs[c][0] + 16 * u * kRowB;
-        const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)src);
-        const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (FW_LDS v4i16_t *)(buf + vofs[c][1] + (16 * u + 8) * kRowB));
-        dst[c] = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-    };
-    bf16x8_t vop[2][4];
-    read_v(0, vop[0]);
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
-    }
-    __builtin_amdgcn_s_setprio(0);
-  };
-  auto wave_needs = [&](int t) {
-    const int kb = t * kKT;
-    return w_any && kb < w_hi && kb + kKT > w_lo;
-  };
-
-  // ---- main loop: tile t computes from one buffer while tile t+1 is fetched
-  // (issued once the QK MFMAs are queued) and then stored into the other; one
-  // barrier per tile (this wave's LDS stores and operand reads done, no memory
-  // fence).
-  auto tile_barrier = [&]() {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-  };
-  auto step = [&](int t, const FW_LDS uint8_t *cur, FW_LDS uint8_t *kn, FW_LDS uint8_t *vn) {
-    const int tn = t + 1 < t_end ? t + 1 : -1;
-    const bool need = wave_needs(t);
-    f32x16_t sacc[2];
-    if (need) qk(cur, sacc);
-    if (tn >= 0) fetch_tile(tn);
-    if (need) softmax_pv(t, cur, sacc);
-    if (tn >= 0) store_tile(kn, vn);
-    tile_barrier();
-  };
-  FW_LDS uint8_t *kd0 = (FW_LDS uint8_t *)lds0, *vd0 = kd0 + kTileB;
-  FW_LDS uint8_t *kd1 = (FW_LDS uint8_t *)lds1, *vd1 = kd1 + kTileB;
-  if (t_begin < t_end) {
-    fetch_tile(t_begin);
-    store_tile(kd0, vd0);
-    tile_barrier();
-  }
-  for (int t = t_begin; t < t_end; t += 2) {
-    step(t, kd0, kd1, vd1);
-    if (t + 1 >= t_end) break;
-    step(t + 1, kd1, kd0, vd0);
-  }
-
-  // ------------------------------------------------------------ epilogue
-  l_run += __shfl_xor(l_run, 32, 64);
-  float M = m_run, Lsum = l_run, oscale = 1.f;
-  if (a.sinks) {
-    const float sk = a.sinks[h] * kLog2e;
-    if (sk != -INFINITY) {
-      const float Mn = fmaxf(M, sk);
-      const float c_old = fast_exp2(M - Mn);
-      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
-      oscale = c_old;
-      M = Mn;
-    }
-  }
-  if (!row_ok) return;
-  const bool any = Lsum > 0.f && l_run > 0.f;
-  const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
-  uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
-                          pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
-      *(u32x2_t *)(op + 32 * c + 8 * rr + 4 * g) = wv;
-    }
-  if (a.lse && g == 0) {
-    a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] =
-        Lsum > 0.f ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // bf16 K/V, ping-pong schedule.  Workgroup = 8 waves = 256 q rows of one query
 // head (wave w owns rows 32w .. 32w+31), one workgroup per CU, so each SIMD
@@ -794,10 +448,10 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_kernel(PrefillArgs a) {
 //   slot 2j+1 : group 0  softmax(j)         group 1  PV(j-1) QK(j)
 // The MFMA pipe and the VALU of a SIMD are then busy at the same time by
 // construction rather than by chance.
-// K/V tiles rotate through three LDS buffers (tile j in buffer j % 3), read in
-// slots 2j .. 2j+2; each half of a tile is written two slots after its loads
-// were issued and only after the buffer's previous tile has passed its last
-// reader's barrier.  All 8 waves share the loads (8 key rows each).
+// K/V tiles rotate through four LDS buffers (tile j in buffer j % 4) and
+// arrive by direct global->LDS copies; every wave copies its own 8 key rows of
+// tile j+2 in its softmax slot of tile j.  With softcap (SOFTCAP) the tanh
+// runs in the softmax slot too.
 constexpr int kPPWaves = 8;
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
@@ -811,7 +465,7 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
                :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
 }
 
-template <int MODE>
+template <int MODE, bool SOFTCAP>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kPPBuf];
 
@@ -1012,7 +666,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   };
   auto mslot = [&](const int bq, const int bp, const bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
     const uint32_t bufq = bq * kTileB, bufp = bp * kTileB;
-    const float m_init = m_run == -INFINITY ? 0.f : -m_run;
+    // the QK accumulates onto -anchor (with softcap onto 0: the anchor is
+    // subtracted after the tanh)
+    const float m_init = (SOFTCAP || m_run == -INFINITY) ? 0.f : -m_run;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < 32; ++st) {
@@ -1045,8 +701,10 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // O/l rescale, exponentiate again).
   auto softmax = [&](int t, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
     const int kb = t * kKT;
-    // the scores arrive as s - anchor (the MFMA accumulated onto -anchor)
+    // the scores arrive as s - anchor (the MFMA accumulated onto -anchor, or
+    // the softcap subtracts it)
     const float m_qk = m_run == -INFINITY ? 0.f : m_run;
+    if constexpr (SOFTCAP) softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
     bool row_has_key = true;
@@ -1285,21 +943,20 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
   return align_up((size_t)(1 + 2 * max_sched_tiles(p, kQT)) * sizeof(int32_t), 256);
 }
 
-// Kernel choice: bf16 K/V without softcap -> ping-pong kernel (256-row
-// tiles); with softcap the softmax is too heavy to hide behind one group's
-// MFMAs and the 4-wave kernel (128-row tiles, two per CU) is faster; fp8
-// pools -> register-staged kernel.
+// Kernel choice: bf16 K/V -> ping-pong kernel (256-row tiles; the softcap
+// variant is 3% faster on C4's shape than a 4-wave, two-per-CU kernel that
+// ran the tanh beside its own MFMAs); fp8 pools -> register-staged kernel.
 static bool use_pingpong(const fw_prefill_params *p) {
-  return p->kv_dtype == FW_BF16 && !(p->softcap > 0.f);
+  return p->kv_dtype == FW_BF16;
 }
 
 template <int MODE>
-static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, bool pingpong,
+static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype,
                         hipStream_t s) {
   switch (kv_dtype) {
     case FW_BF16:
-      if (pingpong) fw_prefill_pp_kernel<MODE><<<grid, 512, 0, s>>>(a);
-      else fw_prefill_kernel<MODE><<<grid, 256, 0, s>>>(a);
+      if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
+      else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
       break;
     case FW_FP8_E4M3:
       if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E4M3><<<grid, 256, 0, s>>>(a);
@@ -1371,8 +1028,8 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, pingpong, s);
-    return check_launch("fw_prefill_kernel");
+    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, s);
+    return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
   FW_REQUIRE(p->workspace_bytes >= fw_prefill_workspace_bytes(p), FW_ERR_VALUE,
@@ -1391,7 +1048,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   int st = check_launch("fw_prefill_schedule");
   if (st != FW_OK) return st;
   dim3 grid(max_tiles, p->nheads);
-  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, pingpong, s);
-  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, pingpong, s);
-  return check_launch("fw_prefill_kernel");
+  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, s);
+  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, s);
+  return check_launch("fw_prefill");
 }
