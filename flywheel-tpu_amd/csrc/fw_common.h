@@ -91,15 +91,23 @@ __device__ __forceinline__ float fast_tanh(float x) {
 }
 
 // softcap_log2 * tanh(x) for the scores of a wave (sc: an array of floats or
-// of float vectors, read and written through sc[i][e] / sc[e]).  When every
-// |x| of the wave is at most kTanhPolyBound, an odd degree-5 polynomial is
-// used: x (c0 + c1 x^2 + c2 x^4), minimax on [-0.3, 0.3] (abs error < 2.5e-7
-// with float32 evaluation; the Taylor polynomial through x^7 has 4.3e-7 there),
-// three full-rate FMAs and two multiplies per score; otherwise fast_tanh (two
-// transcendentals).  The choice is wave-uniform.  With ANCHOR the result is
-// softcap_log2 * tanh(x) - anchor (the last multiply becomes an FMA).
+// of float vectors, read and written through sc[i][e] / sc[e]).  By the
+// largest |x| of the wave (a wave-uniform choice):
+//   <= kTanhPoly3Bound: x (d0 + d1 x^2), minimax on [-0.12, 0.12];
+//   <= kTanhPolyBound:  x (c0 + c1 x^2 + c2 x^4), minimax on [-0.3, 0.3];
+//   else fast_tanh (two transcendentals).
+// Both polynomials stay below 2.5e-7 abs error with float32 evaluation (the
+// Taylor polynomial through x^7 has 4.3e-7 on [-0.3, 0.3]).  With ANCHOR the
+// result is softcap_log2 * tanh(x) - anchor (the last multiply becomes an FMA).
 constexpr float kTanhPolyBound = 0.3f;
 constexpr float kTanhC0 = 0.999995887f, kTanhC1 = -0.332973301f, kTanhC2 = 0.125218078f;
+constexpr float kTanhPoly3Bound = 0.12f;
+constexpr float kTanhD0 = 0.999990642f, kTanhD1 = -0.330870956f;
+template <bool ANCHOR>
+__device__ __forceinline__ float tanh_poly3_scaled(float x, float d0, float d1, float anchor) {
+  const float p = fmaf(x * x, d1, d0);
+  return ANCHOR ? fmaf(x, p, -anchor) : x * p;
+}
 template <bool ANCHOR>
 __device__ __forceinline__ float tanh_poly_scaled(float x, float c0, float c1, float c2,
                                                   float anchor) {
@@ -122,7 +130,7 @@ __device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2, floa
       for (int e = 0; e < M; ++e)
         sc[i][e] = ANCHOR ? fmaf(fast_tanh(sc[i][e]), softcap_log2, -anchor)
                           : fast_tanh(sc[i][e]) * softcap_log2;
-  } else {
+  } else if (__any(amax > kTanhPoly3Bound)) {
     const float c0 = softcap_log2 * kTanhC0, c1 = softcap_log2 * kTanhC1;
     const float c2 = softcap_log2 * kTanhC2;
 #pragma unroll
@@ -130,6 +138,13 @@ __device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2, floa
 #pragma unroll
       for (int e = 0; e < M; ++e)
         sc[i][e] = tanh_poly_scaled<ANCHOR>(sc[i][e], c0, c1, c2, anchor);
+  } else {
+    const float d0 = softcap_log2 * kTanhD0, d1 = softcap_log2 * kTanhD1;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int e = 0; e < M; ++e)
+        sc[i][e] = tanh_poly3_scaled<ANCHOR>(sc[i][e], d0, d1, anchor);
   }
 }
 
