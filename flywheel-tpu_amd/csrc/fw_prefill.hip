@@ -49,6 +49,23 @@ struct PrefillArgs {
   int seqused_plus_q;  // paged: kv length = seqused_k + the sequence's q length
 };
 
+// Varlen/paged workgroup -> (schedule slot, query head).  The heads of a slot
+// are consecutive workgroups, so slots start in schedule order (heaviest
+// first).  Workgroup bid runs on XCD bid % 8; when H % 8 == 0 XCD x takes
+// heads x*H/8 .. (x+1)*H/8 - 1 of every slot, i.e. whole GQA groups whenever
+// H/8 is a multiple of the group size, so their K/V stay in that XCD's L2.
+__device__ __forceinline__ void sched_slot(const PrefillArgs &a, int &slot, int &h) {
+  const int bid = blockIdx.x;
+  if (a.H % 8 == 0) {
+    const int x = bid & 7, wi = bid >> 3, hx = a.H >> 3;
+    slot = wi / hx;
+    h = x * hx + wi % hx;
+  } else {
+    slot = bid / a.H;
+    h = bid % a.H;
+  }
+}
+
 // RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7, at table
 // row tb / 64, in f32 with one rounding to bf16 (rotary.py:170-215).  Both
 // partners of every pair are in the lane: dims d and d + 64 are words j and
@@ -186,10 +203,11 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     sq_len = a.Sq;
     sk_len = a.Sk;
   } else {
-    if ((int)blockIdx.x >= a.sched[0]) return;
-    seq = a.sched[1 + 2 * blockIdx.x];
-    q0 = a.sched[2 + 2 * blockIdx.x];
-    h = blockIdx.y;
+    int slot;
+    sched_slot(a, slot, h);
+    if (slot >= a.sched[0]) return;
+    seq = a.sched[1 + 2 * slot];
+    q0 = a.sched[2 + 2 * slot];
     if (seq < 0) {  // packed padding rows: out 0, lse -inf
       const int r0 = q0 + w * 32 + n;
       for (int rr = 0; rr < 1; ++rr) {
@@ -496,10 +514,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     sq_len = a.Sq;
     sk_len = a.Sk;
   } else {
-    if ((int)blockIdx.x >= a.sched[0]) return;
-    seq = a.sched[1 + 2 * blockIdx.x];
-    q0 = a.sched[2 + 2 * blockIdx.x];
-    h = blockIdx.y;
+    int slot;
+    sched_slot(a, slot, h);
+    if (slot >= a.sched[0]) return;
+    seq = a.sched[1 + 2 * slot];
+    q0 = a.sched[2 + 2 * slot];
     if (seq < 0) {  // packed padding rows: out 0, lse -inf
       const int r0 = q0 + w * 32 + n;
       if (r0 < a.Sq) {
@@ -888,11 +907,19 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 
 // One workgroup: per-sequence q tiles from cu_seqlens_q, then padding tiles
 // for the packed rows past cu_seqlens_q[num_active] (schedule.py:617-717).
-__global__ __launch_bounds__(1024) void fw_prefill_schedule(const int32_t *cu_q,
-                                                            const int32_t *num_active, int B,
-                                                            int total_q, int32_t *sched,
-                                                            int max_tiles, int qt) {
+// When there are at most kSortTiles sequence tiles they are ordered by cost,
+// the number of 64-key tiles a q tile visits (its causal/window key range),
+// heaviest first, so the longest workgroups start first and the short ones
+// fill the tail (a greedy longest-first list schedule); padding tiles go last.
+// The order changes no result: every q tile is computed independently.
+constexpr int kSortTiles = 2048;
+__global__ __launch_bounds__(1024) void fw_prefill_schedule(
+    const int32_t *cu_q, const int32_t *num_active, int B, int total_q, int32_t *sched,
+    int max_tiles, int qt, const int32_t *cu_k, const int32_t *seqused_k, int plus_q, int wl,
+    int wr) {
   __shared__ int part[1024];
+  __shared__ unsigned long long key[kSortTiles];
+  __shared__ int eseq[kSortTiles], eq0[kSortTiles];
   const int tid = threadIdx.x;
   const int nact = num_active ? min(max(*num_active, 0), B) : B;
   const int per = (nact + 1023) / 1024;
@@ -907,18 +934,54 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(const int32_t *cu_q,
     part[tid] += v;
     __syncthreads();
   }
+  const int real = part[1023];
+  const bool sort = real <= kSortTiles;
   int idx = part[tid] - mine;
   for (int s = s0; s < s1; ++s) {
     const int len = cu_q[s + 1] - cu_q[s];
+    const int sk = cu_k ? cu_k[s + 1] - cu_k[s] : seqused_k[s] + (plus_q ? len : 0);
+    const int off = sk - len;  // bottom-right alignment, as in the kernels
     for (int q0 = 0; q0 < len; q0 += qt) {
-      if (idx < max_tiles) {
+      if (sort) {
+        const int last = min(q0 + qt, len) - 1;
+        const int lo = wl >= 0 ? max(0, q0 + off - wl) : 0;
+        const int hi = wr >= 0 ? min(sk, last + off + wr + 1) : sk;
+        const int cost = hi > lo ? (hi + kKT - 1) / kKT - lo / kKT : 0;
+        key[idx] = ((unsigned long long)cost << 32) | (unsigned)(idx + 1);
+        eseq[idx] = s;
+        eq0[idx] = q0;
+      } else if (idx < max_tiles) {
         sched[1 + 2 * idx] = s;
         sched[2 + 2 * idx] = q0;
       }
       ++idx;
     }
   }
-  const int real = part[1023];
+  if (sort) {
+    int n = 1;
+    while (n < real) n <<= 1;
+    for (int i = real + tid; i < n; i += 1024) key[i] = 0;  // below every real key
+    __syncthreads();
+    for (int k = 2; k <= n; k <<= 1)  // bitonic sort, descending
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < n; i += 1024) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const unsigned long long x = key[i], y = key[ixj];
+            if ((i & k) == 0 ? x < y : x > y) {
+              key[i] = y;
+              key[ixj] = x;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    for (int i = tid; i < real && i < max_tiles; i += 1024) {
+      const int e = (int)(unsigned)(key[i] & 0xffffffffu) - 1;
+      sched[1 + 2 * i] = eseq[e];
+      sched[2 + 2 * i] = eq0[e];
+    }
+  }
   const int pad0 = nact > 0 ? cu_q[nact] : 0;
   const int npad = total_q > pad0 ? (total_q - pad0 + qt - 1) / qt : 0;
   for (int i = tid; i < npad; i += 1024) {
@@ -1043,11 +1106,16 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   }
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);
+  const bool varlen = p->kv_mode == FW_KV_VARLEN;
   fw_prefill_schedule<<<1, 1024, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
-                                         (int32_t *)p->workspace, max_tiles, qt_rows);
+                                         (int32_t *)p->workspace, max_tiles, qt_rows,
+                                         varlen ? p->cu_seqlens_k : nullptr,
+                                         varlen ? nullptr : p->seqused_k, a.seqused_plus_q,
+                                         a.wl, a.wr);
   int st = check_launch("fw_prefill_schedule");
   if (st != FW_OK) return st;
-  dim3 grid(max_tiles, p->nheads);
+  // one workgroup per (schedule slot, query head); see sched_slot
+  dim3 grid(max_tiles * p->nheads);
   if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, s);
   else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, s);
   return check_launch("fw_prefill");

@@ -121,6 +121,34 @@ def test_flash_attn_varlen_packed(causal, window, softcap):
     assert np.isneginf(lses[:, cu_q[-1]:]).all()
 
 
+@pytest.mark.parametrize("nseq", [300, 2100])
+def test_flash_attn_varlen_many_sequences(nseq):
+    """Many short packed sequences: the tile schedule orders up to 2048 q tiles
+    by cost (300) and keeps the sequence order beyond that (2100)."""
+    announce(f"varlen packed many sequences n={nseq}")
+    rng = np.random.default_rng(15)
+    qlens = rng.integers(1, 5, nseq)
+    qlens[::97] = 300  # a few multi-tile sequences among the short ones
+    klens = qlens + rng.integers(0, 40, nseq)
+    h, hk, d = 2, 1, 128
+    cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    q = randn(rng, (h, cu_q[-1], d))
+    k = randn(rng, (hk, cu_k[-1], d))
+    v = randn(rng, (hk, cu_k[-1], d))
+    out = flash_attn_varlen_func(
+        to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), torch.tensor(cu_q, device=DEV),
+        torch.tensor(cu_k, device=DEV), int(qlens.max()), int(klens.max()), causal=True)
+    torch.cuda.synchronize()
+    outs = out.float().cpu().numpy()
+    for s in range(nseq):
+        qs = q[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2)[None]
+        ks = k[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        vs = v[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        ro, _ = A.attention_ref(qs, ks, vs, causal=True, round_scaled_q=True)
+        assert_close(outs[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2), ro[0], what=f"seq {s}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3", "e5m2"])
 def test_paged_varlen_read_only(dtype):
     """flash_attn_varlen_func(block_table=...) over a merged pool; reference
