@@ -589,13 +589,25 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // Tile t goes from global memory straight into LDS buffer t % 4
   // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
   // per instruction); this wave moves key rows 8w .. 8w+7.
-  auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
+  // Paged: the block-table entry of this wave's 8 rows of tile j.  In the
+  // loop it is fetched one softmax slot ahead by a scalar load issued from asm
+  // (table_sload) and is complete at that slot's closing barrier (lgkmcnt(0)),
+  // so the copy does not wait on a dependent load.
+  auto table_entry = [&](int j, const int wv) __attribute__((always_inline)) {
+    const int key0 = min((t_begin + j) * kKT + 8 * wv, sk_len - 1) & ~7;
+    return a.table + (size_t)seq * a.max_pages + key0 / a.P;
+  };
+  auto table_sload = [&](int j, const int wv) __attribute__((always_inline)) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0" : "=s"(v) : "s"(table_entry(j, wv)) : "memory");
+    return v;
+  };
+  auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
     int key0 = min((t_begin + j) * kKT + 8 * wv, kmax);
     const uint8_t *kp, *vp;
     if constexpr (MODE == FW_KV_PAGED) {
       key0 &= ~7;  // an 8-row group never straddles a page (P % 16 == 0)
-      int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
       page = min(max(page, 0), a.num_pages - 1);
       kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
       vp = kp + 256;
@@ -611,6 +623,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 4 * kTileB);
     lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
     lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 4 * kTileB);
+  };
+  auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
+    int page = 0;
+    if constexpr (MODE == FW_KV_PAGED) page = *table_entry(j, wv);
+    dma_tile_pg(j, buf, wv, page);
   };
   // Tile 0's copy goes out before the Q loads so the two latencies overlap.
   if (T > 0) dma_tile(0, 0, w);
@@ -795,6 +812,10 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
     __syncthreads();
     // Tile 0 from every wave (issued before the Q loads); tile 1 likewise here.
+    int page_next = 0;  // paged: table entry of tile j+2 in body j
+    if constexpr (MODE == FW_KV_PAGED) {
+      if (T > 2) page_next = table_sload(2, w);  // complete at the barrier below
+    }
     if (T > 1) {
       dma_tile(1, 1, w);
       asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -833,7 +854,12 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
       const bool copy = j + 2 < T;
-      if (copy) dma_tile(j + 2, (B + 2) % 4, w);
+      if (copy) {
+        dma_tile_pg(j + 2, (B + 2) % 4, w, page_next);
+        if constexpr (MODE == FW_KV_PAGED) {
+          if (j + 3 < T) page_next = table_sload(j + 3, w);  // for the next body
+        }
+      }
       if (j < T) softmax(t_begin + j, pops);
       mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
       if (grp == 0) {
