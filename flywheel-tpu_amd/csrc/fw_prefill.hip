@@ -946,21 +946,21 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
   __shared__ int part[1024];
   __shared__ unsigned long long key[kSortTiles];
   __shared__ int eseq[kSortTiles], eq0[kSortTiles];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nt = blockDim.x;  // nt: a power of two, 64 .. 1024
   const int nact = num_active ? min(max(*num_active, 0), B) : B;
-  const int per = (nact + 1023) / 1024;
+  const int per = (nact + nt - 1) / nt;
   const int s0 = tid * per, s1 = min(nact, s0 + per);
   int mine = 0;
   for (int s = s0; s < s1; ++s) mine += (cu_q[s + 1] - cu_q[s] + qt - 1) / qt;
   part[tid] = mine;
   __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {  // inclusive scan
+  for (int o = 1; o < nt; o <<= 1) {  // inclusive scan
     int v = tid >= o ? part[tid - o] : 0;
     __syncthreads();
     part[tid] += v;
     __syncthreads();
   }
-  const int real = part[1023];
+  const int real = part[nt - 1];
   const bool sort = real <= kSortTiles;
   int idx = part[tid] - mine;
   for (int s = s0; s < s1; ++s) {
@@ -986,11 +986,11 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
   if (sort) {
     int n = 1;
     while (n < real) n <<= 1;
-    for (int i = real + tid; i < n; i += 1024) key[i] = 0;  // below every real key
+    for (int i = real + tid; i < n; i += nt) key[i] = 0;  // below every real key
     __syncthreads();
     for (int k = 2; k <= n; k <<= 1)  // bitonic sort, descending
       for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < n; i += 1024) {
+        for (int i = tid; i < n; i += nt) {
           const int ixj = i ^ j;
           if (ixj > i) {
             const unsigned long long x = key[i], y = key[ixj];
@@ -1002,7 +1002,7 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
         }
         __syncthreads();
       }
-    for (int i = tid; i < real && i < max_tiles; i += 1024) {
+    for (int i = tid; i < real && i < max_tiles; i += nt) {
       const int e = (int)(unsigned)(key[i] & 0xffffffffu) - 1;
       sched[1 + 2 * i] = eseq[e];
       sched[2 + 2 * i] = eq0[e];
@@ -1010,7 +1010,7 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
   }
   const int pad0 = nact > 0 ? cu_q[nact] : 0;
   const int npad = total_q > pad0 ? (total_q - pad0 + qt - 1) / qt : 0;
-  for (int i = tid; i < npad; i += 1024) {
+  for (int i = tid; i < npad; i += nt) {
     if (real + i < max_tiles) {
       sched[1 + 2 * (real + i)] = -1;
       sched[2 + 2 * (real + i)] = pad0 + i * qt;
@@ -1133,7 +1133,10 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);
   const bool varlen = p->kv_mode == FW_KV_VARLEN;
-  fw_prefill_schedule<<<1, 1024, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
+  // one wave per 64 sequences (at most 16): fewer waves, cheaper barriers
+  int sched_threads = 64;
+  while (sched_threads < 1024 && sched_threads < p->batch) sched_threads <<= 1;
+  fw_prefill_schedule<<<1, sched_threads, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
                                          (int32_t *)p->workspace, max_tiles, qt_rows,
                                          varlen ? p->cu_seqlens_k : nullptr,
                                          varlen ? nullptr : p->seqused_k, a.seqused_plus_q,
