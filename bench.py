@@ -226,7 +226,9 @@ def workload_c3(args, device):
         cpu=cpu)
 
 
-def workload_c4(args, device):
+def workload_c4(args, device, fp8=False):
+    """C4; with fp8=True the same call over an e4m3 pool
+    (extra workload c4fp8: descales 0.8 / 1.25, values N(0,1) / descale)."""
     from flywheel_tpu import flash_attn_with_kvcache
     n, h, hk, d, page, window = 8, 32, 8, 128, 16, 4096
     rng = np.random.default_rng(0)
@@ -248,12 +250,23 @@ def workload_c4(args, device):
     q = torch.randn((tq, h, d), generator=gen, device=device, dtype=torch.bfloat16)
     kn = torch.randn((tq, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
     vn = torch.randn((tq, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    extra = {}
+    if fp8:
+        kd, vd = 0.8, 1.25
+        pool = pool.float()
+        pool[:, :, 0::2] /= kd
+        pool[:, :, 1::2] /= vd
+        pool = pool.to(torch.float8_e4m3fn)
+        kn = (kn.float() / kd).to(torch.float8_e4m3fn)
+        vn = (vn.float() / vd).to(torch.float8_e4m3fn)
+        extra = dict(k_descale=kd, v_descale=vd)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(chunks)]), dtype=torch.int32, device=device)
     lens = torch.tensor(prior, dtype=torch.int32, device=device)
     tab = torch.from_numpy(table).to(device)
     step = lambda: flash_attn_with_kvcache(
         q, pool, None, kn, vn, cache_seqlens=lens, block_table=tab, cu_seqlens_q=cu,
-        max_seqlen_q=int(chunks.max()), causal=True, window_size=(window - 1, 0), softcap=50.0)
+        max_seqlen_q=int(chunks.max()), causal=True, window_size=(window - 1, 0), softcap=50.0,
+        **extra)
     ms = timed(step, args.steps, args.warmup)
     pairs = 0
     for p, c in zip(prior, chunks):
@@ -262,15 +275,18 @@ def workload_c4(args, device):
     flops = 4.0 * h * d * pairs
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(
-        name="c4", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        name="c4fp8" if fp8 else "c4", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
         config={"workload": "ragged chunked prefill over paged cache (append + attend)",
+                "kv_cache": "e4m3" if fp8 else "bf16",
                 "requests": n, "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
                 "window_size": [window - 1, 0], "softcap": 50.0, "total_q": tq,
                 "visible_pairs": pairs},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                  "traffic": read_traffic("c4"),
-                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_pp_kernel<PAGED, softcap> (whole step)",
+                  "traffic": None if fp8 else read_traffic("c4"),
+                  "kernel": "fw_append_kernel + fw_prefill_schedule + " + (
+                      "fw_prefill_staged_kernel<PAGED, e4m3>" if fp8
+                      else "fw_prefill_pp_kernel<PAGED, softcap>") + " (whole step)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=None)
 
@@ -390,7 +406,8 @@ def workload_rope(args, device):
 
 
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
-EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope}
+EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope,
+         "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 
 
 def main():
