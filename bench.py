@@ -39,7 +39,9 @@ import torch  # noqa: E402
 METRIC = "paged decode HBM GB/s (% of 8 TB/s); prefill TFLOP/s (% MFMA peak)"
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
-CPU_THREADS = 16
+# The CPU oracle's BLAS threads: the host's cores, at most 16 (the GPU box's
+# CPU share for one GPU).
+CPU_THREADS = min(16, os.cpu_count() or 1)
 
 
 def log(msg):
@@ -99,6 +101,30 @@ def read_traffic(name):
     return None
 
 
+def cpu_info(sample, value, unit):
+    """A cpu_baseline record: the threads actually used and the host's CPU
+    count beside the measured value."""
+    return {"value": value, "unit": unit, "cores": CPU_THREADS,
+            "host_cpus": os.cpu_count(), "kind": "port", "sample": sample}
+
+
+def seq_values(pool, table_np, row, length, hk):
+    """(length, Hk, D) K and V values (f32, stored / not yet descaled) of
+    one sequence of a device pool, gathered on the host."""
+    from oracle import paged as P
+    from oracle.dtypes import bf16_to_f32, fp8_decode
+    page = pool.shape[1]
+    pos = np.arange(length)
+    pages = table_np[row, pos // page]
+    sel = pool[torch.from_numpy(pages).to(pool.device), torch.from_numpy(pos % page).to(pool.device)]
+    if pool.dtype == torch.bfloat16:
+        vals = bf16_to_f32(sel.view(torch.int16).cpu().numpy().view(np.uint16))
+    else:
+        fmt = "e4m3" if pool.dtype == torch.float8_e4m3fn else "e5m2"
+        vals = fp8_decode(sel.view(torch.uint8).cpu().numpy(), fmt)
+    return P.split_kv_heads(vals, hk)
+
+
 def cpu_limits():
     try:
         from threadpoolctl import threadpool_limits
@@ -155,10 +181,9 @@ def workload_c2(args, device):
         vc = rng.standard_normal((1, s, 2, d), dtype=np.float32)
         with cpu_limits():
             t = cpu_time(lambda: A.attention_ref(qc, kc, vc, causal=True))
-        return {"value": round(4.0 * s * s * heads * d / 2 / t / 1e12, 5), "unit": "TFLOP/s",
-                "cores": CPU_THREADS, "kind": "port",
-                "sample": "oracle.attention_ref, 8 of 32 heads (2 KV heads) at full 4096 causal,"
-                          " median of 3 after 1 warm-up"}
+        return cpu_info("oracle.attention_ref, 8 of 32 heads (2 KV heads) at full 4096 causal,"
+                        " median of 3 after 1 warm-up",
+                        round(4.0 * s * s * heads * d / 2 / t / 1e12, 5), "TFLOP/s")
 
     return dict(
         name="c2", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
@@ -171,8 +196,9 @@ def workload_c2(args, device):
         cpu=cpu)
 
 
-def workload_c3(args, device):
-    from flywheel_tpu import flash_attn_with_kvcache
+def inputs_c3(device):
+    """the seeded C3 draw (also used by the full-size
+    parity test)."""
     b, h, hk, d, page = 64, 32, 8, 128, 16
     rng = np.random.default_rng(0)
     lengths = rng.integers(1024, 32768 + 1, b)
@@ -182,6 +208,16 @@ def workload_c3(args, device):
     kn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
     vn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
     lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    return dict(b=b, h=h, hk=hk, d=d, page=page, lengths=lengths, pool=pool, table=table,
+                table_np=table_np, q=q, kn=kn, vn=vn, lens=lens)
+
+
+def workload_c3(args, device):
+    from flywheel_tpu import flash_attn_with_kvcache
+    x = inputs_c3(device)
+    b, h, hk, d, page, lengths = x["b"], x["h"], x["hk"], x["d"], x["page"], x["lengths"]
+    pool, table, table_np, q, kn, vn, lens = (x[k] for k in ("pool", "table", "table_np", "q", "kn",
+                                                            "vn", "lens"))
     step = lambda: flash_attn_with_kvcache(q, pool, None, kn, vn, cache_seqlens=lens,
                                            block_table=table)
     ms = timed(step, args.steps, args.warmup)
@@ -192,27 +228,20 @@ def workload_c3(args, device):
 
     def cpu():
         from oracle import attention as A
-        from oracle import paged as P
         rows = 4  # sample: 4 of the 64 rows, gathered from the same pool
-        pl = pool.view(torch.int16)
+        tot = lengths[:rows] + 1
+        cap = int(tot.max())
+        krows = np.zeros((rows, cap, hk, d), np.float32)
+        vrows = np.zeros_like(krows)
+        for r in range(rows):
+            krows[r, :tot[r]], vrows[r, :tot[r]] = seq_values(pool, table_np, r, int(tot[r]), hk)
+        qn = q[:rows].float().cpu().numpy()
         with cpu_limits():
-            sel = list(range(rows))
-            tabs = table_np[sel]
-            used = np.unique(tabs)
-            codes = pl[torch.from_numpy(used).to(device)].cpu().numpy().view(np.uint16)
-            remap = {int(p): i for i, p in enumerate(used)}
-            tloc = np.vectorize(lambda p: remap[int(p)])(tabs)
-            from oracle.dtypes import bf16_to_f32
-            kp, vp = P.split_kv_heads(bf16_to_f32(codes), hk)
-            krows, vrows = P.gather_rows(kp, tloc), P.gather_rows(vp, tloc)
-            qn = q[:rows].float().cpu().numpy()
-            tot = lengths[:rows] + 1
             t = cpu_time(lambda: A.kvcache_reference(qn, krows, vrows, tot))
         sample_bytes = float(np.sum(tot)) * row_bytes
-        return {"value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": CPU_THREADS,
-                "kind": "port",
-                "sample": f"oracle.kvcache_reference on rows 0..{rows - 1} of the same pool"
-                          f" ({int(np.sum(tot))} keys), median of 3 after 1 warm-up"}
+        return cpu_info(f"oracle.kvcache_reference on rows 0..{rows - 1} of the same pool"
+                        f" ({int(np.sum(tot))} keys), median of 3 after 1 warm-up",
+                        round(sample_bytes / t / 1e9, 3), "GB/s")
 
     return dict(
         name="c3", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
@@ -226,10 +255,9 @@ def workload_c3(args, device):
         cpu=cpu)
 
 
-def workload_c4(args, device, fp8=False):
-    """C4 (BASELINE configs[3]); with fp8=True the same call over an e4m3 pool
-    (extra workload c4fp8: descales 0.8 / 1.25, values N(0,1) / descale)."""
-    from flywheel_tpu import flash_attn_with_kvcache
+def inputs_c4(device, fp8=False):
+    """the seeded C4 draw; with fp8 the same draw over an
+    e4m3 pool (descales 0.8 / 1.25, values N(0,1) / descale)."""
     n, h, hk, d, page, window = 8, 32, 8, 128, 16, 4096
     rng = np.random.default_rng(0)
     chunks = rng.integers(256, 2048 + 1, n)
@@ -263,6 +291,20 @@ def workload_c4(args, device, fp8=False):
     cu = torch.tensor(np.concatenate([[0], np.cumsum(chunks)]), dtype=torch.int32, device=device)
     lens = torch.tensor(prior, dtype=torch.int32, device=device)
     tab = torch.from_numpy(table).to(device)
+    return dict(n=n, h=h, hk=hk, d=d, page=page, window=window, chunks=chunks, prior=prior,
+                pool=pool, q=q, kn=kn, vn=vn, cu=cu, lens=lens, tab=tab, table_np=table,
+                extra=extra, tq=tq)
+
+
+def workload_c4(args, device, fp8=False):
+    """C4 (BASELINE configs[3]); with fp8=True the same call over an e4m3 pool
+    (extra workload c4fp8: descales 0.8 / 1.25, values N(0,1) / descale)."""
+    from flywheel_tpu import flash_attn_with_kvcache
+    x = inputs_c4(device, fp8)
+    n, h, hk, d, page, window = x["n"], x["h"], x["hk"], x["d"], x["page"], x["window"]
+    chunks, prior, pool, q, kn, vn, cu, lens, tab, extra, tq = (
+        x[k] for k in ("chunks", "prior", "pool", "q", "kn", "vn", "cu", "lens", "tab", "extra",
+                       "tq"))
     step = lambda: flash_attn_with_kvcache(
         q, pool, None, kn, vn, cache_seqlens=lens, block_table=tab, cu_seqlens_q=cu,
         max_seqlen_q=int(chunks.max()), causal=True, window_size=(window - 1, 0), softcap=50.0,
@@ -274,6 +316,27 @@ def workload_c4(args, device, fp8=False):
         pairs += int(vis.sum())
     flops = 4.0 * h * d * pairs
     tflops = flops / (ms * 1e-3) / 1e12
+
+    def cpu():
+        from oracle import attention as A
+        # sample: the request with the fewest visible pairs, all 32 heads
+        vis = [int(np.minimum(p + np.arange(c) + 1, window).sum()) for p, c in zip(prior, chunks)]
+        s_ = int(np.argmin(vis))
+        total = int(prior[s_] + chunks[s_])
+        k, v = seq_values(pool, x["table_np"], s_, total, hk)
+        c0 = int(np.sum(chunks[:s_]))
+        qs = q[c0:c0 + int(chunks[s_])].float().cpu().numpy()
+        kw = dict(causal=True, window_left=window - 1, softcap=50.0, round_scaled_q=True,
+                  **({"k_descale": extra["k_descale"], "v_descale": extra["v_descale"]}
+                     if fp8 else {}))
+        with cpu_limits():
+            t = cpu_time(lambda: A.ragged_reference(qs, k[None], v[None],
+                                                    np.array([0, chunks[s_]]), np.array([total]),
+                                                    np.zeros((1, 1), np.int64), **kw))
+        return cpu_info(f"oracle.ragged_reference on request {s_} (prior {int(prior[s_])}, chunk"
+                        f" {int(chunks[s_])}, {vis[s_]} visible pairs x 32 heads), median of 3"
+                        " after 1 warm-up", round(4.0 * h * d * vis[s_] / t / 1e12, 5), "TFLOP/s")
+
     return dict(
         name="c4fp8" if fp8 else "c4", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
         config={"workload": "ragged chunked prefill over paged cache (append + attend)",
@@ -288,38 +351,69 @@ def workload_c4(args, device, fp8=False):
                       "fw_prefill_staged_kernel<PAGED, e4m3>" if fp8
                       else "fw_prefill_pp_kernel<PAGED, softcap>") + " (whole step)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
-        cpu=None)
+        cpu=cpu)
 
 
-def workload_c5(args, device):
-    from flywheel_tpu import flash_attn_with_kvcache
+def inputs_c5(device):
+    """the seeded C5 draw (e4m3 pool, 4-token window)."""
     b, h, hk, d, page, sq = 128, 32, 8, 128, 16, 4
     rng = np.random.default_rng(0)
     lengths = rng.integers(4096, 65536 + 1, b)
     k_descale, v_descale = (float(x) for x in rng.uniform(0.5, 2.0, 2))
     gen = torch.Generator(device=device).manual_seed(0)
-    pool, table, _ = paged_pool(gen, rng, lengths, sq, hk, d, page, torch.float8_e4m3fn, device,
-                                descales=(k_descale, v_descale))
+    pool, table, table_np = paged_pool(gen, rng, lengths, sq, hk, d, page, torch.float8_e4m3fn,
+                                       device, descales=(k_descale, v_descale))
     q = torch.randn((b, sq, h, d), generator=gen, device=device, dtype=torch.bfloat16)
     kn = (torch.randn((b, sq, hk, d), generator=gen, device=device) / k_descale).to(torch.float8_e4m3fn)
     vn = (torch.randn((b, sq, hk, d), generator=gen, device=device) / v_descale).to(torch.float8_e4m3fn)
     lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    return dict(b=b, h=h, hk=hk, d=d, page=page, sq=sq, lengths=lengths, k_descale=k_descale,
+                v_descale=v_descale, pool=pool, table=table, table_np=table_np, q=q, kn=kn, vn=vn,
+                lens=lens)
+
+
+def workload_c5(args, device):
+    from flywheel_tpu import flash_attn_with_kvcache
+    x = inputs_c5(device)
+    b, h, hk, d, page, sq, lengths = (x[k] for k in ("b", "h", "hk", "d", "page", "sq", "lengths"))
+    k_descale, v_descale, pool, table, q, kn, vn, lens = (
+        x[k] for k in ("k_descale", "v_descale", "pool", "table", "q", "kn", "vn", "lens"))
     step = lambda: flash_attn_with_kvcache(q, pool, None, kn, vn, cache_seqlens=lens,
                                            block_table=table, causal=True, k_descale=k_descale,
                                            v_descale=v_descale)
     ms = timed(step, args.steps, args.warmup)
     nbytes = float(np.sum(lengths + sq)) * 2 * hk * d * 1
     gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def cpu():
+        from oracle import attention as A
+        rows = 2  # sample: rows 0 and 1 of the same pool, fp8 decoded to f32
+        tot = lengths[:rows] + sq
+        cap = int(tot.max())
+        krows = np.zeros((rows, cap, hk, d), np.float32)
+        vrows = np.zeros_like(krows)
+        for r in range(rows):
+            krows[r, :tot[r]], vrows[r, :tot[r]] = seq_values(pool, x["table_np"], r, int(tot[r]), hk)
+        qn = q[:rows].float().cpu().numpy()
+        with cpu_limits():
+            t = cpu_time(lambda: A.kvcache_reference(qn, krows, vrows, tot, causal=True,
+                                                     k_descale=k_descale, v_descale=v_descale))
+        sample_bytes = float(np.sum(tot)) * 2 * hk * d
+        return cpu_info(f"oracle.kvcache_reference on rows 0..{rows - 1} of the same pool"
+                        f" ({int(np.sum(tot))} keys, e4m3 decoded to f32), median of 3 after 1"
+                        " warm-up", round(sample_bytes / t / 1e9, 3), "GB/s")
+
     return dict(
         name="c5", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
         config={"workload": "fp8 e4m3 paged decode, 4-token verify window", "batch": b,
                 "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
-                "ctx": "U[4096, 65536]", "k_descale": k_descale, "v_descale": v_descale},
+                "kv_cache": "e4m3", "ctx": "U[4096, 65536]", "k_descale": k_descale,
+                "v_descale": v_descale},
         roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic("c5"),
                   "kernel": "fw_append_kernel + fw_decode_kernel<e4m3> + fw_decode_combine (whole step)",
                   "algorithmic_per_launch": f"{nbytes:.4e} B"},
-        cpu=None)
+        cpu=cpu)
 
 
 def workload_copy(args, device):
@@ -368,10 +462,9 @@ def workload_bwd(args, device):
         qc, kc, vc, dc = x(heads), x(1), x(1), x(heads)
         with cpu_limits():
             t = cpu_time(lambda: OB.attention_bwd_ref(qc, kc, vc, dc, causal=True), min_rounds=1)
-        return {"value": round(2.5 * 4.0 * s * s * heads * d / 2 / t / 1e12, 5), "unit": "TFLOP/s",
-                "cores": CPU_THREADS, "kind": "port",
-                "sample": "oracle.backward.attention_bwd_ref (float64), 2 of 32 heads at full"
-                          " 4096 causal"}
+        return cpu_info("oracle.backward.attention_bwd_ref (float64), 2 of 32 heads at full"
+                        " 4096 causal", round(2.5 * 4.0 * s * s * heads * d / 2 / t / 1e12, 5),
+                        "TFLOP/s")
 
     return dict(
         name="bwd", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void fw_append_kernel(
     const int32_t *table, const int32_t *num_active, int B, int T, int Hk, int head_bytes, int CH,
     int P, int num_pages, int max_pages) {
   const int i = blockIdx.x;
-  const int nact = num_active ? min(*num_active, B) : B;
+  const int nact = num_active ? min(max(*num_active, 0), B) : B;
   int r, first;
   if (cu) {
     if (i >= cu[nact]) return;  // rows past the last active request are padding
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void fw_write_pages_kernel(
 using namespace fw;
 
 extern "C" const char *fw_last_error(void) { return g_last_error.c_str(); }
-extern "C" int fw_abi_version(void) { return 4; }
+extern "C" int fw_abi_version(void) { return 5; }
 
 extern "C" int fw_append_ragged(void *kv_cache, const void *k, const void *v,
                                 const int32_t *cu_seqlens, const int32_t *cache_seqlens,

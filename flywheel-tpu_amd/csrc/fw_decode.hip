@@ -36,8 +36,8 @@ struct DecodeArgs {
   const int32_t *cache_seqlens;
   const int32_t *block_table;
   const int32_t *num_active;
-  float *ws_o;   // [items][16][128] unnormalised partial O
-  float2 *ws_ml; // [items][16] (running max in log2 units, row sum)
+  float *ws_o;   // [items][rows_item][128] unnormalised partial O
+  float2 *ws_ml; // [items][rows_item] (running max in log2 units, row sum)
   int B, Sq, H, Hk, G, Rq, n_qtiles, P, max_pages, CH;
   // Token-row geometry: a token row holds CH head rows; KV head h's K row is
   // head row kstep*h and its V row head row kstep*h + vhead, vdelta bytes
@@ -47,14 +47,20 @@ struct DecodeArgs {
   int64_t vdelta;
   int split_keys, nsplit;
   int seqlen_add, has_new, causal, window_left, num_pages;
+  int rows_item;      // partial rows stored per work item: min(16, Rq)
   float qscale;       // folded into q before its bf16 rounding
   float softcap_log2; // softcap * log2(e), 0 = off
+  // Device descale scalars (or null: k_descale is already in qscale).  With
+  // kd the kernel forms qscale = (sm_scale * kd) * log2e, or / softcap, in
+  // the host's operation order.
+  const float *kd;
+  float sm_scale, softcap;
 };
 
 constexpr int kD = 128;
 constexpr float kPsumTrigger = 65536.f;  // lane partial-sum bound of the fast path
-constexpr int kStageRow = 132;
-constexpr int kTblPerLane = 4;            // block-table entries a lane prefetches per split           // padded f32 row of the partial-O staging slot
+constexpr int kStageRow = 132;           // padded f32 row of the partial-O staging slot
+constexpr int kTblPerLane = 4;           // block-table entries a lane prefetches per split
 
 // Visible key range of a row: [lo, total) overall; per folded row the causal
 // limit drops by (Sq - 1 - t).
@@ -112,6 +118,7 @@ struct DecodeTile {
   KRow<KV> krow[2];  // K of the two 16-key sub-tiles (lane row n)
   // V of keys 4g+i / 16+4g+i, dims 8n .. 8n+7 (16 or 8 bytes a key)
   typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8];
+  bool bad[2];  // a sub-tile's page id is out of range: its keys are masked
 };
 
 
@@ -151,8 +158,10 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
 
   // ---- fused append: the last split's wave of q tile 0 writes the new row.
   // (A row already at its capacity has no slot: nothing is written.)
-  if (a.has_new && qt == 0 && s == nsplit_row - 1 && L0 / a.P < a.max_pages) {
-    const int page = min(max(table[L0 / a.P], 0), a.num_pages - 1);
+  // An out-of-range page id is never written (as in fw_append_kernel).
+  const int new_page = a.has_new && L0 / a.P < a.max_pages ? table[L0 / a.P] : -1;
+  if (a.has_new && qt == 0 && s == nsplit_row - 1 && new_page >= 0 && new_page < a.num_pages) {
+    const int page = new_page;
     uint8_t *dst = a.cache + ((size_t)page * a.P + L0 % a.P) * row_bytes;
     const size_t hb = (size_t)kD * EB;  // bytes of one head row
     const uint8_t *kn = a.k_new + ((size_t)b * a.Hk + h) * hb;
@@ -175,6 +184,11 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   const bool row_ok = r < a.Rq;
   const int tok = row_ok ? r / a.G : 0;
   const int hq = h * a.G + (row_ok ? r % a.G : 0);
+  float qscale = a.qscale;
+  if (a.kd) {
+    const float sm = a.sm_scale * *a.kd;
+    qscale = a.softcap > 0.f ? sm / a.softcap : sm * kLog2e;
+  }
   bf16x8_t qop[4];
   {
     const uint16_t *qrow = a.q + (((size_t)b * a.Sq + tok) * a.H + hq) * kD;
@@ -184,7 +198,7 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
       u32x4_t o;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        o[e] = row_ok ? pack_bf16(bf16_lo(w[e]) * a.qscale, bf16_hi(w[e]) * a.qscale) : 0u;
+        o[e] = row_ok ? pack_bf16(bf16_lo(w[e]) * qscale, bf16_hi(w[e]) * qscale) : 0u;
       qop[j] = __builtin_bit_cast(bf16x8_t, o);
     }
   }
@@ -211,39 +225,51 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
 #pragma unroll
   for (int t = 0; t < kTblPerLane; ++t) tbl_lane[t] = table[min(first_page + 64 * t + lane, a.max_pages - 1)];
 
+  // Cache keys of this split are [k_begin, k_stop): the appended token (key
+  // L0) is folded in after the loop from k_new / v_new.
+  const int k_stop = a.has_new ? min(k_end, L0) : k_end;
+  const int last_cache_key = k_stop - 1;
   // Per-lane byte offsets inside a 16-row sub-tile: a load is the sub-tile's
-  // uniform page row pointer plus a 32-bit lane offset.
-  const uint32_t k_lane_off = (uint32_t)(n * row_bytes + kh_off);
-  uint32_t v_lane_off[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    v_lane_off[i] = (uint32_t)((4 * g + i) * row_bytes + vh_off + (KV == FW_BF16 ? 16 : 8) * n);
+  // uniform page row pointer plus a 32-bit lane offset.  Rows past the last
+  // cache key of the split (slots not written yet: their contents may be
+  // anything, NaN included, and 0 * NaN would poison the PV product) are
+  // clamped onto that key's row, which the masks then hide.
+  const uint32_t kh_lane = (uint32_t)kh_off;
+  const uint32_t vh_lane = (uint32_t)(vh_off + (KV == FW_BF16 ? 16 : 8) * n);
+  const uint32_t rb = (uint32_t)row_bytes;
 
   // Loads are branch-free so the compiler can count them: a tile past the end
-  // is clamped onto the last valid sub-tile (an L2 hit, never used).
+  // is clamped onto the last valid sub-tile (an L2 hit, never used).  A page
+  // id outside [0, num_pages) is never dereferenced: the loads read page 0
+  // and the sub-tile's keys are masked (the tile's `bad` flag).
   auto load_tile = [&](int tb, DecodeTile<KV> &tl) {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      const int sbc = min(tb + 16 * sub, last_key) & ~15;  // clamp into valid pages
+      const int sbc = min(tb + 16 * sub, last_cache_key) & ~15;  // clamp into valid pages
       const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
       int page = __builtin_amdgcn_readlane(tbl_lane[0], pi & 63);
 #pragma unroll
       for (int t = 1; t < kTblPerLane; ++t)
         page = (pi >> 6) == t ? __builtin_amdgcn_readlane(tbl_lane[t], pi & 63) : page;
-      page = min(max(page, 0), a.num_pages - 1);
+      const bool bad = page < 0 || page >= a.num_pages;
+      tl.bad[sub] = bad;
+      page = bad ? 0 : page;
       const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
       const uint8_t *vrow = prow + a.vdelta;
-      load_k_row<KV>(prow + k_lane_off, g, tl.krow[sub]);
+      const uint32_t lim = (uint32_t)(last_cache_key - sbc);  // rows 0..lim hold cache keys
+      load_k_row<KV>(prow + (min((uint32_t)n, lim) * rb + kh_lane), g, tl.krow[sub]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(vrow + v_lane_off[i]);
-        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(vrow + v_lane_off[i]);
+        const uint32_t vo = min((uint32_t)(4 * g + i), lim) * rb + vh_lane;
+        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(vrow + vo);
+        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(vrow + vo);
       }
     }
   };
   // The appended token's K/V, from k_new / v_new into every key slot (only the
   // slot of key L0 is unmasked).
   auto load_new_tile = [&](DecodeTile<KV> &tl) {
+    tl.bad[0] = tl.bad[1] = false;
     const uint8_t *kp = a.k_new + new_off;
     const uint8_t *vp = a.v_new + new_off + (KV == FW_BF16 ? 16 : 8) * n;
 #pragma unroll
@@ -255,9 +281,6 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
     }
   };
 
-  // Cache keys of this split are [k_begin, k_stop): the appended token (key
-  // L0) is folded in after the loop from k_new / v_new.
-  const int k_stop = a.has_new ? min(k_end, L0) : k_end;
   const int row_hi = min(key_hi, k_stop);
   // Keys every row of this wave sees: tiles inside need no mask.
   int all_lo = row_ok ? key_lo : k_begin, all_hi = row_ok ? row_hi : k_stop;
@@ -267,7 +290,17 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
     all_hi = min(all_hi, __shfl_xor(all_hi, m, 64));
   }
 
-  auto compute_tile = [&](int tb, const DecodeTile<KV> &tl, int lo, int hi, bool edge) {
+  auto compute_tile = [&](int tb, DecodeTile<KV> &tl, int lo, int hi, bool edge) {
+    // V of an invalid page's sub-tile was read from page 0 (which may hold
+    // anything): zeros keep 0 * NaN out of the PV product.
+    if (tl.bad[0] || tl.bad[1]) {
+#pragma unroll
+      for (int k8 = 0; k8 < 8; ++k8)
+        if (tl.bad[k8 >> 2]) {
+          if constexpr (KV == FW_BF16) tl.vraw[k8] = u32x4_t{0, 0, 0, 0};
+          else tl.vraw[k8] = u32x2_t{0, 0};
+        }
+    }
     // -------- S^T = K Q^T
     f32x4_t sacc[2];
 #pragma unroll
@@ -283,11 +316,12 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
-    if (edge) {
+    if (edge || tl.bad[0] || tl.bad[1]) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int key = tb + 16 * (e >> 2) + 4 * g + (e & 3);
-        sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
+        // keys on an out-of-range page are hidden
+        sc[e] = (key >= lo && key < hi && !tl.bad[e >> 2]) ? sc[e] : -INFINITY;
       }
     }
     // Static anchor: exponentiate against the row's anchor m_run; only when a
@@ -390,14 +424,14 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
     *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i + 4) = v1;
   }
   const int rows_valid = min(16, a.Rq - qt * 16);
-  float *po = a.ws_o + item * 16 * kD;
+  float *po = a.ws_o + item * a.rows_item * kD;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int row = 2 * k + (lane >> 5), col = 4 * (lane & 31);
     if (row < rows_valid)
       *(f32x4_t *)(po + row * kD + col) = *(const f32x4_t *)(st + row * kStageRow + col);
   }
-  if (row_ok && g == 0) a.ws_ml[item * 16 + n] = make_float2(m_run, l_run);
+  if (row_ok && g == 0) a.ws_ml[item * a.rows_item + n] = make_float2(m_run, l_run);
 }
 
 struct CombineArgs {
@@ -409,7 +443,9 @@ struct CombineArgs {
   uint16_t *out;
   float *lse;
   int B, Sq, H, Hk, G, Rq, n_qtiles, nsplit, split_keys, has_new, seqlen_add, window_left;
+  int rows_item;
   float v_descale;
+  const float *vd;  // device v_descale scalar, or null (v_descale above)
 };
 
 // One block per (b, kv head, q tile, group of 4 rows): thread t merges row
@@ -435,6 +471,9 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
     if (a.window_left >= 0) lo = max(0, total - a.Sq - a.window_left);
     const int base = lo & ~31;
     nsp = total > base ? (total - base + a.split_keys - 1) / a.split_keys : 0;
+    // a row longer than the capacity the host sized the grid for has no
+    // partials past nsplit (the decode kernel drops those keys)
+    nsp = min(nsp, a.nsplit);
   }
   const size_t item0 = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit;
   float M = -INFINITY, Lsum = 0.f;
@@ -449,8 +488,8 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int s = min(s0 + 4 * i, nsp - 1);
-        ml[i] = a.ws_ml[(item0 + s) * 16 + row];
-        const float *po = a.ws_o + ((item0 + s) * 16 + row) * kD + part * 8;
+        ml[i] = a.ws_ml[(item0 + s) * a.rows_item + row];
+        const float *po = a.ws_o + ((item0 + s) * a.rows_item + row) * kD + part * 8;
         v0[i] = *(const f32x4_t *)po;
         v1[i] = *(const f32x4_t *)(po + 4);
       }
@@ -503,7 +542,8 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
     }
   }
   const bool any = active && Lt > 0.f;
-  const float scale = any ? a.v_descale / Lt : 0.f;
+  const float vdesc = a.vd ? *a.vd : a.v_descale;
+  const float scale = any ? vdesc / Lt : 0.f;
   uint16_t *op = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
   u32x4_t w;
 #pragma unroll
@@ -550,7 +590,7 @@ static int pick_split(const fw_decode_params *p, int n_qtiles) {
 }
 
 struct DecodeLayout {
-  int G, Rq, n_qtiles, split, nsplit;
+  int G, Rq, n_qtiles, split, nsplit, rows_item;
   size_t o_bytes, ml_bytes;
 };
 
@@ -569,9 +609,10 @@ static int decode_layout(const fw_decode_params *p, DecodeLayout *L) {
   L->split = pick_split(p, L->n_qtiles);
   const long capacity = (long)p->max_pages * p->page_size;
   L->nsplit = (int)((capacity + 32 + L->split - 1) / L->split);
+  L->rows_item = std::min(L->Rq, 16);
   const size_t items = (size_t)p->batch * p->nheads_k * L->n_qtiles * L->nsplit;
-  L->o_bytes = align_up(items * 16 * kD * sizeof(float), 256);
-  L->ml_bytes = align_up(items * 16 * sizeof(float2), 256);
+  L->o_bytes = align_up(items * L->rows_item * kD * sizeof(float), 256);
+  L->ml_bytes = align_up(items * L->rows_item * sizeof(float2), 256);
   return FW_OK;
 }
 
@@ -585,7 +626,10 @@ extern "C" size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p) {
   return L.o_bytes + L.ml_bytes;
 }
 
-extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
+// The launch of both entry points: ws / ws_bytes is the split-K partial
+// buffer (the caller's workspace, or the library's static scratch).
+static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
+                         fw_stream_t stream) {
   DecodeLayout L;
   int st = decode_layout(p, &L);
   if (st != FW_OK) return st;
@@ -595,8 +639,8 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
              "a fused append takes one query token per row; got seqlen_q=%d", p->seqlen_q);
   FW_REQUIRE((p->k_new == nullptr) == (p->v_new == nullptr), FW_ERR_VALUE,
              "k_new and v_new must be given together");
-  FW_REQUIRE(p->workspace_bytes >= L.o_bytes + L.ml_bytes && p->workspace, FW_ERR_VALUE,
-             "workspace of %zu bytes is smaller than the %zu needed", p->workspace_bytes,
+  FW_REQUIRE(ws_bytes >= L.o_bytes + L.ml_bytes && ws, FW_ERR_VALUE,
+             "workspace of %zu bytes is smaller than the %zu needed", ws_bytes,
              L.o_bytes + L.ml_bytes);
   FW_REQUIRE(p->q && p->kv_cache && p->cache_seqlens && p->block_table && p->out, FW_ERR_VALUE,
              "q, kv_cache, cache_seqlens, block_table and out are required");
@@ -611,8 +655,8 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   a.cache_seqlens = p->cache_seqlens;
   a.block_table = p->block_table;
   a.num_active = p->num_active;
-  a.ws_o = (float *)p->workspace;
-  a.ws_ml = (float2 *)((char *)p->workspace + L.o_bytes);
+  a.ws_o = (float *)ws;
+  a.ws_ml = (float2 *)((char *)ws + L.o_bytes);
   a.B = p->batch;
   a.Sq = p->seqlen_q;
   a.H = p->nheads;
@@ -643,6 +687,10 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   const float sm = p->softmax_scale * p->k_descale;
   a.qscale = p->softcap > 0.f ? sm / p->softcap : sm * kLog2e;
   a.softcap_log2 = p->softcap > 0.f ? p->softcap * kLog2e : 0.f;
+  a.kd = p->k_descale_ptr;
+  a.sm_scale = p->softmax_scale;
+  a.softcap = p->softcap;
+  a.rows_item = L.rows_item;
   hipStream_t s = (hipStream_t)stream;
   const int items = p->nheads_k * L.n_qtiles;
   const int waves = items < 4 ? items : 4;
@@ -676,7 +724,13 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   c.seqlen_add = a.seqlen_add;
   c.window_left = p->window_left;
   c.v_descale = p->v_descale;
+  c.vd = p->v_descale_ptr;
+  c.rows_item = L.rows_item;
   const int row_groups = (std::min(L.Rq, 16) + 3) / 4;
   fw_decode_combine<<<dim3(row_groups, p->nheads_k * L.n_qtiles, p->batch), 256, 0, s>>>(c);
   return check_launch("fw_decode_combine");
+}
+
+extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
+  return decode_launch(p, p->workspace, p->workspace_bytes, stream);
 }

@@ -44,6 +44,10 @@ struct PrefillArgs {
   int B, H, Hk, G, Sq, Sk, n_qt, P, max_pages, num_pages, CH;
   int causal, wl, wr;
   float qscale, softcap_log2, v_descale;
+  // Device descale scalars or null.  With kd, qscale is formed on the device
+  // as (sm_scale * kd) * log2e (or / softcap), the host's operation order.
+  const float *kd, *vd;
+  float sm_scale, softcap;
   const void *rcos, *rsin;  // fused Q RoPE tables, or null
   int rrows, rf32, ril;
   int seqused_plus_q;  // paged: kv length = seqused_k + the sequence's q length
@@ -64,6 +68,15 @@ __device__ __forceinline__ void sched_slot(const PrefillArgs &a, int &slot, int 
     slot = bid / a.H;
     h = bid % a.H;
   }
+}
+
+__device__ __forceinline__ float q_scale_of(const PrefillArgs &a) {
+  if (!a.kd) return a.qscale;
+  const float sm = a.sm_scale * *a.kd;
+  return a.softcap > 0.f ? sm / a.softcap : sm * kLog2e;
+}
+__device__ __forceinline__ float v_descale_of(const PrefillArgs &a) {
+  return a.vd ? *a.vd : a.v_descale;
 }
 
 // RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7, at table
@@ -145,10 +158,20 @@ template <int MODE, int KV>
 struct KvAddr {
   const PrefillArgs &a;
   int b, hk, seq, kbase;
+  // paged: the key's page id is outside [0, num_pages) (never dereferenced:
+  // k_row / v_row then point into page 0 and the caller drops the data)
+  __device__ __forceinline__ bool bad(int key) const {
+    if constexpr (MODE == FW_KV_PAGED) {
+      const int page = a.table[(size_t)seq * a.max_pages + key / a.P];
+      return page < 0 || page >= a.num_pages;
+    } else {
+      return false;
+    }
+  }
   __device__ __forceinline__ const uint8_t *k_row(int key) const {
     if constexpr (MODE == FW_KV_PAGED) {
       int page = a.table[(size_t)seq * a.max_pages + key / a.P];
-      page = min(max(page, 0), a.num_pages - 1);
+      page = page < 0 || page >= a.num_pages ? 0 : page;
       constexpr int EB = KV == FW_BF16 ? 2 : 1;
       return a.k + (((size_t)page * a.P + key % a.P) * a.CH + 2 * hk) * 128 * EB;
     } else {
@@ -174,6 +197,7 @@ struct KvAddr {
 template <int MODE, int KV>
 __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kKsBytes + kVtBytes];
+  __shared__ uint32_t kflags;  // byte p: 16-key group p of the tile has an invalid page
   uint16_t *Ks = (uint16_t *)smem;
   uint16_t *Vt = (uint16_t *)(smem + kKsBytes);
 
@@ -258,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
+    const float qs = row_ok ? q_scale_of(a) : 0.f;  // rows past the end get q = 0
     load_q_operand(a, qp, g, qs, qrow + off, qop);
   }
 
@@ -277,13 +301,23 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   const int sc = tid & 15;
   const int sr = tid >> 4;
   u32x4_t kst[4], vst[4];
+  uint32_t kbad = 0;  // byte p: K row group p came from an invalid page
+  // Rows of an invalid page are replaced by zeros (the page 0 they were read
+  // from may hold anything, and 0 * NaN would poison the PV product); the
+  // softmax masks their keys through kflags.
+  // Every 16-key group of a tile lies on one page (P % 16 == 0), and a row
+  // clamped to kmax lies on the page of its group's first key <= kmax, so
+  // one flag per group says which K and V rows to drop.
   auto gload = [&](int t) {
     const int kb = t * kKT;
     const int kmax = sk_len - 1;
+    kbad = 0;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int key = min(kb + sr + 16 * p, kmax);
       kst[p] = load_row8<KV>(addr.k_row(key), sc);
+      // wave-uniform: the page of the group's first key <= kmax
+      if (addr.bad(min(kb + 16 * p, kmax))) kbad |= 1u << (8 * p);
     }
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -294,6 +328,16 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     }
   };
   auto lds_store = [&]() {
+    if (tid == 0) kflags = kbad;
+    if (kbad) {  // rare: drop the rows of invalid pages
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        if ((kbad >> (8 * p)) & 1u) kst[p] = u32x4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if ((kbad >> (8 * ((2 * sr + 32 * p) >> 4))) & 1u)
+          vst[2 * p] = vst[2 * p + 1] = u32x4_t{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int p = 0; p < 4; ++p) *(u32x4_t *)(Ks + (sr + 16 * p) * kKS + 8 * sc) = kst[p];
 #pragma unroll
@@ -340,15 +384,17 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     }
     // ---------------- online softmax (log2 units), lane = query row n
     if (a.softcap_log2 != 0.f) softcap_scores<2, 16>(sacc, a.softcap_log2);
+    const uint32_t fl = MODE == FW_KV_PAGED ? __builtin_amdgcn_readfirstlane(kflags) : 0u;
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
-                      kb + kKT <= sk_len;
+                      kb + kKT <= sk_len && fl == 0;
     if (!full) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
+          const bool badk = (fl >> (8 * (2 * st + (e >> 3)))) & 0xffu;
+          sacc[st][e] = (key >= r_lo && key < r_hi && !badk) ? sacc[st][e] : -INFINITY;
         }
     }
     float tmax = -INFINITY;
@@ -417,7 +463,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   }
   if (!row_ok) return;
   const bool any = Lsum > 0.f && l_run > 0.f;
-  const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
+  const float scale = any ? oscale * v_descale_of(a) / Lsum : 0.f;
   uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
 #pragma unroll
   for (int c = 0; c < 4; ++c)
@@ -471,6 +517,9 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 // tile j+2 in its softmax slot of tile j.  With softcap (SOFTCAP) the tanh
 // runs in the softmax slot too.
 constexpr int kPPWaves = 8;
+// One zero K row and V row (256 B each): the copy source for the keys of an
+// invalid page id.
+__device__ __attribute__((aligned(256))) uint8_t kZeroKV[512];
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
 
@@ -486,6 +535,8 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
 template <int MODE, bool SOFTCAP>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kPPBuf];
+  // paged: per buffer, per 8-key row group: the group's page id is invalid
+  __shared__ __attribute__((aligned(8))) uint8_t pflags[4 * kPPWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -586,6 +637,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)lds;
+  const uint32_t pflags_base = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)pflags;
   // Tile t goes from global memory straight into LDS buffer t % 4
   // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
   // per instruction); this wave moves key rows 8w .. 8w+7.
@@ -602,20 +654,28 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     asm volatile("s_load_dword %0, %1, 0x0" : "=s"(v) : "s"(table_entry(j, wv)) : "memory");
     return v;
   };
+  // Paged: a page id outside [0, num_pages) is never dereferenced.  The wave
+  // still issues its four copies (the vmcnt waits count them), all from the
+  // zero row kZeroKV (zeros rather than other cache rows, which may hold
+  // anything, NaN included: 0 * NaN would poison the PV product), and
+  // pflags[buf][wave] tells the softmax to mask those keys.
   auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
     int key0 = min((t_begin + j) * kKT + 8 * wv, kmax);
     const uint8_t *kp, *vp;
+    bool bad = false;
     if constexpr (MODE == FW_KV_PAGED) {
       key0 &= ~7;  // an 8-row group never straddles a page (P % 16 == 0)
-      page = min(max(page, 0), a.num_pages - 1);
+      bad = page < 0 || page >= a.num_pages;
       kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
+      if (bad) kp = kZeroKV;
       vp = kp + 256;
+      if (lane == 0) *(FW_LDS uint8_t *)(pflags_base + buf * kPPWaves + wv) = bad ? 1 : 0;
     } else {
       kp = kbase_p + (size_t)key0 * kstB;
       vp = vbase_p + (size_t)key0 * vstB;
     }
-    const uint32_t lim = (uint32_t)(kmax - key0);
+    const uint32_t lim = bad ? 0u : (uint32_t)(kmax - key0);
     const uint32_t lra = min(lr0, lim), lrb = min(lr0 + 4u, lim);
     const uint32_t c16a = c16b ^ (16u * ((2 * wv) & 3)), c16c = c16b ^ (16u * ((2 * wv + 1) & 3));
     const uint32_t d = lds0 + (uint32_t)(8 * wv * kRowB) + (uint32_t)buf * kTileB;
@@ -637,7 +697,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
-    const float qs = row_ok ? a.qscale : 0.f;  // rows past the end get q = 0
+    const float qs = row_ok ? q_scale_of(a) : 0.f;  // rows past the end get q = 0
     load_q_operand(a, qp, g, qs, qrow + off, qop);
   }
 
@@ -735,14 +795,16 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // partial row sum overflows 2^16 (a score more than ~11 above the anchor) or
   // a row sees its first valid key take the slow path (row max, new anchor,
   // O/l rescale, exponentiate again).
-  auto softmax = [&](int t, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
+  // fl0 / fl1: bytes of the tile's 8-key row groups 0-3 / 4-7 whose page id
+  // is invalid (nonzero = masked).
+  auto softmax = [&](int t, bf16x8_t (&pop)[4], uint32_t fl0, uint32_t fl1) __attribute__((always_inline)) {
     const int kb = t * kKT;
     // the scores arrive as s - anchor (the MFMA accumulated onto -anchor, or
     // the softcap subtracts it)
     const float m_qk = m_run == -INFINITY ? 0.f : m_run;
     if constexpr (SOFTCAP) softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
-                      kb + kKT <= sk_len;
+                      kb + kKT <= sk_len && (fl0 | fl1) == 0;
     bool row_has_key = true;
     if (!full) {
 #pragma unroll
@@ -750,7 +812,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
+          const uint32_t flw = st ? fl1 : fl0;
+          const bool badk = (flw >> (8 * (e >> 2))) & 0xffu;
+          sacc[st][e] = (key >= r_lo && key < r_hi && !badk) ? sacc[st][e] : -INFINITY;
         }
       row_has_key = max(r_lo, kb) < min(r_hi, kb + kKT);
     }
@@ -855,12 +919,24 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       slot_barrier();
       const bool copy = j + 2 < T;
       if (copy) {
+        // page_next came from an asm scalar load whose completion the
+        // compiler cannot see: it is complete at the lgkmcnt(0) of the
+        // barrier above, and this wait ties its use to after that point.
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(page_next));
         dma_tile_pg(j + 2, (B + 2) % 4, w, page_next);
         if constexpr (MODE == FW_KV_PAGED) {
           if (j + 3 < T) page_next = table_sload(j + 3, w);  // for the next body
         }
       }
-      if (j < T) softmax(t_begin + j, pops);
+      if (j < T) {
+        uint32_t fl0 = 0, fl1 = 0;  // invalid-page flags of tile j's row groups
+        if constexpr (MODE == FW_KV_PAGED) {
+          const u32x2_t fl = *(const FW_LDS u32x2_t *)(pflags_base + 8 * B);
+          fl0 = __builtin_amdgcn_readfirstlane(fl[0]);
+          fl1 = __builtin_amdgcn_readfirstlane(fl[1]);
+        }
+        softmax(t_begin + j, pops, fl0, fl1);
+      }
       mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
       if (grp == 0) {
         if (copy) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // tile j+1 in
@@ -898,7 +974,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
   }
   const bool any = Lsum > 0.f && l_run > 0.f;
-  const float scale = any ? oscale * a.v_descale / Lsum : 0.f;
+  const float scale = any ? oscale * v_descale_of(a) / Lsum : 0.f;
   // O goes out as whole 256-byte rows: each wave stages its 32 rows in its own
   // 8 KiB of LDS (16-byte chunks XOR-swizzled by row), then every lane stores
   // 16 contiguous bytes.  All LDS reads of the loop finished at its last
@@ -1106,6 +1182,10 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.qscale = p->softcap > 0.f ? sm / p->softcap : sm * kLog2e;
   a.softcap_log2 = p->softcap > 0.f ? p->softcap * kLog2e : 0.f;
   a.v_descale = p->v_descale;
+  a.kd = p->k_descale_ptr;
+  a.vd = p->v_descale_ptr;
+  a.sm_scale = p->softmax_scale;
+  a.softcap = p->softcap;
   a.rcos = p->rotary_cos;
   a.rsin = p->rotary_sin;
   a.rrows = p->rotary_rows;

@@ -40,6 +40,7 @@ class DecodeParams(ctypes.Structure):
         ("k_descale", _f32), ("v_descale", _f32),
         ("split_keys", _i32),
         ("v_cache", _c_p),
+        ("k_descale_ptr", _c_p), ("v_descale_ptr", _c_p),
     ]
 
 
@@ -65,6 +66,7 @@ class PrefillParams(ctypes.Structure):
         ("rotary_cos", _c_p), ("rotary_sin", _c_p),
         ("rotary_rows", _i32), ("rotary_f32", _i32), ("rotary_interleaved", _i32),
         ("seqused_k_excludes_q", _i32),
+        ("k_descale_ptr", _c_p), ("v_descale_ptr", _c_p),
     ]
 
 

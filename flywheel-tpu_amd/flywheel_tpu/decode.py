@@ -30,6 +30,7 @@ from .inputs import (
     effective_window,
     int32_device,
     resolve_scale,
+    set_descales,
 )
 from .kv_layout import resolve_merged_kv_heads
 
@@ -66,14 +67,12 @@ def append_ragged(kv_cache, k, v, cu_seqlens, cache_seqlens, block_table, num_ac
         N.KV_DTYPES[kv_cache.dtype], N.stream_of(kv_cache)))
 
 
-def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_active, sinks, *,
-                 nheads_k, softmax_scale, softcap, causal, window_left, k_descale, v_descale,
-                 seqlen_add=0, return_lse=False, split_keys=0, v_cache=None):
-    """The split-K decode kernel (kernels/decode.py:463-1915) over a merged
-    pool, or with v_cache over the contiguous (batch_cache, capacity, nheads_k,
-    head_dim) K/V pair, block_table then being cache_batch_idx as (batch, 1).
-
-    q (batch, seqlen_q, nheads, head_dim) bf16.  Returns (out, lse|None)."""
+def decode_params(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_active, sinks, *,
+                  nheads_k, softmax_scale, softcap, causal, window_left, k_descale, v_descale,
+                  seqlen_add=0, return_lse=False, split_keys=0, v_cache=None):
+    """A filled fw_decode_params (no workspace yet) and the tensors it points
+    at: returns (params, out, lse | None, keep), keep holding every tensor the
+    launch reads that the caller does not already hold."""
     batch, seqlen_q, nheads, head_dim = q.shape
     out = torch.empty_like(q)
     lse = (torch.empty((batch, nheads, seqlen_q), dtype=torch.float32, device=q.device)
@@ -89,8 +88,20 @@ def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_acti
     p.seqlen_add = seqlen_add
     p.softmax_scale, p.softcap = softmax_scale, softcap
     p.causal, p.window_left = int(causal), window_left
-    p.k_descale, p.v_descale = k_descale, v_descale
+    keep = set_descales(p, k_descale, v_descale)
     p.split_keys = split_keys
+    return p, out, lse, keep
+
+
+def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_active, sinks, **kw):
+    """The split-K decode kernel (kernels/decode.py:463-1915) over a merged
+    pool, or with v_cache over the contiguous (batch_cache, capacity, nheads_k,
+    head_dim) K/V pair, block_table then being cache_batch_idx as (batch, 1).
+
+    q (batch, seqlen_q, nheads, head_dim) bf16; keyword arguments as
+    decode_params.  Returns (out, lse|None)."""
+    p, out, lse, keep = decode_params(q, kv_cache, k_new, v_new, cache_seqlens, block_table,
+                                      num_active, sinks, **kw)
     lib = N.lib()
     nbytes = lib.fw_paged_decode_workspace_bytes(p)
     if nbytes == 0:
@@ -98,6 +109,7 @@ def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_acti
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = N.ptr(ws), nbytes
     N.check(lib.fw_paged_decode(p, N.stream_of(q)))
+    del keep
     return out, lse
 
 
@@ -136,7 +148,7 @@ def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active,
     p.kv_dtype = N.KV_DTYPES[kv_cache.dtype]
     p.softmax_scale, p.softcap = softmax_scale, softcap
     p.causal, p.window_left, p.window_right = int(causal), left, right
-    p.k_descale, p.v_descale = k_descale, v_descale
+    keep_d = set_descales(p, k_descale, v_descale)
     p.seqused_k_excludes_q = int(seqused_excludes_q)
     keep = None if q_rotary is None else R.set_q_rotary(p, *q_rotary, q.device)
     lib = N.lib()
@@ -144,7 +156,7 @@ def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active,
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = N.ptr(ws), ws.numel()
     N.check(lib.fw_prefill(p, N.stream_of(q)))
-    del keep
+    del keep, keep_d
     return out, lse
 
 
@@ -292,8 +304,8 @@ def flash_attn_with_kvcache(
             f" pool) float8_e4m3fn / float8_e5m2; got q {q.dtype}, KV"
             f" {tuple(str(t.dtype) for t in kv_operands)}."
         )
-    k_descale = descale_scalar(k_descale, "k_descale")
-    v_descale = descale_scalar(v_descale, "v_descale")
+    k_descale = descale_scalar(k_descale, "k_descale", q.device)
+    v_descale = descale_scalar(v_descale, "v_descale", q.device)
     expected_new_shape = (*q.shape[:-2], nheads_k, head_dim)
     if has_new and (tuple(k.shape) != expected_new_shape or tuple(v.shape) != expected_new_shape):
         raise ValueError(

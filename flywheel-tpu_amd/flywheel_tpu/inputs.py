@@ -49,16 +49,39 @@ def check_common_kwargs(
     return tuple(int(b) for b in window_size)
 
 
-def descale_scalar(descale, arg_name):
-    """`inputs.py:61-72`: one per-tensor descale as a Python float; None is 1."""
+def descale_scalar(descale, arg_name, device=None):
+    """`inputs.py:61-72`: one per-tensor descale; None is 1.
+
+    A Python number comes back as a float (passed to the kernels by value).
+    A tensor or array stays a device value: it comes back as a (1,) float32
+    tensor on `device`, which the kernels read by pointer, so no host
+    synchronisation takes place (the reference keeps a traced device scalar).
+    """
     if descale is None:
         return 1.0
-    t = as_tensor(descale) if not isinstance(descale, (int, float)) else None
-    if t is None:
+    if isinstance(descale, (int, float)):
         return float(descale)
+    t = as_tensor(descale)
     if t.numel() != 1:
         raise ValueError(f"{arg_name} must be one per-tensor value; got shape {tuple(t.shape)}.")
-    return float(t.reshape(()).item())
+    return t.reshape(1).to(device=device, dtype=torch.float32)
+
+
+def set_descales(params, k_descale, v_descale):
+    """Fill the k/v descale fields of a DecodeParams / PrefillParams from
+    descale_scalar's results (a float by value, a device tensor by pointer).
+    Returns the tensors the launch reads, to be kept alive until it is
+    enqueued."""
+    keep = []
+    for name, val in (("k_descale", k_descale), ("v_descale", v_descale)):
+        if isinstance(val, torch.Tensor):
+            setattr(params, name, 1.0)
+            setattr(params, name + "_ptr", val.data_ptr())
+            keep.append(val)
+        else:
+            setattr(params, name, float(val))
+            setattr(params, name + "_ptr", None)
+    return keep
 
 
 def check_sinks(sinks, nheads, device):

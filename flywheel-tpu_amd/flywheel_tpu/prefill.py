@@ -376,7 +376,8 @@ def flash_attn_varlen_func(
         q = q.contiguous()
         sinks = check_sinks(learnable_sink, nheads, device)
         bt_dev = bt.to(device=device, dtype=torch.int32).contiguous()
-        kd, vd = descale_scalar(k_descale, "k_descale"), descale_scalar(v_descale, "v_descale")
+        kd = descale_scalar(k_descale, "k_descale", device)
+        vd = descale_scalar(v_descale, "v_descale", device)
 
         def run_paged(q, k, unused_v):
             return paged_prefill(

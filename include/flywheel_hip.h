@@ -15,7 +15,12 @@
  *                      row is [k0, v0, k1, v1, ...]; an fp8 pool pads an odd
  *                      KV head count with one zero head
  *                      (reference kv_layout.py:39-46, 67-70).
- *   block_table        (batch, max_pages) int32, row-major.
+ *   block_table        (batch, max_pages) int32, row-major.  Device
+ *                      metadata is trusted as in the reference (no checks
+ *                      with a host round trip), with one rule for a page id
+ *                      outside [0, num_pages): it is never dereferenced;
+ *                      writes to it are dropped and its keys are masked
+ *                      (they take no part in any softmax).
  */
 #ifndef FLYWHEEL_HIP_H
 #define FLYWHEEL_HIP_H
@@ -44,7 +49,7 @@ enum fw_dtype {
 
 /* The last error message of the calling thread ("" if none). */
 const char *fw_last_error(void);
-/* ABI version of this header: 4. */
+/* ABI version of this header: 5. */
 int fw_abi_version(void);
 
 /*
@@ -97,10 +102,17 @@ typedef struct fw_decode_params {
    * bf16, and block_table = cache_batch_idx as a (batch, 1) table
    * (max_pages 1); the new token goes to [cache_batch_idx[b], cache_seqlens[b]]. */
   const void *v_cache;
+  /* Per-tensor descales as device f32 scalars (the reference keeps them as
+   * traced device values, softmax_attention/inputs.py:61-72): when non-NULL
+   * they are read on the device and k_descale / v_descale above are ignored,
+   * so no host synchronisation is needed. */
+  const float *k_descale_ptr;
+  const float *v_descale_ptr;
 } fw_decode_params;
 
 size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p);
 int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream);
+
 
 /*
  * Ragged append of packed new tokens into the merged pool.  Replaces
@@ -191,6 +203,9 @@ typedef struct fw_prefill_params {
    * q rows were appended (the cache lengths of a chunked prefill), and the kv
    * length is seqused_k[s] + cu_seqlens_q[s+1] - cu_seqlens_q[s]. */
   int32_t seqused_k_excludes_q;
+  /* Device f32 descale scalars, or NULL; as in fw_decode_params. */
+  const float *k_descale_ptr;
+  const float *v_descale_ptr;
 } fw_prefill_params;
 
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);

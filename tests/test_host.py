@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} is declared but not exported"
     assert set(names) == set(N.SIGNATURES), "ctypes bindings and header disagree"
-    assert lib.fw_abi_version() == 4
+    assert lib.fw_abi_version() == 5
 
 
 def test_struct_layouts_match_header_fields():
@@ -53,6 +53,43 @@ def test_struct_layouts_match_header_fields():
                 m = re.search(r"\**([A-Za-z_0-9]+)\s*$", part.strip())
                 fields.append(m.group(1))
         assert fields == [f[0] for f in cls._fields_], struct
+
+
+STRUCTS = (("fw_decode_params", N.DecodeParams), ("fw_prefill_params", N.PrefillParams),
+           ("fw_rotary_params", N.RotaryParams), ("fw_attn_bwd_params", N.AttnBwdParams))
+
+
+def test_struct_offsets_and_widths_match_c(tmp_path):
+    """Every field's offset and width, and each struct's size, as the C
+    compiler lays out include/flywheel_hip.h, against the ctypes mirror: an
+    int32 / int64 / size_t / pointer mismatch moves an offset or a width."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"',
+             "int main(void) {"]
+    for struct, cls in STRUCTS:
+        lines.append(f'printf("{struct} sizeof %zu %zu\\n", sizeof({struct}), (size_t)0);')
+        for name, _ in cls._fields_:
+            lines.append(f'printf("{struct} {name} %zu %zu\\n", offsetof({struct}, {name}),'
+                         f' sizeof((({struct} *)0)->{name}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-std=c99", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                               text=True).stdout.splitlines():
+        struct, name, off, size = line.split()
+        got[(struct, name)] = (int(off), int(size))
+    for struct, cls in STRUCTS:
+        assert got[(struct, "sizeof")][0] == ctypes.sizeof(cls), struct
+        for name, _ in cls._fields_:
+            f = getattr(cls, name)
+            assert got[(struct, name)] == (f.offset, f.size), f"{struct}.{name}"
 
 
 def test_capi_validation_status_codes():

@@ -287,3 +287,69 @@ def test_ragged_reference_matches_attention_ref():
                 causal=causal, window_size=(-1 if wl is None else wl, -1), softcap=sc)
             np.testing.assert_allclose(out[cu[s]:cu[s + 1]], ro[0], atol=2e-5)
             np.testing.assert_allclose(lse[:, cu[s]:cu[s + 1]], rl[0], atol=2e-5)
+
+
+def brute_force_rounded(q, k, v, causal, window, softcap, scale, k_descale=1.0, v_descale=1.0):
+    """brute_force with the kernels' q convention, element by element in
+    float64: q is multiplied by the fused factor (scale * k_descale / softcap,
+    or scale * k_descale * log2 e), rounded to bf16 (torch's cast), and the
+    score in natural units is tanh(q_s . k) * softcap, or (q_s . k) * ln 2."""
+    fac = np.float32(scale * k_descale / softcap if softcap else scale * k_descale * math.log2(math.e))
+    qs = torch.from_numpy(np.ascontiguousarray(q * fac, np.float32)).to(torch.bfloat16).double().numpy()
+    sq, h, d = q.shape
+    sk, hk, _ = k.shape
+    out = np.zeros((sq, h, d))
+    lse = np.full((h, sq), -np.inf)
+    for hh in range(h):
+        kh = hh // (h // hk)
+        for i in range(sq):
+            diag = i + sk - sq
+            logits = []
+            for j in range(sk):
+                if causal and j > diag:
+                    continue
+                if window[0] >= 0 and j < diag - window[0]:
+                    continue
+                dot = sum(float(qs[i, hh, x]) * float(k[j, kh, x]) for x in range(d))
+                s = math.tanh(dot) * softcap if softcap else dot * math.log(2.0)
+                logits.append((j, s))
+            if not logits:
+                continue
+            m = max(s for _, s in logits)
+            z = sum(math.exp(s - m) for _, s in logits)
+            lse[hh, i] = m + math.log(z)
+            for j, s in logits:
+                out[i, hh] += math.exp(s - m) / z * v[j, kh].astype(np.float64) * v_descale
+    return out, lse
+
+
+@pytest.mark.parametrize("softcap,window,causal", [(5.0, (-1, -1), True), (30.0, (3, -1), True),
+                                                   (0.0, (2, -1), True), (2.0, (-1, -1), False)])
+def test_rounded_q_softcap_branches_brute_force(softcap, window, causal):
+    """The rounded-q branches of attention_ref, kvcache_reference and
+    ragged_reference (with softcap and descales) against brute force."""
+    rng = np.random.default_rng(9)
+    sq, sk, h, hk, d = 4, 11, 4, 2, 16
+    q = randn(rng, (1, sq, h, d)) * 3
+    k = randn(rng, (1, sk, hk, d))
+    v = randn(rng, (1, sk, hk, d))
+    scale = 1 / math.sqrt(d)
+    bo, bl = brute_force_rounded(q[0], k[0], v[0], causal, window, softcap, scale)
+    out, lse = A.attention_ref(q, k, v, causal=causal, window_size=window, softcap=softcap,
+                               round_scaled_q=True)
+    np.testing.assert_allclose(out[0], bo, atol=2e-5, rtol=1e-4)
+    np.testing.assert_allclose(lse[0], bl, atol=2e-5, rtol=1e-5)
+    kd, vd = 0.75, 1.5
+    bo, bl = brute_force_rounded(q[0], k[0], v[0], causal, window, softcap, scale, kd, vd)
+    out, lse = A.kvcache_reference(q, k, v, np.array([sk]), causal=causal, window_size=window,
+                                   softcap=softcap, k_descale=kd, v_descale=vd)
+    np.testing.assert_allclose(out[0], bo, atol=4e-5, rtol=1e-4)
+    np.testing.assert_allclose(lse[0], bl, atol=2e-5, rtol=1e-5)
+    if causal:  # the paged varlen oracle: k / v as one page of sk keys
+        out, lse = A.ragged_reference(q[0], k, v, np.array([0, sq]), np.array([sk]),
+                                      np.zeros((1, 1), np.int64), causal=True,
+                                      window_left=None if window[0] < 0 else window[0],
+                                      softcap=softcap, k_descale=kd, v_descale=vd,
+                                      round_scaled_q=True)
+        np.testing.assert_allclose(out, bo, atol=4e-5, rtol=1e-4)
+        np.testing.assert_allclose(lse, bl, atol=2e-5, rtol=1e-5)
