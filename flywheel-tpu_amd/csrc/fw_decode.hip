@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <type_traits>
 #include <cstdlib>
+#include <mutex>
 
 namespace fw {
 
@@ -733,4 +734,49 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
 
 extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
   return decode_launch(p, p->workspace, p->workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// fw_paged_decode_noalloc: the same launch with the split-K partials in a
+// file-scope device array instead of a caller workspace, for callers that
+// cannot allocate.  Each device holds its own copy of the array; its address
+// comes from hipGetSymbolAddress on the first call made on that device (the
+// array's name in host code is only a stand-in, not a device address).
+// Nothing in it needs clearing between calls: every partial the merge reads
+// was written by the same call's decode kernel.  Calls that overlap on one
+// device share the array and race.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[FW_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+extern "C" int fw_paged_decode_noalloc(const fw_decode_params *p, fw_stream_t stream) {
+  DecodeLayout L;
+  int st = decode_layout(p, &L);
+  if (st != FW_OK) return st;
+  const size_t need = L.o_bytes + L.ml_bytes;
+  FW_REQUIRE(need <= FW_DECODE_SCRATCH_BYTES, FW_ERR_VALUE,
+             "fw_paged_decode_noalloc: this call needs %zu bytes of split-K scratch, more than"
+             " the library's static %zu (FW_DECODE_SCRATCH_BYTES); use fw_paged_decode with a"
+             " workspace (or a larger split_keys)", need, (size_t)FW_DECODE_SCRATCH_BYTES);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  FW_REQUIRE(e == hipSuccess, FW_ERR_RUNTIME, "hipGetDevice: %s", hipGetErrorString(e));
+  FW_REQUIRE(dev >= 0 && dev < kMaxDevices, FW_ERR_RUNTIME, "device %d out of range", dev);
+  void *ptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void *addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      FW_REQUIRE(e == hipSuccess && addr, FW_ERR_RUNTIME,
+                 "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      g_scratch_ptr[dev] = addr;
+    }
+    ptr = g_scratch_ptr[dev];
+  }
+  return decode_launch(p, ptr, FW_DECODE_SCRATCH_BYTES, stream);
 }

@@ -19,6 +19,7 @@ _lib = None
 FW_OK, FW_ERR_VALUE, FW_ERR_NOT_IMPLEMENTED, FW_ERR_RUNTIME = 0, 1, 2, 3
 FW_BF16, FW_FP8_E4M3, FW_FP8_E5M2 = 0, 1, 2
 FW_KV_DENSE, FW_KV_VARLEN, FW_KV_PAGED = 0, 1, 2
+FW_DECODE_SCRATCH_BYTES = 64 << 20  # include/flywheel_hip.h
 
 _c_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -103,6 +104,7 @@ SIGNATURES = {
     "fw_abi_version": (ctypes.c_int, []),
     "fw_paged_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeParams)]),
     "fw_paged_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _c_p]),
+    "fw_paged_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _c_p]),
     "fw_append_ragged": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p]),
     "fw_write_kv_cache_pages": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _i32, _c_p,

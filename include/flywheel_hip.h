@@ -113,6 +113,20 @@ typedef struct fw_decode_params {
 size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p);
 int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream);
 
+/*
+ * fw_paged_decode without a workspace.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The same
+ * kernels as fw_paged_decode, with the split-K partials in a library-owned
+ * static device buffer of FW_DECODE_SCRATCH_BYTES per GPU (held from the
+ * library's load until the process ends) instead of p->workspace, which is
+ * ignored.  It allocates nothing.  A call whose partials need more than
+ * FW_DECODE_SCRATCH_BYTES (fw_paged_decode_workspace_bytes(p) > the limit)
+ * fails with FW_ERR_VALUE.  Calls that overlap on one GPU share the buffer
+ * and race: serialise them (one stream, or events).
+ */
+#define FW_DECODE_SCRATCH_BYTES (64u << 20)
+int fw_paged_decode_noalloc(const fw_decode_params *p, fw_stream_t stream);
 
 /*
  * Ragged append of packed new tokens into the merged pool.  Replaces
