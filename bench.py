@@ -503,7 +503,56 @@ EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope,
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 
 
+def short_kernel_name(name):
+    """fw::fw_prefill_pp_kernel<0, true>(fw::PrefillArgs) -> fw_prefill_pp_kernel<0, true>;
+    anything else (torch's setup kernels) cut to 48 characters."""
+    name = name.strip('"')
+    if name.startswith("void "):
+        name = name[5:]
+    if name.startswith("fw::"):
+        name = name[4:]
+        depth, out = 0, []
+        for ch in name:
+            if ch == "(" and depth == 0:
+                break
+            depth += ch == "<"
+            depth -= ch == ">"
+            out.append(ch)
+        return "".join(out).replace("fw::", "")
+    return name[:48]
+
+
+def trace_summary(csv_path, last):
+    """Per (kernel, grid) statistics of a rocprofv3 --kernel-trace CSV: all
+    dispatches, and the last `last` dispatches, which are the timed steps of
+    bench.py (each workload's timed steps are its kernels' final launches;
+    the burn-in and warm-up come before them).  Prints a text table."""
+    import csv
+    rows = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            key = (short_kernel_name(r["Kernel_Name"]),
+                   f'{r["Grid_Size_X"]}x{r["Grid_Size_Y"]}x{r["Grid_Size_Z"]}')
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            rows.setdefault(key, []).append((int(r["Start_Timestamp"]), dur))
+    print(f"# {'kernel':<44} {'grid':>18} {'calls':>6} {'avg_all':>9} "
+          f"{'last':>4} {'median':>9} {'avg':>9} {'min':>9} {'max':>9}   (us)")
+    for (name, grid), v in sorted(rows.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        v.sort()
+        durs = np.array([d for _, d in v])
+        tail = durs[-last:]
+        print(f"{name[:46]:<46} {grid:>18} {len(durs):>6} {durs.mean():>9.2f} {len(tail):>4} "
+              f"{np.median(tail):>9.2f} {tail.mean():>9.2f} {tail.min():>9.2f} {tail.max():>9.2f}")
+
+
 def main():
+    if "--trace-summary" in sys.argv:
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--trace-summary", required=True, help="rocprofv3 kernel_trace.csv")
+        ap.add_argument("--last", type=int, default=20, help="timed steps per workload")
+        a = ap.parse_args()
+        trace_summary(a.trace_summary, a.last)
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
