@@ -119,7 +119,7 @@ struct DecodeTile {
   KRow<KV> krow[2];  // K of the two 16-key sub-tiles (lane row n)
   // V of keys 4g+i / 16+4g+i, dims 8n .. 8n+7 (16 or 8 bytes a key)
   typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8];
-  bool bad[2];  // a sub-tile's page id is out of range: its keys are masked
+  bool bad[2];  // a sub-tile's page id is out of range: its keys read as zeros
 };
 
 
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   // Loads are branch-free so the compiler can count them: a tile past the end
   // is clamped onto the last valid sub-tile (an L2 hit, never used).  A page
   // id outside [0, num_pages) is never dereferenced: the loads read page 0
-  // and the sub-tile's keys are masked (the tile's `bad` flag).
+  // and the compute stage replaces the sub-tile by zero K and V rows.
   auto load_tile = [&](int tb, DecodeTile<KV> &tl) {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
@@ -292,14 +292,20 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
   }
 
   auto compute_tile = [&](int tb, DecodeTile<KV> &tl, int lo, int hi, bool edge) {
-    // V of an invalid page's sub-tile was read from page 0 (which may hold
-    // anything): zeros keep 0 * NaN out of the PV product.
+    // The keys of an invalid page id read as zero K and V rows (the loads
+    // used page 0, which may hold anything).
     if (tl.bad[0] || tl.bad[1]) {
 #pragma unroll
-      for (int k8 = 0; k8 < 8; ++k8)
-        if (tl.bad[k8 >> 2]) {
-          if constexpr (KV == FW_BF16) tl.vraw[k8] = u32x4_t{0, 0, 0, 0};
-          else tl.vraw[k8] = u32x2_t{0, 0};
+      for (int sub = 0; sub < 2; ++sub)
+        if (tl.bad[sub]) {
+#pragma unroll
+          for (int j = 0; j < (KV == FW_BF16 ? 4 : 2); ++j)
+            tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = u32x4_t{0, 0, 0, 0};
+            else tl.vraw[4 * sub + i] = u32x2_t{0, 0};
+          }
         }
     }
     // -------- S^T = K Q^T
@@ -317,12 +323,11 @@ __global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(Decode
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
-    if (edge || tl.bad[0] || tl.bad[1]) {
+    if (edge) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int key = tb + 16 * (e >> 2) + 4 * g + (e & 3);
-        // keys on an out-of-range page are hidden
-        sc[e] = (key >= lo && key < hi && !tl.bad[e >> 2]) ? sc[e] : -INFINITY;
+        sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
       }
     }
     // Static anchor: exponentiate against the row's anchor m_run; only when a

@@ -159,7 +159,7 @@ struct KvAddr {
   const PrefillArgs &a;
   int b, hk, seq, kbase;
   // paged: the key's page id is outside [0, num_pages) (never dereferenced:
-  // k_row / v_row then point into page 0 and the caller drops the data)
+  // k_row / v_row then point into page 0 and the caller zeroes the data)
   __device__ __forceinline__ bool bad(int key) const {
     if constexpr (MODE == FW_KV_PAGED) {
       const int page = a.table[(size_t)seq * a.max_pages + key / a.P];
@@ -197,7 +197,6 @@ struct KvAddr {
 template <int MODE, int KV>
 __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kKsBytes + kVtBytes];
-  __shared__ uint32_t kflags;  // byte p: 16-key group p of the tile has an invalid page
   uint16_t *Ks = (uint16_t *)smem;
   uint16_t *Vt = (uint16_t *)(smem + kKsBytes);
 
@@ -301,13 +300,11 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   const int sc = tid & 15;
   const int sr = tid >> 4;
   u32x4_t kst[4], vst[4];
-  uint32_t kbad = 0;  // byte p: K row group p came from an invalid page
-  // Rows of an invalid page are replaced by zeros (the page 0 they were read
-  // from may hold anything, and 0 * NaN would poison the PV product); the
-  // softmax masks their keys through kflags.
-  // Every 16-key group of a tile lies on one page (P % 16 == 0), and a row
-  // clamped to kmax lies on the page of its group's first key <= kmax, so
-  // one flag per group says which K and V rows to drop.
+  uint32_t kbad = 0;  // byte p: K row group p came from an invalid page id
+  // The keys of an invalid page id read as zero K and V rows (the page 0 the
+  // loads used may hold anything).  Every 16-key group of a tile lies on one
+  // page (P % 16 == 0), and a row clamped to kmax lies on the page of its
+  // group's first key <= kmax, so one flag per group says which rows to zero.
   auto gload = [&](int t) {
     const int kb = t * kKT;
     const int kmax = sk_len - 1;
@@ -328,8 +325,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     }
   };
   auto lds_store = [&]() {
-    if (tid == 0) kflags = kbad;
-    if (kbad) {  // rare: drop the rows of invalid pages
+    if (kbad) {  // rare: zero the rows of invalid page ids
 #pragma unroll
       for (int p = 0; p < 4; ++p)
         if ((kbad >> (8 * p)) & 1u) kst[p] = u32x4_t{0, 0, 0, 0};
@@ -384,17 +380,15 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     }
     // ---------------- online softmax (log2 units), lane = query row n
     if (a.softcap_log2 != 0.f) softcap_scores<2, 16>(sacc, a.softcap_log2);
-    const uint32_t fl = MODE == FW_KV_PAGED ? __builtin_amdgcn_readfirstlane(kflags) : 0u;
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
-                      kb + kKT <= sk_len && fl == 0;
+                      kb + kKT <= sk_len;
     if (!full) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          const bool badk = (fl >> (8 * (2 * st + (e >> 3)))) & 0xffu;
-          sacc[st][e] = (key >= r_lo && key < r_hi && !badk) ? sacc[st][e] : -INFINITY;
+          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
         }
     }
     float tmax = -INFINITY;
@@ -535,8 +529,6 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
 template <int MODE, bool SOFTCAP>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kPPBuf];
-  // paged: per buffer, per 8-key row group: the group's page id is invalid
-  __shared__ __attribute__((aligned(8))) uint8_t pflags[4 * kPPWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -637,7 +629,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)lds;
-  const uint32_t pflags_base = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)pflags;
   // Tile t goes from global memory straight into LDS buffer t % 4
   // (global_load_lds_dwordx4: 64 lanes x 16 B land contiguously, 4 key rows
   // per instruction); this wave moves key rows 8w .. 8w+7.
@@ -654,11 +645,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     asm volatile("s_load_dword %0, %1, 0x0" : "=s"(v) : "s"(table_entry(j, wv)) : "memory");
     return v;
   };
-  // Paged: a page id outside [0, num_pages) is never dereferenced.  The wave
-  // still issues its four copies (the vmcnt waits count them), all from the
-  // zero row kZeroKV (zeros rather than other cache rows, which may hold
-  // anything, NaN included: 0 * NaN would poison the PV product), and
-  // pflags[buf][wave] tells the softmax to mask those keys.
+  // Paged: a page id outside [0, num_pages) is never dereferenced: its keys
+  // read as zero K and V rows.  The wave still issues its four copies (the
+  // vmcnt waits count them), all from the zero row kZeroKV.
   auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
     int key0 = min((t_begin + j) * kKT + 8 * wv, kmax);
@@ -670,7 +659,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 256;
       if (bad) kp = kZeroKV;
       vp = kp + 256;
-      if (lane == 0) *(FW_LDS uint8_t *)(pflags_base + buf * kPPWaves + wv) = bad ? 1 : 0;
     } else {
       kp = kbase_p + (size_t)key0 * kstB;
       vp = vbase_p + (size_t)key0 * vstB;
@@ -795,16 +783,14 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // partial row sum overflows 2^16 (a score more than ~11 above the anchor) or
   // a row sees its first valid key take the slow path (row max, new anchor,
   // O/l rescale, exponentiate again).
-  // fl0 / fl1: bytes of the tile's 8-key row groups 0-3 / 4-7 whose page id
-  // is invalid (nonzero = masked).
-  auto softmax = [&](int t, bf16x8_t (&pop)[4], uint32_t fl0, uint32_t fl1) __attribute__((always_inline)) {
+  auto softmax = [&](int t, bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
     const int kb = t * kKT;
     // the scores arrive as s - anchor (the MFMA accumulated onto -anchor, or
     // the softcap subtracts it)
     const float m_qk = m_run == -INFINITY ? 0.f : m_run;
     if constexpr (SOFTCAP) softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
-                      kb + kKT <= sk_len && (fl0 | fl1) == 0;
+                      kb + kKT <= sk_len;
     bool row_has_key = true;
     if (!full) {
 #pragma unroll
@@ -812,9 +798,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-          const uint32_t flw = st ? fl1 : fl0;
-          const bool badk = (flw >> (8 * (e >> 2))) & 0xffu;
-          sacc[st][e] = (key >= r_lo && key < r_hi && !badk) ? sacc[st][e] : -INFINITY;
+          sacc[st][e] = (key >= r_lo && key < r_hi) ? sacc[st][e] : -INFINITY;
         }
       row_has_key = max(r_lo, kb) < min(r_hi, kb + kKT);
     }
@@ -928,15 +912,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
           if (j + 3 < T) page_next = table_sload(j + 3, w);  // for the next body
         }
       }
-      if (j < T) {
-        uint32_t fl0 = 0, fl1 = 0;  // invalid-page flags of tile j's row groups
-        if constexpr (MODE == FW_KV_PAGED) {
-          const u32x2_t fl = *(const FW_LDS u32x2_t *)(pflags_base + 8 * B);
-          fl0 = __builtin_amdgcn_readfirstlane(fl[0]);
-          fl1 = __builtin_amdgcn_readfirstlane(fl[1]);
-        }
-        softmax(t_begin + j, pops, fl0, fl1);
-      }
+      if (j < T) softmax(t_begin + j, pops);
       mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
       if (grp == 0) {
         if (copy) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // tile j+1 in

@@ -19,8 +19,8 @@
  *                      metadata is trusted as in the reference (no checks
  *                      with a host round trip), with one rule for a page id
  *                      outside [0, num_pages): it is never dereferenced;
- *                      writes to it are dropped and its keys are masked
- *                      (they take no part in any softmax).
+ *                      writes to it are dropped and its keys read as zero K
+ *                      and V rows (score 0, value 0).
  */
 #ifndef FLYWHEEL_HIP_H
 #define FLYWHEEL_HIP_H

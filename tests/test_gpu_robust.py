@@ -5,7 +5,7 @@
   kernels/fwd_paged.py:285-290, kernels/decode.py:836; its test
   tests/softmax_attention/test_paged.py:465 pads with NaN);
 * a block-table entry outside [0, num_pages) is never dereferenced: writes to
-  it are dropped and its keys are masked;
+  it are dropped and its keys read as zero K and V rows;
 * k_descale / v_descale given as device tensors are read on the device: the
   result equals the Python-float call bit for bit, and the call needs no host
   synchronisation (it can be captured into a graph).
@@ -136,15 +136,15 @@ def test_verify_window_and_chunked_prefill_ignore_nan(dtype):
 
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
 @pytest.mark.parametrize("bad_id", [-1, 1 << 30])
-def test_invalid_page_ids_are_masked(dtype, bad_id):
-    """Decode (with the fused append) and the paged varlen prefill over a
-    table with out-of-range entries: their keys drop out of the softmax and
-    nothing is written through them.  With no causal / window mask the
-    expected result is the oracle over the table with those pages removed."""
+def test_invalid_page_ids_read_as_zero_rows(dtype, bad_id):
+    """Decode (with the fused append), the folded verify window and the paged
+    varlen prefill over a table with out-of-range entries: nothing is read or
+    written through them, and their keys act as zero K and V rows.  Expected:
+    the oracle over the same table with those entries pointing at a page of
+    zeros."""
     announce(f"invalid page ids {dtype} id={bad_id}")
     rng = np.random.default_rng(42)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
-    page = 16
     lengths = [64, 700, 333, 1500]
     case = PagedCase(rng, batch=4, nheads=8, nheads_k=2, lengths=lengths, new_tokens=[1] * 4,
                      dtype=dt, extra_pages=2)
@@ -163,35 +163,27 @@ def test_invalid_page_ids_are_masked(dtype, bad_id):
     torch.cuda.synchronize()
     exp_pool = case.expected_pool()
     np.testing.assert_array_equal(codes_of(pool), exp_pool)
-    # compacted view: the valid pages in order, the lengths reduced
     totals = case.lengths + 1
     kp, vp = case.kv_pages(exp_pool)
-    kp, vp = np.nan_to_num(kp, nan=0.0), np.nan_to_num(vp, nan=0.0)
-    keep_t, keep_l = [], []
-    for r in range(4):
-        n_pages = -(-int(totals[r]) // page)
-        rows = [p for i, p in enumerate(table[r, :n_pages]) if i not in bad[r]]
-        keep_t.append(rows)
-        keep_l.append(int(totals[r]) - page * len(bad[r]))
-    width = max(len(t) for t in keep_t)
-    ctab = np.zeros((4, width), np.int64)
-    for r, t in enumerate(keep_t):
-        ctab[r, :len(t)] = t
-    krows, vrows = P.gather_rows(kp, ctab), P.gather_rows(vp, ctab)
-    ro, rl = A.kvcache_reference(q, krows, vrows, np.array(keep_l))
+    zero = kp.shape[0]  # an extra all-zero page stands for every invalid id
+    kp = np.concatenate([np.nan_to_num(kp, nan=0.0), np.zeros_like(kp[:1])])
+    vp = np.concatenate([np.nan_to_num(vp, nan=0.0), np.zeros_like(vp[:1])])
+    ztab = np.where((table < 0) | (table >= zero), zero, table)
+    krows, vrows = clean_rows(P.gather_rows(kp, ztab), P.gather_rows(vp, ztab), totals)
+    ro, rl = A.kvcache_reference(q, krows, vrows, totals)
     assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
     assert_lse(lse.cpu().numpy(), rl)
-    # paged varlen prefill over the same table (no causal mask)
+    # paged varlen prefill over the same table, causal with a window
     qlens = np.array([5, 300, 1, 64])
     cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
     qp = randn(rng, (int(cu[-1]), 8, 128))
     out2, lse2 = flash_attn_varlen_func(
         to_dev_bf16(np.ascontiguousarray(qp.transpose(1, 0, 2))), pool, None,
-        torch.tensor(cu, device=DEV), None, int(qlens.max()), int(totals.max()), causal=False,
-        return_softmax_lse=True, block_table=torch.tensor(table, device=DEV),
+        torch.tensor(cu, device=DEV), None, int(qlens.max()), int(totals.max()), causal=True,
+        window_size=(200, 0), return_softmax_lse=True, block_table=torch.tensor(table, device=DEV),
         seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), nheads_k=2)
     torch.cuda.synchronize()
-    ro2, rl2 = A.ragged_reference(qp, kp, vp, cu, np.array(keep_l), ctab, causal=False,
+    ro2, rl2 = A.ragged_reference(qp, kp, vp, cu, totals, ztab, causal=True, window_left=200,
                                   round_scaled_q=True)
     assert_close(out2.float().cpu().numpy().transpose(1, 0, 2), ro2, fp8=dtype != "bf16")
     assert_lse(lse2.cpu().numpy(), rl2)
