@@ -1,25 +1,30 @@
-// Paged decode with the new token's append fused in, split-K over waves, and
-// a log-sum-exp merge of the split partials.
+// Paged decode with the new token's append fused in, a stream-K split of the
+// batch's keys over the GPU, and a log-sum-exp merge of the partials.
 //
 // Replaces the reference's persistent decode kernel (flywheel_tpu/
 // softmax_attention/kernels/decode.py:463-1915, called from
 // flash_attn_kvcache_pallas :2046-2475).  The reference walks a row's KV blocks
-// sequentially in one core with a static-anchor softmax; here each wave owns
-// one (row, KV head, split of `split_keys` keys) work item with an exact
-// running max, and fw_decode_combine merges the items of a row.
+// sequentially in one core with a static-anchor softmax.  Here the visible
+// keys of all rows, in 32-key tiles, are laid end to end and cut into NW equal
+// ranges, one per workgroup (NW = the workgroups the GPU runs at once), so
+// every workgroup streams the same number of bytes whatever the row lengths.
+// A range that covers parts of several rows yields one partial per (row,
+// range) segment; fw_decode_combine merges a row's segments.
 //
-// Work item (one wave64):
+// Workgroup = up to 8 waves = the KV heads (x q tiles) of one segment, so a
+// token row of the pool (all KV heads' K and V) is read by one CU.
+// Work item (one wave64) of a segment:
 //   rows    = the KV head's folded query rows r = t * G + j (token t of the
 //             verify window, head j of the GQA group), 16 per q tile;
-//   keys    = [split start, split end) of the row's visible range, in tiles of
-//             32 keys = two 16-key sub-tiles (a sub-tile never crosses a page
-//             because page_size % 16 == 0).
+//   keys    = the segment's keys, in tiles of 32 keys = two 16-key sub-tiles
+//             (a sub-tile never crosses a page because page_size % 16 == 0).
 //   S^T (16 keys x 16 rows) = K (A operand, straight from HBM in MFMA layout)
 //                             x Q^T (B operand, resident in registers);
-//   O^T (16 dims x 16 rows) += V^T (A operand: 8-byte V loads that cover whole
-//                             128-byte lines, transposed by v_perm)
+//   O^T (16 dims x 16 rows) += V^T (A operand: V loads that cover whole
+//                             rows, transposed in registers by v_perm)
 //                             x P^T (B operand, the S^T registers as bf16).
 // Both products use v_mfma_f32_16x16x32_bf16; nothing goes through LDS.
+// head_dim D is 128 or 256 (D / 128 "halves" of V and O).
 #include "fw_common.h"
 
 #include <algorithm>
@@ -37,8 +42,8 @@ struct DecodeArgs {
   const int32_t *cache_seqlens;
   const int32_t *block_table;
   const int32_t *num_active;
-  float *ws_o;   // [items][rows_item][128] unnormalised partial O
-  float2 *ws_ml; // [items][rows_item] (running max in log2 units, row sum)
+  float *ws_o;   // [segments][items][rows_item][D] unnormalised partial O
+  float2 *ws_ml; // [segments][items][rows_item] (running max in log2 units, row sum)
   int B, Sq, H, Hk, G, Rq, n_qtiles, P, max_pages, CH;
   // Token-row geometry: a token row holds CH head rows; KV head h's K row is
   // head row kstep*h and its V row head row kstep*h + vhead, vdelta bytes
@@ -46,9 +51,11 @@ struct DecodeArgs {
   // kstep 1, vhead 0, vdelta = v_cache - k_cache).
   int kstep, vhead;
   int64_t vdelta;
-  int split_keys, nsplit;
+  int nw;          // stream-K workgroups (per head group): the key ranges
+  int chunk_keys;  // keys whose block-table entries one prefetch covers
   int seqlen_add, has_new, causal, window_left, num_pages;
   int rows_item;      // partial rows stored per work item: min(16, Rq)
+  int waves;          // work items per workgroup
   float qscale;       // folded into q before its bf16 rounding
   float softcap_log2; // softcap * log2(e), 0 = off
   // Device descale scalars (or null: k_descale is already in qscale).  With
@@ -58,41 +65,105 @@ struct DecodeArgs {
   float sm_scale, softcap;
 };
 
-constexpr int kD = 128;
 constexpr float kPsumTrigger = 65536.f;  // lane partial-sum bound of the fast path
 constexpr int kStageRow = 132;           // padded f32 row of the partial-O staging slot
-constexpr int kTblPerLane = 4;           // block-table entries a lane prefetches per split
+constexpr int kTblPerLane = 4;           // block-table entries a lane prefetches per chunk
+constexpr int kMaxWaves = 8;
+// Work items (waves) per workgroup: 8 at d128 (two waves per SIMD), 4 at
+// d256 (one wave per SIMD with the whole register file).
+template <int D> constexpr int kWgWaves = D > 128 ? 4 : 8;
 
+// ---------------------------------------------------------------- row ranges
 // Visible key range of a row: [lo, total) overall; per folded row the causal
 // limit drops by (Sq - 1 - t).
+__device__ __forceinline__ int row_total(const DecodeArgs &a, int b) {
+  return a.cache_seqlens[b] + (a.has_new ? 1 : a.seqlen_add);
+}
 __device__ __forceinline__ int row_lo_all(const DecodeArgs &a, int total) {
   if (a.window_left < 0) return 0;
   int lo = total - a.Sq - a.window_left;  // token 0's window start
   return lo > 0 ? lo : 0;
 }
+// The row's first visible key rounded down to a tile, and its tile count
+// (0 for a row past num_active or with no key).
+__device__ __forceinline__ int row_tiles(const DecodeArgs &a, int b, int nact, int &base) {
+  base = 0;
+  if (b >= nact) return 0;
+  const int total = row_total(a, b);
+  base = row_lo_all(a, total) & ~31;
+  return total > base ? (total - base + 31) >> 5 : 0;
+}
+__device__ __forceinline__ int active_rows(const DecodeArgs &a) {
+  return a.num_active ? min(max(*a.num_active, 0), a.B) : a.B;
+}
+// Inclusive prefix sum over a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+// Tiles of all rows (every lane gets the total).
+__device__ __forceinline__ int total_tiles(const DecodeArgs &a, int nact, int lane) {
+  int sum = 0;
+  for (int c = 0; c < a.B; c += 64) {
+    int base;
+    const int t = c + lane < a.B ? row_tiles(a, c + lane, nact, base) : 0;
+    sum += wave_sum(t);
+  }
+  return sum;
+}
+// The first row whose tiles reach past global tile g0, and the tiles of the
+// rows before it (wave-uniform).  Returns B when g0 >= the total.
+__device__ __forceinline__ int first_row_after(const DecodeArgs &a, int nact, int lane, int g0,
+                                               int &off) {
+  int acc = 0;
+  for (int c = 0; c < a.B; c += 64) {
+    int base;
+    const int t = c + lane < a.B ? row_tiles(a, c + lane, nact, base) : 0;
+    const int incl = wave_incl_scan(t, lane);
+    const uint64_t hit = __ballot(acc + incl > g0);
+    if (hit) {
+      const int f = __builtin_ctzll(hit);
+      off = acc + __shfl(incl - t, f, 64);
+      return c + f;
+    }
+    acc += __shfl(incl, 63, 64);
+  }
+  off = acc;
+  return a.B;
+}
 
+// ---------------------------------------------------------------- K / V tiles
 // K of one key row: bf16 is loaded straight into the A-operand registers;
-// fp8 stays as raw bytes (two 16-byte loads) until the compute stage.
-template <int KV>
+// fp8 stays as raw bytes (16-byte loads) until the compute stage.
+template <int KV, int D>
 struct KRow {
-  typename std::conditional<KV == FW_BF16, bf16x8_t, u32x4_t>::type w[KV == FW_BF16 ? 4 : 2];
+  typename std::conditional<KV == FW_BF16, bf16x8_t, u32x4_t>::type w[KV == FW_BF16 ? D / 32 : D / 64];
 };
 
-template <int KV>
-__device__ __forceinline__ void load_k_row(const uint8_t *row, int g, KRow<KV> &k) {
+template <int KV, int D>
+__device__ __forceinline__ void load_k_row(const uint8_t *row, int g, KRow<KV, D> &k) {
   if constexpr (KV == FW_BF16) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < D / 32; ++j)
       k.w[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(row + 64 * j + 16 * g));
   } else {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) k.w[hh] = *(const u32x4_t *)(row + 64 * hh + 16 * g);
+    for (int hh = 0; hh < D / 64; ++hh) k.w[hh] = *(const u32x4_t *)(row + 64 * hh + 16 * g);
   }
 }
 
 // A operand of MFMA step j from a loaded K row.
-template <int KV>
-__device__ __forceinline__ bf16x8_t k_operand(const KRow<KV> &k, int j) {
+template <int KV, int D>
+__device__ __forceinline__ bf16x8_t k_operand(const KRow<KV, D> &k, int j) {
   if constexpr (KV == FW_BF16) {
     return k.w[j];
   } else {
@@ -114,390 +185,442 @@ __device__ __forceinline__ int qk_dim(int j, int g) {
   else return 64 * (j >> 1) + 16 * g + 8 * (j & 1);
 }
 
-template <int KV>
+template <int KV, int D>
 struct DecodeTile {
-  KRow<KV> krow[2];  // K of the two 16-key sub-tiles (lane row n)
-  // V of keys 4g+i / 16+4g+i, dims 8n .. 8n+7 (16 or 8 bytes a key)
-  typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8];
+  static constexpr int VH = D / 128;
+  KRow<KV, D> krow[2];  // K of the two 16-key sub-tiles (lane row n)
+  // V of keys 4g+i / 16+4g+i, dims 128h + 8n .. +7 (16 or 8 bytes a key)
+  typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8][VH];
   bool bad[2];  // a sub-tile's page id is out of range: its keys read as zeros
 };
 
+// Waves per SIMD the decode kernel is built for: 2 at d128 (an 8-wave
+// workgroup per CU), 1 at d256 (about twice the registers).
+template <int KV, int D> constexpr int kDecodeOcc = D > 128 ? 1 : 2;
 
-// Register-ring depth and waves/SIMD: bf16 2 stages at 2 waves; fp8 2 stages
-// at 3 waves (its tiles are half the bytes, so more waves keep more in flight).
-template <int KV> constexpr int kDecodeStages = 2;
-template <int KV> constexpr int kDecodeWaves = KV == FW_BF16 ? 2 : 3;
-
-template <int KV>
-__global__ __launch_bounds__(256, kDecodeWaves<KV>) void fw_decode_kernel(DecodeArgs a) {
+template <int KV, int D>
+__global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_decode_kernel(DecodeArgs a) {
   constexpr int EB = KV == FW_BF16 ? 2 : 1;  // bytes per cache element
-  __shared__ __attribute__((aligned(16))) float stage[4][16 * kStageRow];  // partial-O staging
+  constexpr int VH = D / 128;
+  constexpr int VB = KV == FW_BF16 ? 16 : 8;  // bytes of one lane's V piece
+  __shared__ __attribute__((aligned(16))) float stage[kMaxWaves][16 * kStageRow];
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;
-  const int g = lane >> 4;
-  // A workgroup's waves are the KV heads (and q tiles) of one (row, split):
-  // they walk the same pages at the same time.
-  const int s = blockIdx.x;
-  const int hq_item = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (hq_item >= a.Hk * a.n_qtiles) return;
-  const int h = hq_item / a.n_qtiles;
-  const int qt = hq_item % a.n_qtiles;
-  const int b = blockIdx.z;
-  if (s >= a.nsplit) return;
-  if (a.num_active && b >= *a.num_active) return;
+  const int wv = threadIdx.x >> 6;
+  const int item = blockIdx.y * a.waves + wv;  // (KV head, q tile)
+  const int n_items = a.Hk * a.n_qtiles;
+  if (item >= n_items) return;
+  const int h = item / a.n_qtiles;
+  const int qt = item % a.n_qtiles;
+  const int x = blockIdx.x;
 
-  const int L0 = a.cache_seqlens[b];
-  const int total = L0 + (a.has_new ? 1 : a.seqlen_add);
-  const int lo_all = row_lo_all(a, total);
-  const int base = lo_all & ~31;
-  const int k_begin = base + s * a.split_keys;
-  if (k_begin >= total) return;
-  const int k_end = min(total, k_begin + a.split_keys);
-  const int nsplit_row = (total - base + a.split_keys - 1) / a.split_keys;
-  const int32_t *table = a.block_table + (size_t)b * a.max_pages;
-  const size_t row_bytes = (size_t)a.CH * kD * EB;
+  // ---- this workgroup's share of the batch's key tiles
+  const int nact = active_rows(a);
+  const int total_t = total_tiles(a, nact, lane);
+  const int per = (total_t + a.nw - 1) / a.nw;
+  const int g0 = x * per, g1 = min(g0 + per, total_t);
+  if (g0 >= g1) return;
+  int off;
+  int b = first_row_after(a, nact, lane, g0, off);
 
-  // ---- fused append: the last split's wave of q tile 0 writes the new row.
-  // (A row already at its capacity has no slot: nothing is written.)
-  // An out-of-range page id is never written (as in fw_append_kernel).
-  const int new_page = a.has_new && L0 / a.P < a.max_pages ? table[L0 / a.P] : -1;
-  if (a.has_new && qt == 0 && s == nsplit_row - 1 && new_page >= 0 && new_page < a.num_pages) {
-    const int page = new_page;
-    uint8_t *dst = a.cache + ((size_t)page * a.P + L0 % a.P) * row_bytes;
-    const size_t hb = (size_t)kD * EB;  // bytes of one head row
-    const uint8_t *kn = a.k_new + ((size_t)b * a.Hk + h) * hb;
-    const uint8_t *vn = a.v_new + ((size_t)b * a.Hk + h) * hb;
-    uint8_t *kdst = dst + (size_t)(a.kstep * h) * hb;
-    uint8_t *vdst = dst + a.vdelta + (size_t)(a.kstep * h + a.vhead) * hb;
-    for (int off = lane * 4; off < (int)hb; off += 256) {
-      *(uint32_t *)(kdst + off) = *(const uint32_t *)(kn + off);
-      *(uint32_t *)(vdst + off) = *(const uint32_t *)(vn + off);
-    }
-    if (h == a.Hk - 1) {  // an fp8 pool's zero pad head
-      for (int hp = 2 * a.Hk; hp < a.CH; ++hp)
-        for (int off = lane * 4; off < (int)hb; off += 256)
-          *(uint32_t *)(dst + hp * hb + off) = 0u;
-    }
-  }
-
-  // ---- Q^T operand: row r = qt*16 + n (zero if past Rq), scaled and rounded.
-  const int r = qt * 16 + n;
-  const bool row_ok = r < a.Rq;
-  const int tok = row_ok ? r / a.G : 0;
-  const int hq = h * a.G + (row_ok ? r % a.G : 0);
+  const size_t row_bytes = (size_t)a.CH * D * EB;
+  const size_t hb = (size_t)D * EB;  // bytes of one head row
+  const size_t kh_off = (size_t)(a.kstep * h) * hb;
+  const size_t vh_off = (size_t)(a.kstep * h + a.vhead) * hb;
+  const uint32_t kh_lane = (uint32_t)kh_off;
+  const uint32_t rb = (uint32_t)row_bytes;
   float qscale = a.qscale;
   if (a.kd) {
     const float sm = a.sm_scale * *a.kd;
     qscale = a.softcap > 0.f ? sm / a.softcap : sm * kLog2e;
   }
-  bf16x8_t qop[4];
-  {
-    const uint16_t *qrow = a.q + (((size_t)b * a.Sq + tok) * a.H + hq) * kD;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t w = *(const u32x4_t *)(qrow + qk_dim<KV>(j, g));
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = row_ok ? pack_bf16(bf16_lo(w[e]) * qscale, bf16_hi(w[e]) * qscale) : 0u;
-      qop[j] = __builtin_bit_cast(bf16x8_t, o);
-    }
-  }
-  // Row-visible key limits for this lane's row n.
-  const int hi_r = a.causal ? total - (a.Sq - 1 - tok) : total;
-  const int lo_r = a.window_left < 0 ? 0 : max(0, hi_r - 1 - a.window_left);
-  const int key_lo = max(lo_r, k_begin);
-  const int key_hi = min(hi_r, k_end);
 
-  f32x4_t oacc[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) oacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (; b < a.B && off < g1; ++b) {
+    // Per-lane values are derived afresh in every segment from an opaque
+    // copy of the lane id: hoisted out of this loop they would stay live
+    // through the whole kernel (measured: +23 registers and spills).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int n = ln & 15;
+    const int g = ln >> 4;
+    const uint32_t vh_lane = (uint32_t)(vh_off + VB * n);
+    const int r = qt * 16 + n;
+    const bool row_ok = r < a.Rq;
+    const int tok = row_ok ? r / a.G : 0;
+    const int hq = h * a.G + (row_ok ? r % a.G : 0);
+    int base;
+    const int T = row_tiles(a, b, nact, base);
+    const int seg_lo = max(g0 - off, 0), seg_hi = min(g1 - off, T);
+    off += T;
+    if (seg_hi <= seg_lo) continue;
+    const int L0 = a.cache_seqlens[b];
+    const int total = L0 + (a.has_new ? 1 : a.seqlen_add);
+    const int k_begin = base + 32 * seg_lo;
+    const int k_end = min(total, base + 32 * seg_hi);
+    const bool last_seg = seg_hi == T;
+    const int32_t *table = a.block_table + (size_t)b * a.max_pages;
 
-  const size_t kh_off = (size_t)(a.kstep * h) * kD * EB;
-  const size_t vh_off = (size_t)(a.kstep * h + a.vhead) * kD * EB;
-  const size_t new_off = ((size_t)b * a.Hk + h) * kD * EB;
-  const int last_key = total - 1;
-  // Block-table entries of the whole split, kTblPerLane per lane (a split
-  // spans at most 64 * kTblPerLane pages); a sub-tile's page is then a
-  // readlane, off the load path.
-  const int first_page = k_begin / a.P;
-  int tbl_lane[kTblPerLane];
-#pragma unroll
-  for (int t = 0; t < kTblPerLane; ++t) tbl_lane[t] = table[min(first_page + 64 * t + lane, a.max_pages - 1)];
-
-  // Cache keys of this split are [k_begin, k_stop): the appended token (key
-  // L0) is folded in after the loop from k_new / v_new.
-  const int k_stop = a.has_new ? min(k_end, L0) : k_end;
-  const int last_cache_key = k_stop - 1;
-  // Per-lane byte offsets inside a 16-row sub-tile: a load is the sub-tile's
-  // uniform page row pointer plus a 32-bit lane offset.  Rows past the last
-  // cache key of the split (slots not written yet: their contents may be
-  // anything, NaN included, and 0 * NaN would poison the PV product) are
-  // clamped onto that key's row, which the masks then hide.
-  const uint32_t kh_lane = (uint32_t)kh_off;
-  const uint32_t vh_lane = (uint32_t)(vh_off + (KV == FW_BF16 ? 16 : 8) * n);
-  const uint32_t rb = (uint32_t)row_bytes;
-
-  // Loads are branch-free so the compiler can count them: a tile past the end
-  // is clamped onto the last valid sub-tile (an L2 hit, never used).  A page
-  // id outside [0, num_pages) is never dereferenced: the loads read page 0
-  // and the compute stage replaces the sub-tile by zero K and V rows.
-  auto load_tile = [&](int tb, DecodeTile<KV> &tl) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int sbc = min(tb + 16 * sub, last_cache_key) & ~15;  // clamp into valid pages
-      const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
-      int page = __builtin_amdgcn_readlane(tbl_lane[0], pi & 63);
-#pragma unroll
-      for (int t = 1; t < kTblPerLane; ++t)
-        page = (pi >> 6) == t ? __builtin_amdgcn_readlane(tbl_lane[t], pi & 63) : page;
-      const bool bad = page < 0 || page >= a.num_pages;
-      tl.bad[sub] = bad;
-      page = bad ? 0 : page;
-      const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
-      const uint8_t *vrow = prow + a.vdelta;
-      const uint32_t lim = (uint32_t)(last_cache_key - sbc);  // rows 0..lim hold cache keys
-      load_k_row<KV>(prow + (min((uint32_t)n, lim) * rb + kh_lane), g, tl.krow[sub]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t vo = min((uint32_t)(4 * g + i), lim) * rb + vh_lane;
-        if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = *(const u32x4_t *)(vrow + vo);
-        else tl.vraw[4 * sub + i] = *(const u32x2_t *)(vrow + vo);
+    // ---- fused append: the row's last segment's wave of q tile 0 writes the
+    // new row.  (A row already at its capacity has no slot: nothing is
+    // written; an out-of-range page id is never written, as in
+    // fw_append_kernel.)
+    if (a.has_new && qt == 0 && last_seg && L0 / a.P < a.max_pages) {
+      const int page = table[L0 / a.P];
+      if (page >= 0 && page < a.num_pages) {
+        uint8_t *dst = a.cache + ((size_t)page * a.P + L0 % a.P) * row_bytes;
+        const uint8_t *kn = a.k_new + ((size_t)b * a.Hk + h) * hb;
+        const uint8_t *vn = a.v_new + ((size_t)b * a.Hk + h) * hb;
+        uint8_t *kdst = dst + kh_off;
+        uint8_t *vdst = dst + a.vdelta + vh_off;
+        for (int o = lane * 4; o < (int)hb; o += 256) {
+          *(uint32_t *)(kdst + o) = *(const uint32_t *)(kn + o);
+          *(uint32_t *)(vdst + o) = *(const uint32_t *)(vn + o);
+        }
+        if (h == a.Hk - 1) {  // an fp8 pool's zero pad head
+          for (int hp = 2 * a.Hk; hp < a.CH; ++hp)
+            for (int o = lane * 4; o < (int)hb; o += 256)
+              *(uint32_t *)(dst + hp * hb + o) = 0u;
+        }
       }
     }
-  };
-  // The appended token's K/V, from k_new / v_new into every key slot (only the
-  // slot of key L0 is unmasked).
-  auto load_new_tile = [&](DecodeTile<KV> &tl) {
-    tl.bad[0] = tl.bad[1] = false;
-    const uint8_t *kp = a.k_new + new_off;
-    const uint8_t *vp = a.v_new + new_off + (KV == FW_BF16 ? 16 : 8) * n;
+
+    // ---- Q^T operand: row r = qt*16 + n (zero if past Rq), scaled and rounded.
+    bf16x8_t qop[D / 32];
+    {
+      const uint16_t *qrow = a.q + (((size_t)b * a.Sq + tok) * a.H + hq) * D;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) load_k_row<KV>(kp, g, tl.krow[sub]);
+      for (int j = 0; j < D / 32; ++j) {
+        u32x4_t w = *(const u32x4_t *)(qrow + qk_dim<KV>(j, g));
+        u32x4_t o;
 #pragma unroll
-    for (int k8 = 0; k8 < 8; ++k8) {
-      if constexpr (KV == FW_BF16) tl.vraw[k8] = *(const u32x4_t *)vp;
-      else tl.vraw[k8] = *(const u32x2_t *)vp;
+        for (int e = 0; e < 4; ++e)
+          o[e] = row_ok ? pack_bf16(bf16_lo(w[e]) * qscale, bf16_hi(w[e]) * qscale) : 0u;
+        qop[j] = __builtin_bit_cast(bf16x8_t, o);
+      }
     }
-  };
+    // Row-visible key limits for this lane's row n.
+    const int hi_r = a.causal ? total - (a.Sq - 1 - tok) : total;
+    const int lo_r = a.window_left < 0 ? 0 : max(0, hi_r - 1 - a.window_left);
+    const int key_lo = max(lo_r, k_begin);
+    const int key_hi = min(hi_r, k_end);
 
-  const int row_hi = min(key_hi, k_stop);
-  // Keys every row of this wave sees: tiles inside need no mask.
-  int all_lo = row_ok ? key_lo : k_begin, all_hi = row_ok ? row_hi : k_stop;
+    f32x4_t oacc[8 * VH];
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    all_lo = max(all_lo, __shfl_xor(all_lo, m, 64));
-    all_hi = min(all_hi, __shfl_xor(all_hi, m, 64));
-  }
+    for (int c = 0; c < 8 * VH; ++c) oacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
 
-  auto compute_tile = [&](int tb, DecodeTile<KV> &tl, int lo, int hi, bool edge) {
-    // The keys of an invalid page id read as zero K and V rows (the loads
-    // used page 0, which may hold anything).
-    if (tl.bad[0] || tl.bad[1]) {
+    // Cache keys of this segment are [k_begin, k_stop): the appended token
+    // (key L0) is folded in after the loop from k_new / v_new.
+    const int k_stop = a.has_new ? min(k_end, L0) : k_end;
+    const int row_hi = min(key_hi, k_stop);
+    // Keys every row of this wave sees: tiles inside need no mask.
+    int all_lo = row_ok ? key_lo : k_begin, all_hi = row_ok ? row_hi : k_stop;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      all_lo = max(all_lo, __shfl_xor(all_lo, m, 64));
+      all_hi = min(all_hi, __shfl_xor(all_hi, m, 64));
+    }
+    auto edge = [&](int tb) { return tb < all_lo || tb + 32 > all_hi; };
+
+    auto compute_tile = [&](int tb, DecodeTile<KV, D> &tl, int lo, int hi, bool is_edge) {
+      // The keys of an invalid page id read as zero K and V rows (the loads
+      // used page 0, which may hold anything).
+      if (tl.bad[0] || tl.bad[1]) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+          if (tl.bad[sub]) {
+#pragma unroll
+            for (int j = 0; j < (KV == FW_BF16 ? D / 32 : D / 64); ++j)
+              tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int vh = 0; vh < VH; ++vh)
+                tl.vraw[4 * sub + i][vh] = std::remove_reference_t<decltype(tl.vraw[0][0])>{};
+          }
+      }
+      // -------- S^T = K Q^T
+      f32x4_t sacc[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        sacc[sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j)
+          sacc[sub] = mfma16(k_operand<KV, D>(tl.krow[sub], j), qop[j], sacc[sub]);
+      }
+      // -------- online softmax on this lane's 8 (row n, key) scores
+      if (a.softcap_log2 != 0.f) softcap_scores<2, 4>(sacc, a.softcap_log2);
+      float sc[8];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
-        if (tl.bad[sub]) {
 #pragma unroll
-          for (int j = 0; j < (KV == FW_BF16 ? 4 : 2); ++j)
-            tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
+        for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
+      if (is_edge) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if constexpr (KV == FW_BF16) tl.vraw[4 * sub + i] = u32x4_t{0, 0, 0, 0};
-            else tl.vraw[4 * sub + i] = u32x2_t{0, 0};
+        for (int e = 0; e < 8; ++e) {
+          const int key = tb + 16 * (e >> 2) + 4 * g + (e & 3);
+          sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
+        }
+      }
+      // Static anchor: exponentiate against the row's anchor m_run; only when
+      // a lane's partial sum overflows 2^16 (a score more than ~13 above the
+      // anchor) or a row meets its first valid key does the wave reduce the
+      // row max across its four lane groups and rescale O and l.
+      float psum;
+      uint32_t pw[4];
+      auto exponentiate = [&]() {
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        psum = 0.f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float p0 = fast_exp2(sc[2 * p] - m_use);
+          const float p1 = fast_exp2(sc[2 * p + 1] - m_use);
+          psum += p0 + p1;
+          pw[p] = pack_bf16(p0, p1);
+        }
+      };
+      exponentiate();
+      bool fresh = false;
+      if (m_run == -INFINITY) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fresh = fresh || sc[e] != -INFINITY;
+      }
+      if (__any(!(psum <= kPsumTrigger) || fresh)) {
+        asm volatile("" ::: "memory");  // a real branch: never if-converted
+        float tmax = sc[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sc[e]);
+        tmax = wave_max_xor(tmax, 16);
+        tmax = wave_max_xor(tmax, 32);
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int c = 0; c < 8 * VH; ++c) oacc[c] *= alpha;
+        exponentiate();
+      }
+      l_run += psum;
+      const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, (u32x4_t){pw[0], pw[1], pw[2], pw[3]});
+      // -------- O^T += V^T P^T, 8 tiles of 16 dims per half; tile 8vh + c
+      // holds dim 128vh + 8m + c.  Word w of a key's V (dims 8n+2w, 8n+2w+1)
+      // feeds tiles 2w and 2w+1.
+#pragma unroll
+      for (int vh = 0; vh < VH; ++vh)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t vk[8];
+#pragma unroll
+          for (int k8 = 0; k8 < 8; ++k8) {
+            if constexpr (KV == FW_BF16) vk[k8] = tl.vraw[k8][vh][w];
+            else vk[k8] = fp8x2_to_bf16x2<KV>(tl.vraw[k8][vh][w >> 1], w & 1);
+          }
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            u32x4_t vw;
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+              vw[p] = half ? perm_hi(vk[2 * p], vk[2 * p + 1]) : perm_lo(vk[2 * p], vk[2 * p + 1]);
+            oacc[8 * vh + 2 * w + half] =
+                mfma16(__builtin_bit_cast(bf16x8_t, vw), pop, oacc[8 * vh + 2 * w + half]);
           }
         }
-    }
-    // -------- S^T = K Q^T
-    f32x4_t sacc[2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      sacc[sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sacc[sub] = mfma16(k_operand<KV>(tl.krow[sub], j), qop[j], sacc[sub]);
-    }
-    // -------- online softmax on this lane's 8 (row n, key) scores
-    if (a.softcap_log2 != 0.f) softcap_scores<2, 4>(sacc, a.softcap_log2);
-    float sc[8];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[4 * sub + i] = sacc[sub][i];
-    if (edge) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = tb + 16 * (e >> 2) + 4 * g + (e & 3);
-        sc[e] = (key >= lo && key < hi) ? sc[e] : -INFINITY;
-      }
-    }
-    // Static anchor: exponentiate against the row's anchor m_run; only when a
-    // lane's partial sum overflows 2^16 (a score more than ~13 above the
-    // anchor) or a row meets its first valid key does the wave reduce the row
-    // max across its four lane groups and rescale O and l.
-    float psum;
-    uint32_t pw[4];
-    auto exponentiate = [&]() {
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      psum = 0.f;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const float p0 = fast_exp2(sc[2 * p] - m_use);
-        const float p1 = fast_exp2(sc[2 * p + 1] - m_use);
-        psum += p0 + p1;
-        pw[p] = pack_bf16(p0, p1);
-      }
     };
-    exponentiate();
-    bool fresh = false;
-    if (m_run == -INFINITY) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fresh = fresh || sc[e] != -INFINITY;
-    }
-    if (__any(!(psum <= kPsumTrigger) || fresh)) {
-      asm volatile("" ::: "memory");  // a real branch: never if-converted
-      float tmax = sc[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sc[e]);
-      tmax = wave_max_xor(tmax, 16);
-      tmax = wave_max_xor(tmax, 32);
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) oacc[c] *= alpha;
-      exponentiate();
-    }
-    l_run += psum;
-    const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, (u32x4_t){pw[0], pw[1], pw[2], pw[3]});
-    // -------- O^T += V^T P^T, 8 tiles of 16 dims; tile c holds dim 8m + c.
-    // Word w of a key's V (dims 8n+2w, 8n+2w+1) feeds tiles 2w and 2w+1.
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t vk[8];
-#pragma unroll
-      for (int k8 = 0; k8 < 8; ++k8) {
-        if constexpr (KV == FW_BF16) vk[k8] = tl.vraw[k8][w];
-        else vk[k8] = fp8x2_to_bf16x2<KV>(tl.vraw[k8][w >> 1], w & 1);
-      }
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4_t vw;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) vw[p] = half ? perm_hi(vk[2 * p], vk[2 * p + 1]) : perm_lo(vk[2 * p], vk[2 * p + 1]);
-        oacc[2 * w + half] = mfma16(__builtin_bit_cast(bf16x8_t, vw), pop, oacc[2 * w + half]);
-      }
-    }
-  };
 
-  // Register ring of two tile buffers: the next tile's loads are in flight
-  // while the current tile is computed.
-  const int last_tile = max(k_begin, (k_stop - 1) & ~31);
-  auto edge = [&](int tb) { return tb < all_lo || tb + 32 > all_hi; };
-  if (k_begin < k_stop) {
-    DecodeTile<KV> t0, t1;
-    load_tile(k_begin, t0);
-    for (int tb = k_begin;; tb += 64) {
-      load_tile(min(tb + 32, last_tile), t1);
-      compute_tile(tb, t0, key_lo, row_hi, edge(tb));
-      if (tb + 32 >= k_stop) break;
-      load_tile(min(tb + 64, last_tile), t0);
-      compute_tile(tb + 32, t1, key_lo, row_hi, edge(tb + 32));
-      if (tb + 64 >= k_stop) break;
+    // Cache keys in chunks whose block-table entries one prefetch covers
+    // (kTblPerLane per lane: up to 64 * kTblPerLane pages); a sub-tile's page
+    // is then a readlane, off the load path.  Chunks start on 32-key tiles,
+    // so no tile straddles two.
+    for (int cb = k_begin; cb < k_stop; cb += a.chunk_keys) {
+      const int ce = min(k_stop, cb + a.chunk_keys);
+      const int first_page = cb / a.P;
+      int tbl_lane[kTblPerLane];
+#pragma unroll
+      for (int t = 0; t < kTblPerLane; ++t)
+        tbl_lane[t] = table[min(first_page + 64 * t + lane, a.max_pages - 1)];
+      // The last key of the chunk: sub-tile starts are clamped onto it (a
+      // tile past the end re-reads the last sub-tile, an L2 hit, never used),
+      // and rows past it (slots not written yet, or the next chunk's) are
+      // clamped onto its row: their contents may be anything, NaN included,
+      // and 0 * NaN would poison the PV product; the masks hide them.
+      const int last_key = ce - 1;
+      // Loads are branch-free so the compiler can count them.  A page id
+      // outside [0, num_pages) is never dereferenced: the loads read page 0
+      // and the compute stage replaces the sub-tile by zero K and V rows.
+      auto load_tile = [&](int tb, DecodeTile<KV, D> &tl) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          const int sbc = min(tb + 16 * sub, last_key) & ~15;
+          const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
+          int page = __builtin_amdgcn_readlane(tbl_lane[0], pi & 63);
+#pragma unroll
+          for (int t = 1; t < kTblPerLane; ++t)
+            page = (pi >> 6) == t ? __builtin_amdgcn_readlane(tbl_lane[t], pi & 63) : page;
+          const bool bad = page < 0 || page >= a.num_pages;
+          tl.bad[sub] = bad;
+          page = bad ? 0 : page;
+          const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
+          const uint8_t *vrow = prow + a.vdelta;
+          const uint32_t lim = (uint32_t)(last_key - sbc);  // rows 0..lim hold cache keys
+          load_k_row<KV, D>(prow + (min((uint32_t)n, lim) * rb + kh_lane), g, tl.krow[sub]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t vo = min((uint32_t)(4 * g + i), lim) * rb + vh_lane;
+#pragma unroll
+            for (int vh = 0; vh < VH; ++vh) {
+              if constexpr (KV == FW_BF16)
+                tl.vraw[4 * sub + i][vh] = *(const u32x4_t *)(vrow + vo + 128 * EB * vh);
+              else
+                tl.vraw[4 * sub + i][vh] = *(const u32x2_t *)(vrow + vo + 128 * EB * vh);
+            }
+          }
+        }
+      };
+      // Register ring of two tile buffers: the next tile's loads are in
+      // flight while the current tile is computed.
+      const int last_tile = (ce - 1) & ~31;
+      DecodeTile<KV, D> t0, t1;
+      load_tile(cb, t0);
+      for (int tb = cb;; tb += 64) {
+        load_tile(min(tb + 32, last_tile), t1);
+        compute_tile(tb, t0, key_lo, row_hi, edge(tb));
+        if (tb + 32 >= ce) break;
+        load_tile(min(tb + 64, last_tile), t0);
+        compute_tile(tb + 32, t1, key_lo, row_hi, edge(tb + 32));
+        if (tb + 64 >= ce) break;
+      }
     }
-  }
-  if (a.has_new && L0 >= k_begin && L0 < k_end) {
-    DecodeTile<KV> tn;
-    load_new_tile(tn);
-    compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true);
-  }
+    // The appended token's K/V, from k_new / v_new into every key slot (only
+    // the slot of key L0 is unmasked).
+    if (a.has_new && L0 >= k_begin && L0 < k_end) {
+      DecodeTile<KV, D> tn;
+      tn.bad[0] = tn.bad[1] = false;
+      const size_t new_off = ((size_t)b * a.Hk + h) * hb;
+      const uint8_t *kp = a.k_new + new_off;
+      const uint8_t *vp = a.v_new + new_off + VB * n;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) load_k_row<KV, D>(kp, g, tn.krow[sub]);
+#pragma unroll
+      for (int k8 = 0; k8 < 8; ++k8)
+#pragma unroll
+        for (int vh = 0; vh < VH; ++vh) {
+          if constexpr (KV == FW_BF16) tn.vraw[k8][vh] = *(const u32x4_t *)(vp + 128 * EB * vh);
+          else tn.vraw[k8][vh] = *(const u32x2_t *)(vp + 128 * EB * vh);
+        }
+      compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true);
+    }
 
-  // ---- write the partial: rows n < Rq of this q tile.
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-  const size_t item = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit + s;
-  // The (16 rows x 128 dims) f32 partial goes out through a wave-private LDS
-  // slot so that every global store writes two whole 512-byte rows (lane
-  // order = address order); stored straight from the MFMA layout each
-  // instruction would scatter 64 16-byte pieces.  Rows are padded to 132
-  // floats: the 16 rows of one column group land on distinct banks.
-  float *st = stage[threadIdx.x >> 6];
+    // ---- write the partial of segment (x, b): rows n < Rq of this q tile.
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    const size_t slot = ((size_t)(x + b) * n_items + item) * a.rows_item;
+    // The (16 rows x D) f32 partial goes out through a wave-private LDS slot,
+    // 128 dims at a time, so that every global store writes two whole rows
+    // of 128 floats (lane order = address order); stored straight from the
+    // MFMA layout each instruction would scatter 64 16-byte pieces.  Rows are
+    // padded to 132 floats: the 16 rows of one column group land on distinct
+    // banks.
+    float *st = stage[wv];
+    const int rows_valid = min(16, a.Rq - qt * 16);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // tile c, reg i -> dim 32g + 8i + c
-    const f32x4_t v0 = {oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
-    const f32x4_t v1 = {oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]};
-    *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i) = v0;
-    *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i + 4) = v1;
-  }
-  const int rows_valid = min(16, a.Rq - qt * 16);
-  float *po = a.ws_o + item * a.rows_item * kD;
+    for (int vh = 0; vh < VH; ++vh) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int row = 2 * k + (lane >> 5), col = 4 * (lane & 31);
-    if (row < rows_valid)
-      *(f32x4_t *)(po + row * kD + col) = *(const f32x4_t *)(st + row * kStageRow + col);
+      for (int i = 0; i < 4; ++i) {  // tile c, reg i -> dim 32g + 8i + c
+        const f32x4_t v0 = {oacc[8 * vh + 0][i], oacc[8 * vh + 1][i], oacc[8 * vh + 2][i],
+                            oacc[8 * vh + 3][i]};
+        const f32x4_t v1 = {oacc[8 * vh + 4][i], oacc[8 * vh + 5][i], oacc[8 * vh + 6][i],
+                            oacc[8 * vh + 7][i]};
+        *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i) = v0;
+        *(f32x4_t *)(st + n * kStageRow + 32 * g + 8 * i + 4) = v1;
+      }
+      float *po = a.ws_o + slot * D + 128 * vh;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int row = 2 * k + (lane >> 5), col = 4 * (lane & 31);
+        if (row < rows_valid)
+          *(f32x4_t *)(po + row * D + col) = *(const f32x4_t *)(st + row * kStageRow + col);
+      }
+    }
+    if (row_ok && g == 0) a.ws_ml[slot + n] = make_float2(m_run, l_run);
   }
-  if (row_ok && g == 0) a.ws_ml[item * a.rows_item + n] = make_float2(m_run, l_run);
 }
 
 struct CombineArgs {
-  const float *ws_o;
-  const float2 *ws_ml;
-  const int32_t *cache_seqlens;
-  const int32_t *num_active;
+  DecodeArgs d;  // the decode launch's geometry (row ranges, nw, partial layout)
   const float *sinks;
   uint16_t *out;
   float *lse;
-  int B, Sq, H, Hk, G, Rq, n_qtiles, nsplit, split_keys, has_new, seqlen_add, window_left;
-  int rows_item;
   float v_descale;
   const float *vd;  // device v_descale scalar, or null (v_descale above)
 };
 
-// One block per (b, kv head, q tile, group of 4 rows): thread t merges row
-// 4*blockIdx.x + t/64 over splits s = (t/16)%4, +4, ... for dims
-// 8*(t%16)..+7; the 4 split groups then merge through LDS.
-__global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
-  __shared__ float s_acc[4][4][16][8];
+// One block per (b, work item, group of 4 rows): thread t merges row
+// 4*blockIdx.x + t/64 over the row's segments s = (t/16)%4, +4, ... for dims
+// 8*(t%16) .. +7 (and +128 for d256); the 4 segment groups then merge through
+// LDS.
+template <int D>
+__global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
+  constexpr int VH = D / 128;
+  const DecodeArgs &a = c.d;
+  __shared__ float s_acc[4][4][16][8 * VH];
   __shared__ float2 s_ml[4][4];
+  const int lane = threadIdx.x & 63;
   const int part = threadIdx.x & 15;
   const int grp = (threadIdx.x >> 4) & 3;
   const int rl = threadIdx.x >> 6;
-  const int h = blockIdx.y / a.n_qtiles;
-  const int qt = blockIdx.y % a.n_qtiles;
+  const int item = blockIdx.y;
+  const int h = item / a.n_qtiles;
+  const int qt = item % a.n_qtiles;
   const int b = blockIdx.z;
   const int row = 4 * blockIdx.x + rl;  // row inside the q tile
   const int r = qt * 16 + row;
   const bool valid = row < 16 && r < a.Rq;
-  const bool active = !(a.num_active && b >= *a.num_active);
-  int nsp = 0;
+  const int nact = active_rows(a);
+  const bool active = b < nact;
+  // This row's segments: key ranges x_first .. x_last of the decode launch
+  // (a row longer than the tiles counted there has none past them).
+  int nsp = 0, x_first = 0;
   if (active) {
-    const int total = a.cache_seqlens[b] + (a.has_new ? 1 : a.seqlen_add);
-    int lo = 0;
-    if (a.window_left >= 0) lo = max(0, total - a.Sq - a.window_left);
-    const int base = lo & ~31;
-    nsp = total > base ? (total - base + a.split_keys - 1) / a.split_keys : 0;
-    // a row longer than the capacity the host sized the grid for has no
-    // partials past nsplit (the decode kernel drops those keys)
-    nsp = min(nsp, a.nsplit);
+    int base;
+    const int T = row_tiles(a, b, nact, base);
+    if (T > 0) {
+      const int total_t = total_tiles(a, nact, lane);
+      const int per = (total_t + a.nw - 1) / a.nw;
+      int off;
+      int acc = 0;
+      // tiles of rows before b
+      for (int c0 = 0; c0 < b; c0 += 64) {
+        int bs;
+        const int t = c0 + lane < b ? row_tiles(a, c0 + lane, nact, bs) : 0;
+        acc += wave_sum(t);
+      }
+      off = acc;
+      x_first = off / per;
+      nsp = (off + T - 1) / per - x_first + 1;
+    }
   }
-  const size_t item0 = (((size_t)b * a.Hk + h) * a.n_qtiles + qt) * a.nsplit;
+  const int n_items = a.Hk * a.n_qtiles;
   float M = -INFINITY, Lsum = 0.f;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  // The loads of up to kBatch splits are issued before any of them is used
-  // (one memory latency per batch instead of one per split).
+  float acc[8 * VH];
+#pragma unroll
+  for (int e = 0; e < 8 * VH; ++e) acc[e] = 0.f;
+  // The loads of up to kBatch segments are issued before any of them is used
+  // (one memory latency per batch instead of one per segment).
   constexpr int kBatch = 8;
   if (valid) {
     for (int s0 = grp; s0 < nsp; s0 += 4 * kBatch) {
       float2 ml[kBatch];
-      f32x4_t v0[kBatch], v1[kBatch];
+      f32x4_t v[kBatch][2 * VH];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int s = min(s0 + 4 * i, nsp - 1);
-        ml[i] = a.ws_ml[(item0 + s) * a.rows_item + row];
-        const float *po = a.ws_o + ((item0 + s) * a.rows_item + row) * kD + part * 8;
-        v0[i] = *(const f32x4_t *)po;
-        v1[i] = *(const f32x4_t *)(po + 4);
+        const size_t slot = ((size_t)(x_first + s + b) * n_items + item) * a.rows_item + row;
+        ml[i] = a.ws_ml[slot];
+        const float *po = a.ws_o + slot * D + part * 8;
+#pragma unroll
+        for (int vh = 0; vh < VH; ++vh) {
+          v[i][2 * vh] = *(const f32x4_t *)(po + 128 * vh);
+          v[i][2 * vh + 1] = *(const f32x4_t *)(po + 128 * vh + 4);
+        }
       }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
@@ -505,17 +628,16 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
         const float Mn = fmaxf(M, ml[i].x);
         const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml[i].x - Mn);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = acc[e] * c_old + v0[i][e] * c_new;
-          acc[4 + e] = acc[4 + e] * c_old + v1[i][e] * c_new;
-        }
+        for (int q4 = 0; q4 < 2 * VH; ++q4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[4 * q4 + e] = acc[4 * q4 + e] * c_old + v[i][q4][e] * c_new;
         Lsum = Lsum * c_old + ml[i].y * c_new;
         M = Mn;
       }
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s_acc[rl][grp][part][e] = acc[e];
+  for (int e = 0; e < 8 * VH; ++e) s_acc[rl][grp][part][e] = acc[e];
   if (part == 0) s_ml[rl][grp] = make_float2(M, Lsum);
   __syncthreads();
   if (!valid || grp != 0) return;
@@ -523,103 +645,112 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs a) {
 #pragma unroll
   for (int g2 = 0; g2 < 4; ++g2) Mt = fmaxf(Mt, s_ml[rl][g2].x);
   const int tok = r / a.G, hq = h * a.G + r % a.G;
-  float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float o[8 * VH];
+#pragma unroll
+  for (int e = 0; e < 8 * VH; ++e) o[e] = 0.f;
   float Lt = 0.f;
   if (Mt != -INFINITY) {
 #pragma unroll
     for (int g2 = 0; g2 < 4; ++g2) {
       const float2 ml = s_ml[rl][g2];
       if (ml.x == -INFINITY) continue;
-      const float c = fast_exp2(ml.x - Mt);
-      Lt += ml.y * c;
+      const float cf = fast_exp2(ml.x - Mt);
+      Lt += ml.y * cf;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += s_acc[rl][g2][part][e] * c;
+      for (int e = 0; e < 8 * VH; ++e) o[e] += s_acc[rl][g2][part][e] * cf;
     }
   }
-  if (a.sinks) {
-    const float sk = a.sinks[hq] * kLog2e;
+  if (c.sinks) {
+    const float sk = c.sinks[hq] * kLog2e;
     if (sk != -INFINITY) {
       const float Mn = fmaxf(Mt, sk);
       const float c_old = fast_exp2(Mt - Mn);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] *= c_old;
+      for (int e = 0; e < 8 * VH; ++e) o[e] *= c_old;
       Lt = Lt * c_old + fast_exp2(sk - Mn);
       Mt = Mn;
     }
   }
   const bool any = active && Lt > 0.f;
-  const float vdesc = a.vd ? *a.vd : a.v_descale;
+  const float vdesc = c.vd ? *c.vd : c.v_descale;
   const float scale = any ? vdesc / Lt : 0.f;
-  uint16_t *op = a.out + (((size_t)b * a.Sq + tok) * a.H + hq) * kD + part * 8;
-  u32x4_t w;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) w[e] = pack_bf16(o[2 * e] * scale, o[2 * e + 1] * scale);
-  *(u32x4_t *)op = w;
-  if (a.lse && part == 0)
-    a.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
+  for (int vh = 0; vh < VH; ++vh) {
+    uint16_t *op = c.out + (((size_t)b * a.Sq + tok) * a.H + hq) * D + 128 * vh + part * 8;
+    u32x4_t w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = pack_bf16(o[8 * vh + 2 * e] * scale, o[8 * vh + 2 * e + 1] * scale);
+    *(u32x4_t *)op = w;
+  }
+  if (c.lse && part == 0)
+    c.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
 }
 
-// Keys per split-K work item: about 32K items at full capacity, at least 256
-// keys, and at most what the table prefetch covers (64 * kTblPerLane pages
-// from a 32-key-aligned start: (64 * kTblPerLane - 1) * P + gcd(32, P) keys).
-static int max_split_keys(int P) {
+// Keys whose block-table entries one prefetch covers: 64 * kTblPerLane pages
+// from a 32-key-aligned start: (64 * kTblPerLane - 1) * P + gcd(32, P) keys,
+// rounded down to whole 32-key tiles.
+static int chunk_keys_for(int P) {
   int gcd = 32;
   while (P % gcd) gcd >>= 1;
   return ((64 * kTblPerLane - 1) * P + gcd) / 32 * 32;
 }
 
-static int pick_split(const fw_decode_params *p, int n_qtiles) {
-  const int cap_split = max_split_keys(p->page_size);
-  if (p->split_keys > 0) return std::min((p->split_keys + 31) / 32 * 32, cap_split);
-  const long capacity = (long)p->max_pages * p->page_size;
-  const long items_per_key = (long)p->batch * p->nheads_k * n_qtiles;
-  // Every work item writes a (rows x 128) f32 partial; with many query rows
-  // per item (a verify window) fewer, longer splits pay for themselves.
-  // Measured: C3 (4 rows) best at 896 keys; C5 (16 rows) 4.69 TB/s at 896,
-  // 5.11 at 1792, 5.34 at 3584.
-  const int rows = (int)std::min<long>(16, (long)p->seqlen_q * (p->nheads / p->nheads_k));
-  const long target_items = rows <= 8 ? 32768 : 16384;
-  const long cap_rows = rows <= 8 ? 896 : 3584;
-  long split = (capacity * items_per_key + target_items - 1) / target_items;
-  split = (split + 31) / 32 * 32;
-  if (split < 256) split = 256;
-  if (split > cap_rows) split = cap_rows;
-  if (split > cap_split) split = cap_split / 32 * 32;
-  // Power-of-two multiples of 32 keys measured ~20% slower on MI355X (C3
-  // decode: 512 or 1024 keys ~4.3 TB/s, 576..960 keys 5.3-5.5 TB/s; C5 2048
-  // keys 4.16 TB/s, 1792 keys 5.05 TB/s): step up by half when the caps
-  // allow, else down by an eighth.
-  const long units = split / 32;
-  if (units >= 8 && (units & (units - 1)) == 0)
-    split = split * 3 / 2 <= std::min<long>(cap_rows, cap_split) ? split * 3 / 2 : split * 7 / 8;
-  return (int)split;
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
 }
 
 struct DecodeLayout {
-  int G, Rq, n_qtiles, split, nsplit, rows_item;
+  int G, Rq, n_qtiles, rows_item, waves, groups, nw, occ;
   size_t o_bytes, ml_bytes;
 };
 
 static int decode_layout(const fw_decode_params *p, DecodeLayout *L) {
   FW_REQUIRE(p->nheads_k > 0 && p->nheads > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads=%d must be a multiple of nheads_k=%d", p->nheads, p->nheads_k);
-  FW_REQUIRE(p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 decode kernel takes head_dim 128; got %d", p->head_dim);
+  FW_REQUIRE(p->head_dim == 128 || p->head_dim == 256, FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 decode kernel takes head_dim 128 or 256; got %d", p->head_dim);
   FW_REQUIRE(p->page_size > 0 && p->page_size % 16 == 0, FW_ERR_VALUE,
              "page_size must be a positive multiple of 16; got %d", p->page_size);
   FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->max_pages > 0, FW_ERR_VALUE,
              "batch, seqlen_q and max_pages must be positive");
+  FW_REQUIRE(p->num_splits >= 0, FW_ERR_VALUE, "num_splits must be >= 0; got %d", p->num_splits);
   L->G = p->nheads / p->nheads_k;
   L->Rq = p->seqlen_q * L->G;
   L->n_qtiles = (L->Rq + 15) / 16;
-  L->split = pick_split(p, L->n_qtiles);
-  const long capacity = (long)p->max_pages * p->page_size;
-  L->nsplit = (int)((capacity + 32 + L->split - 1) / L->split);
   L->rows_item = std::min(L->Rq, 16);
-  const size_t items = (size_t)p->batch * p->nheads_k * L->n_qtiles * L->nsplit;
-  L->o_bytes = align_up(items * L->rows_item * kD * sizeof(float), 256);
-  L->ml_bytes = align_up(items * L->rows_item * sizeof(float2), 256);
+  const int items = p->nheads_k * L->n_qtiles;
+  L->waves = std::min(items, p->head_dim > 128 ? kWgWaves<256> : kWgWaves<128>);
+  L->groups = (items + L->waves - 1) / L->waves;
+  L->occ = p->head_dim > 128 ? 1 : 2;
+  if (p->num_splits > 0) {
+    L->nw = p->num_splits;
+  } else {
+    // one key range per workgroup the GPU holds at once: 4 SIMDs x occ waves
+    // per CU, `waves` waves per workgroup
+    const int per_cu = std::max(1, 4 * L->occ / L->waves);
+    L->nw = std::max(1, device_cus() * per_cu / L->groups);
+  }
+  // every segment is (key range x, row b) and its partial sits at x + b
+  const size_t segs = (size_t)L->nw + p->batch;
+  L->o_bytes = align_up(segs * items * L->rows_item * p->head_dim * sizeof(float), 256);
+  L->ml_bytes = align_up(segs * items * L->rows_item * sizeof(float2), 256);
   return FW_OK;
+}
+
+template <int KV, int D>
+static void launch_decode(const DecodeArgs &a, const DecodeLayout &L, hipStream_t s) {
+  fw_decode_kernel<KV, D><<<dim3(L.nw, L.groups, 1), 64 * L.waves, 0, s>>>(a);
 }
 
 }  // namespace fw
@@ -632,8 +763,8 @@ extern "C" size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p) {
   return L.o_bytes + L.ml_bytes;
 }
 
-// The launch of both entry points: ws / ws_bytes is the split-K partial
-// buffer (the caller's workspace, or the library's static scratch).
+// The launch of both entry points: ws / ws_bytes is the partial buffer (the
+// caller's workspace, or the library's static scratch).
 static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
                          fw_stream_t stream) {
   DecodeLayout L;
@@ -683,57 +814,47 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
     a.vhead = 1;
     a.vdelta = 0;
   }
-  a.split_keys = L.split;
-  a.nsplit = L.nsplit;
+  a.nw = L.nw;
+  a.chunk_keys = chunk_keys_for(p->page_size);
   a.has_new = p->k_new != nullptr;
   a.seqlen_add = a.has_new ? 1 : p->seqlen_add;
   a.causal = p->causal;
   a.window_left = p->window_left;
   a.num_pages = p->num_pages;
+  a.rows_item = L.rows_item;
+  a.waves = L.waves;
   const float sm = p->softmax_scale * p->k_descale;
   a.qscale = p->softcap > 0.f ? sm / p->softcap : sm * kLog2e;
   a.softcap_log2 = p->softcap > 0.f ? p->softcap * kLog2e : 0.f;
   a.kd = p->k_descale_ptr;
   a.sm_scale = p->softmax_scale;
   a.softcap = p->softcap;
-  a.rows_item = L.rows_item;
   hipStream_t s = (hipStream_t)stream;
-  const int items = p->nheads_k * L.n_qtiles;
-  const int waves = items < 4 ? items : 4;
-  const int threads = 64 * waves;
-  const dim3 grid(L.nsplit, (items + waves - 1) / waves, p->batch);
+  const bool d256 = p->head_dim == 256;
   switch (p->kv_dtype) {
-    case FW_BF16: fw_decode_kernel<FW_BF16><<<grid, threads, 0, s>>>(a); break;
-    case FW_FP8_E4M3: fw_decode_kernel<FW_FP8_E4M3><<<grid, threads, 0, s>>>(a); break;
-    default: fw_decode_kernel<FW_FP8_E5M2><<<grid, threads, 0, s>>>(a); break;
+    case FW_BF16:
+      d256 ? launch_decode<FW_BF16, 256>(a, L, s) : launch_decode<FW_BF16, 128>(a, L, s);
+      break;
+    case FW_FP8_E4M3:
+      d256 ? launch_decode<FW_FP8_E4M3, 256>(a, L, s) : launch_decode<FW_FP8_E4M3, 128>(a, L, s);
+      break;
+    default:
+      d256 ? launch_decode<FW_FP8_E5M2, 256>(a, L, s) : launch_decode<FW_FP8_E5M2, 128>(a, L, s);
+      break;
   }
   st = check_launch("fw_decode_kernel");
   if (st != FW_OK) return st;
   CombineArgs c;
-  c.ws_o = a.ws_o;
-  c.ws_ml = a.ws_ml;
-  c.cache_seqlens = p->cache_seqlens;
-  c.num_active = p->num_active;
+  c.d = a;
   c.sinks = p->sinks;
   c.out = (uint16_t *)p->out;
   c.lse = p->lse;
-  c.B = p->batch;
-  c.Sq = p->seqlen_q;
-  c.H = p->nheads;
-  c.Hk = p->nheads_k;
-  c.G = L.G;
-  c.Rq = L.Rq;
-  c.n_qtiles = L.n_qtiles;
-  c.nsplit = L.nsplit;
-  c.split_keys = L.split;
-  c.has_new = a.has_new;
-  c.seqlen_add = a.seqlen_add;
-  c.window_left = p->window_left;
   c.v_descale = p->v_descale;
   c.vd = p->v_descale_ptr;
-  c.rows_item = L.rows_item;
-  const int row_groups = (std::min(L.Rq, 16) + 3) / 4;
-  fw_decode_combine<<<dim3(row_groups, p->nheads_k * L.n_qtiles, p->batch), 256, 0, s>>>(c);
+  const int row_groups = (L.rows_item + 3) / 4;
+  const dim3 grid(row_groups, p->nheads_k * L.n_qtiles, p->batch);
+  if (d256) fw_decode_combine<256><<<grid, 256, 0, s>>>(c);
+  else fw_decode_combine<128><<<grid, 256, 0, s>>>(c);
   return check_launch("fw_decode_combine");
 }
 
@@ -742,14 +863,14 @@ extern "C" int fw_paged_decode(const fw_decode_params *p, fw_stream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// fw_paged_decode_noalloc: the same launch with the split-K partials in a
-// file-scope device array instead of a caller workspace, for callers that
-// cannot allocate.  Each device holds its own copy of the array; its address
-// comes from hipGetSymbolAddress on the first call made on that device (the
-// array's name in host code is only a stand-in, not a device address).
-// Nothing in it needs clearing between calls: every partial the merge reads
-// was written by the same call's decode kernel.  Calls that overlap on one
-// device share the array and race.
+// fw_paged_decode_noalloc: the same launch with the partials in a file-scope
+// device array instead of a caller workspace, for callers that cannot
+// allocate.  Each device holds its own copy of the array; its address comes
+// from hipGetSymbolAddress on the first call made on that device (the array's
+// name in host code is only a stand-in, not a device address).  Nothing in it
+// needs clearing between calls: every partial the merge reads was written by
+// the same call's decode kernel.  Calls that overlap on one device share the
+// array and race.
 static __device__ __attribute__((aligned(256))) uint8_t scratch[FW_DECODE_SCRATCH_BYTES];
 
 namespace {
@@ -764,9 +885,9 @@ extern "C" int fw_paged_decode_noalloc(const fw_decode_params *p, fw_stream_t st
   if (st != FW_OK) return st;
   const size_t need = L.o_bytes + L.ml_bytes;
   FW_REQUIRE(need <= FW_DECODE_SCRATCH_BYTES, FW_ERR_VALUE,
-             "fw_paged_decode_noalloc: this call needs %zu bytes of split-K scratch, more than"
-             " the library's static %zu (FW_DECODE_SCRATCH_BYTES); use fw_paged_decode with a"
-             " workspace (or a larger split_keys)", need, (size_t)FW_DECODE_SCRATCH_BYTES);
+             "fw_paged_decode_noalloc: this call needs %zu bytes of partials, more than the"
+             " library's static %zu (FW_DECODE_SCRATCH_BYTES); use fw_paged_decode with a"
+             " workspace", need, (size_t)FW_DECODE_SCRATCH_BYTES);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   FW_REQUIRE(e == hipSuccess, FW_ERR_RUNTIME, "hipGetDevice: %s", hipGetErrorString(e));

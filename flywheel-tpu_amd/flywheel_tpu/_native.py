@@ -39,7 +39,7 @@ class DecodeParams(ctypes.Structure):
         ("softmax_scale", _f32), ("softcap", _f32),
         ("causal", _i32), ("window_left", _i32),
         ("k_descale", _f32), ("v_descale", _f32),
-        ("split_keys", _i32),
+        ("num_splits", _i32),
         ("v_cache", _c_p),
         ("k_descale_ptr", _c_p), ("v_descale_ptr", _c_p),
     ]

@@ -69,7 +69,7 @@ def append_ragged(kv_cache, k, v, cu_seqlens, cache_seqlens, block_table, num_ac
 
 def decode_params(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_active, sinks, *,
                   nheads_k, softmax_scale, softcap, causal, window_left, k_descale, v_descale,
-                  seqlen_add=0, return_lse=False, split_keys=0, v_cache=None):
+                  seqlen_add=0, return_lse=False, num_splits=0, v_cache=None):
     """A filled fw_decode_params (no workspace yet) and the tensors it points
     at: returns (params, out, lse | None, keep), keep holding every tensor the
     launch reads that the caller does not already hold."""
@@ -89,7 +89,7 @@ def decode_params(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_act
     p.softmax_scale, p.softcap = softmax_scale, softcap
     p.causal, p.window_left = int(causal), window_left
     keep = set_descales(p, k_descale, v_descale)
-    p.split_keys = split_keys
+    p.num_splits = num_splits
     return p, out, lse, keep
 
 

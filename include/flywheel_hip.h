@@ -72,6 +72,7 @@ int fw_abi_version(void);
  * num_active  device int32 scalar or NULL: rows >= *num_active are skipped
  *          (no append; out 0, lse -inf).
  * workspace   device scratch of at least fw_paged_decode_workspace_bytes().
+ * head_dim    128 or 256.
  */
 typedef struct fw_decode_params {
   const void *q;
@@ -94,7 +95,9 @@ typedef struct fw_decode_params {
   int32_t causal;      /* a folded window's token t sees keys < total-(Sq-1-t) */
   int32_t window_left; /* -1 = unbounded */
   float k_descale, v_descale;
-  int32_t split_keys;  /* keys per split-K work item; 0 = heuristic */
+  int32_t num_splits;  /* key ranges the batch's keys are cut into (one
+                        * workgroup per range and head group); 0 = as many as
+                        * the GPU runs at once */
   /* NULL: kv_cache is the merged pool above.  Otherwise the contiguous K/V
    * cache pair of single-token decode (softmax_attention/decode.py:383-403,
    * kernels/decode.py:2147-2178): kv_cache = K cache and v_cache = V cache,

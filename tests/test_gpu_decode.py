@@ -174,7 +174,8 @@ def test_anchor_change_known_answer():
 
 
 def test_split_k_invariance_and_determinism():
-    """Forcing 32-key splits must agree with the default split; repeats are
+    """Cutting the keys into many more ranges (so every row spans several
+    segments, some one tile long) must agree with the default; repeats are
     bitwise equal (the reference's race test, test_prefill.py:827-875)."""
     announce("decode split invariance")
     rng = np.random.default_rng(6)
@@ -185,7 +186,7 @@ def test_split_k_invariance_and_determinism():
     table = torch.tensor(case.table, device=DEV)
     kw = dict(nheads_k=2, softmax_scale=1 / math.sqrt(128), softcap=0.0, causal=False,
               window_left=-1, k_descale=1.0, v_descale=1.0, return_lse=True)
-    o1, l1 = paged_decode(q, pool, None, None, lens, table, None, None, split_keys=32, **kw)
+    o1, l1 = paged_decode(q, pool, None, None, lens, table, None, None, num_splits=150, **kw)
     o2, l2 = paged_decode(q, pool, None, None, lens, table, None, None, **kw)
     torch.cuda.synchronize()
     assert_close(o1.float().cpu().numpy(), o2.float().cpu().numpy())
@@ -287,3 +288,25 @@ def test_contiguous_cache_num_active_softcap():
                                      softcap=30.0, num_active=2)
     assert_close(out[:2], ro[:2])
     assert_lse(lse[:2], rl[:2])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
+@pytest.mark.parametrize("seqlen_q", [1, 4])
+def test_decode_head_dim_256(dtype, seqlen_q):
+    """head_dim 256 (the reference's DECODE_HEAD_DIMS, traits.py:50): single
+    token with the fused append, and a causal 4-token verify window."""
+    announce(f"decode d256 {dtype} seqlen_q={seqlen_q}")
+    rng = np.random.default_rng(60)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.8, 1.3)
+    lengths = [0, 17, 1000, 5000, 129]
+    b = len(lengths)
+    case = PagedCase(rng, batch=b, nheads=16, nheads_k=4, lengths=lengths,
+                     new_tokens=[seqlen_q] * b, head_dim=256, dtype=dt, k_descale=ks, v_descale=vs)
+    q = randn(rng, (b, seqlen_q, 16, 256))
+    out, lse, pool = run_decode(case, q, causal=seqlen_q > 1)
+    exp_pool = case.expected_pool()
+    np.testing.assert_array_equal(codes_of(pool), exp_pool)
+    ro, rl = oracle(case, q, exp_pool, causal=seqlen_q > 1)
+    assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)

@@ -71,13 +71,16 @@ def test_noalloc_decode_matches_workspace_decode_twice():
 
 
 def test_noalloc_rejects_a_call_beyond_its_scratch():
+    """Partials scale with (key ranges + rows) x KV heads x query rows: a batch
+    of 4096 rows with a 4-token verify window needs far more than the static
+    scratch, and the call is refused before anything is launched."""
     announce("no-alloc decode, oversized call rejected")
     case, q, kn, vn = _case(52, batch=4, max_len=100)
     pool = case.pool()
     lens = torch.tensor(case.lengths, dtype=torch.int32, device=DEV)
-    table = torch.zeros((4, 1 << 16), dtype=torch.int32, device=DEV)  # 1M-key capacity
-    p, out, lse, keep = decode_params(q, pool, kn, vn, lens, table, None, None, **_kw(case))
-    p.batch = 4
+    table = torch.tensor(case.table, device=DEV)
+    p, out, lse, keep = decode_params(q, pool, None, None, lens, table, None, None, **_kw(case))
+    p.batch, p.seqlen_q = 4096, 4  # only the sizes matter: it is rejected unlaunched
     lib = N.lib()
     assert lib.fw_paged_decode_workspace_bytes(p) > N.FW_DECODE_SCRATCH_BYTES
     assert lib.fw_paged_decode_noalloc(p, N.stream_of(q)) == N.FW_ERR_VALUE
