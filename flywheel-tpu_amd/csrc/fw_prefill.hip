@@ -23,10 +23,10 @@ namespace fw {
 
 constexpr int kQT = 128;     // q rows per workgroup
 constexpr int kKT = 64;      // keys per kv tile
-constexpr int kKS = 136;     // Ks row stride (bf16 elements)
 constexpr int kVS = 68;      // Vt row stride (bf16 elements)
-constexpr int kKsBytes = kKT * kKS * 2;
-constexpr int kVtBytes = 128 * kVS * 2;
+// Staged kernel LDS for head_dim D: Ks [64 keys][D + 8], Vt [D dims][68].
+template <int D> constexpr int kKS = D + 8;  // Ks row stride (bf16 elements)
+template <int D> constexpr int kStagedLds = (kKT * kKS<D> + D * kVS) * 2;
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -123,18 +123,21 @@ __device__ __forceinline__ void rope_q_words(const PrefillArgs &a, size_t tb, in
 // One lane's Q^T operand: dims 16j + 8g .. 16j + 8g + 7 (j = 0..7) of the row
 // at qp, rotated at position pos when RoPE tables are given, then scaled by qs
 // and rounded to bf16.
+template <int D = 128>
 __device__ __forceinline__ void load_q_operand(const PrefillArgs &a, const uint16_t *qp, int g,
-                                               float qs, int pos, bf16x8_t (&qop)[8]) {
-  u32x4_t raw[8];
+                                               float qs, int pos, bf16x8_t (&qop)[D / 16]) {
+  u32x4_t raw[D / 16];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
-  if (a.rcos) {
-    const size_t tb = (size_t)min(max(pos, 0), a.rrows - 1) * 64;
-    if (a.rf32) rope_q_words<true>(a, tb, g, raw);
-    else rope_q_words<false>(a, tb, g, raw);
+  for (int j = 0; j < D / 16; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
+  if constexpr (D == 128) {  // fused RoPE: head_dim 128 (the host checks)
+    if (a.rcos) {
+      const size_t tb = (size_t)min(max(pos, 0), a.rrows - 1) * 64;
+      if (a.rf32) rope_q_words<true>(a, tb, g, raw);
+      else rope_q_words<false>(a, tb, g, raw);
+    }
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < D / 16; ++j) {
     u32x4_t o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = pack_bf16(bf16_lo(raw[j][e]) * qs, bf16_hi(raw[j][e]) * qs);
@@ -154,7 +157,7 @@ __device__ __forceinline__ u32x4_t load_row8(const uint8_t *row, int c) {
   }
 }
 
-template <int MODE, int KV>
+template <int MODE, int KV, int D = 128>
 struct KvAddr {
   const PrefillArgs &a;
   int b, hk, seq, kbase;
@@ -173,7 +176,7 @@ struct KvAddr {
       int page = a.table[(size_t)seq * a.max_pages + key / a.P];
       page = page < 0 || page >= a.num_pages ? 0 : page;
       constexpr int EB = KV == FW_BF16 ? 2 : 1;
-      return a.k + (((size_t)page * a.P + key % a.P) * a.CH + 2 * hk) * 128 * EB;
+      return a.k + (((size_t)page * a.P + key % a.P) * a.CH + 2 * hk) * D * EB;
     } else {
       return a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)(kbase + key) * a.kst);
     }
@@ -181,24 +184,28 @@ struct KvAddr {
   __device__ __forceinline__ const uint8_t *v_row(int key) const {
     if constexpr (MODE == FW_KV_PAGED) {
       constexpr int EB = KV == FW_BF16 ? 2 : 1;
-      return k_row(key) + 128 * EB;
+      return k_row(key) + D * EB;
     } else {
       return a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)(kbase + key) * a.vst);
     }
   }
 };
 
-// fp8 (and generic) K/V: 4 waves = 128 rows; K/V rows are widened to bf16 in
-// registers and staged as
-//   Ks  [64 keys][136 bf16]  row-major (row pad keeps ds_read_b128 conflict-free)
-//   Vt  [128 dims][68 bf16]  transposed, keys in pairs (so the PV operand of a
-//                            lane is two ds_read_b64 with no repacking)
+// fp8 K/V and head_dim 256: 4 waves = 128 rows; K/V rows are widened to
+// bf16 in registers and staged as
+//   Ks  [64 keys][D + 8 bf16]  row-major (row pad keeps ds_read_b128 conflict-free)
+//   Vt  [D dims][68 bf16]      transposed, keys in pairs (so the PV operand of
+//                              a lane is two ds_read_b64 with no repacking)
 // with the next tile's global loads issued before the current tile's math.
-template <int MODE, int KV>
-__global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kKsBytes + kVtBytes];
+// head_dim D = 128 runs two waves per SIMD; D = 256 one (O and Q^T alone
+// take 192 registers per lane).
+template <int MODE, int KV, int D>
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel(PrefillArgs a) {
+  constexpr int KS = kKS<D>;
+  constexpr int CPR = D / 128;  // 8-element chunks of a row per staging thread
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStagedLds<D>];
   uint16_t *Ks = (uint16_t *)smem;
-  uint16_t *Vt = (uint16_t *)(smem + kKsBytes);
+  uint16_t *Vt = (uint16_t *)(smem + kKT * KS * 2);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -236,7 +243,8 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
       for (int rr = 0; rr < 1; ++rr) {
         if (r0 < a.Sq) {
           uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
-          for (int d = g * 64; d < g * 64 + 64; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
+          for (int d = g * (D / 2); d < (g + 1) * (D / 2); d += 8)
+            *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
           if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
         }
       }
@@ -277,29 +285,30 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
 
   // ------------------------------------------------------------ Q^T operand
-  bf16x8_t qop[8];
+  bf16x8_t qop[D / 16];
   {
     const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
                          (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
     const float qs = row_ok ? q_scale_of(a) : 0.f;  // rows past the end get q = 0
-    load_q_operand(a, qp, g, qs, qrow + off, qop);
+    load_q_operand<D>(a, qp, g, qs, qrow + off, qop);
   }
 
-  f32x16_t oacc[4];
+  f32x16_t oacc[D / 32];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < D / 32; ++c)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  const KvAddr<MODE, KV> addr{a, b, hk, seq, kbase};
+  const KvAddr<MODE, KV, D> addr{a, b, hk, seq, kbase};
   const int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
   const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
 
-  // staging assignment: K rows (tid/16) + 16p, V key pairs (tid/16) + 16p
+  // staging assignment: K rows (tid/16) + 16p, V key pairs (tid/16) + 16p;
+  // of each row, thread column sc takes the 8-element chunks sc + 16c
   const int sc = tid & 15;
   const int sr = tid >> 4;
-  u32x4_t kst[4], vst[4];
+  u32x4_t kst[4][CPR], vst[4][CPR];
   uint32_t kbad = 0;  // byte p: K row group p came from an invalid page id
   // The keys of an invalid page id read as zero K and V rows (the page 0 the
   // loads used may hold anything).  Every 16-key group of a tile lies on one
@@ -312,7 +321,8 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int key = min(kb + sr + 16 * p, kmax);
-      kst[p] = load_row8<KV>(addr.k_row(key), sc);
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) kst[p][c] = load_row8<KV>(addr.k_row(key), sc + 16 * c);
       // wave-uniform: the page of the group's first key <= kmax
       if (addr.bad(min(kb + 16 * p, kmax))) kbad |= 1u << (8 * p);
     }
@@ -320,31 +330,43 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     for (int p = 0; p < 2; ++p) {
       const int k0 = min(kb + 2 * (sr + 16 * p), kmax);
       const int k1 = min(kb + 2 * (sr + 16 * p) + 1, kmax);
-      vst[2 * p] = load_row8<KV>(addr.v_row(k0), sc);
-      vst[2 * p + 1] = load_row8<KV>(addr.v_row(k1), sc);
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) {
+        vst[2 * p][c] = load_row8<KV>(addr.v_row(k0), sc + 16 * c);
+        vst[2 * p + 1][c] = load_row8<KV>(addr.v_row(k1), sc + 16 * c);
+      }
     }
   };
   auto lds_store = [&]() {
     if (kbad) {  // rare: zero the rows of invalid page ids
 #pragma unroll
       for (int p = 0; p < 4; ++p)
-        if ((kbad >> (8 * p)) & 1u) kst[p] = u32x4_t{0, 0, 0, 0};
+        if ((kbad >> (8 * p)) & 1u)
+#pragma unroll
+          for (int c = 0; c < CPR; ++c) kst[p][c] = u32x4_t{0, 0, 0, 0};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
         if ((kbad >> (8 * ((2 * sr + 32 * p) >> 4))) & 1u)
-          vst[2 * p] = vst[2 * p + 1] = u32x4_t{0, 0, 0, 0};
+#pragma unroll
+          for (int c = 0; c < CPR; ++c) vst[2 * p][c] = vst[2 * p + 1][c] = u32x4_t{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int p = 0; p < 4; ++p) *(u32x4_t *)(Ks + (sr + 16 * p) * kKS + 8 * sc) = kst[p];
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int c = 0; c < CPR; ++c)
+        *(u32x4_t *)(Ks + (sr + 16 * p) * KS + 8 * (sc + 16 * c)) = kst[p][c];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int kp = sr + 16 * p;  // key pair
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t x0 = vst[2 * p][e], x1 = vst[2 * p + 1][e];
-        *(uint32_t *)(Vt + (8 * sc + 2 * e) * kVS + 2 * kp) = perm_lo(x0, x1);
-        *(uint32_t *)(Vt + (8 * sc + 2 * e + 1) * kVS + 2 * kp) = perm_hi(x0, x1);
-      }
+      for (int c = 0; c < CPR; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t x0 = vst[2 * p][c][e], x1 = vst[2 * p + 1][c][e];
+          const int d0 = 8 * (sc + 16 * c) + 2 * e;
+          *(uint32_t *)(Vt + d0 * kVS + 2 * kp) = perm_lo(x0, x1);
+          *(uint32_t *)(Vt + (d0 + 1) * kVS + 2 * kp) = perm_hi(x0, x1);
+        }
     }
   };
 
@@ -357,25 +379,32 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     const int kb = t * kKT;
     if (!w_any || kb >= w_hi || kb + kKT <= w_lo) continue;  // wave sees nothing here
 
-    // ---------------- S^T = K Q^T : two 32-key sub-tiles.  All 16 K operands
-    // are read up front so the MFMA chain never waits on a single LDS read.
+    // ---------------- S^T = K Q^T : two 32-key sub-tiles.  At head_dim 128
+    // all 16 K operands are read up front so the MFMA chain never waits on a
+    // single LDS read; at 256 a ring of 8 operands runs 8 reads ahead.
     f32x16_t sacc[2];
     {
-      bf16x8_t kop[2][8];
+      constexpr int NJ = D / 16;                  // MFMA steps per sub-tile
+      constexpr int RING = D > 128 ? 8 : 2 * NJ;  // operands in flight
+      bf16x8_t kop[RING];
+      auto kread = [&](int i) {  // operand i = st * NJ + j
+        const int st = i / NJ, j = i % NJ;
+        kop[i % RING] = __builtin_bit_cast(
+            bf16x8_t, *(const u32x4_t *)(Ks + (32 * st + n) * KS + 8 * g + 16 * j));
+      };
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const uint16_t *kr = Ks + (32 * st + n) * kKS + 8 * g;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          kop[st][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(kr + 16 * j));
-      }
+      for (int i = 0; i < RING; ++i) kread(i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sacc[st] = mfma32(kop[st][j], qop[j], sacc[st]);
+        for (int j = 0; j < NJ; ++j) {
+          const int i = st * NJ + j;
+          sacc[st] = mfma32(kop[i % RING], qop[j], sacc[st]);
+          if (i + RING < 2 * NJ) kread(i + RING);
+        }
       }
     }
     // ---------------- online softmax (log2 units), lane = query row n
@@ -418,14 +447,14 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
     l_run = l_run * alpha + psum;
     if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+      for (int c = 0; c < D / 32; ++c) oacc[c] *= alpha;
     }
-    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x 4 dim tiles;
-    // the V operands of step u+1 are read while step u's MFMAs run.
-    bf16x8_t vop[2][4];
-    auto read_v = [&](int u, bf16x8_t (&dst)[4]) {
+    // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x D/32 dim
+    // tiles; the V operands of step u+1 are read while step u's MFMAs run.
+    bf16x8_t vop[2][D / 32];
+    auto read_v = [&](int u, bf16x8_t (&dst)[D / 32]) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < D / 32; ++c) {
         const uint16_t *vr = Vt + (n + 32 * c) * kVS + 16 * u + 4 * g;
         const u32x2_t lo = *(const u32x2_t *)vr;
         const u32x2_t hi = *(const u32x2_t *)(vr + 8);
@@ -438,7 +467,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
       if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
+      for (int c = 0; c < D / 32; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
     }
   }
 
@@ -460,7 +489,7 @@ __global__ __launch_bounds__(256, 2) void fw_prefill_staged_kernel(PrefillArgs a
   const float scale = any ? oscale * v_descale_of(a) / Lsum : 0.f;
   uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < D / 32; ++c)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
@@ -1084,33 +1113,52 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
   return align_up((size_t)(1 + 2 * max_sched_tiles(p, kQT)) * sizeof(int32_t), 256);
 }
 
-// Kernel choice: bf16 K/V -> ping-pong kernel (256-row tiles; the softcap
-// variant is 3% faster on C4's shape than a 4-wave, two-per-CU kernel that
-// ran the tanh beside its own MFMAs); fp8 pools -> register-staged kernel.
+// Kernel choice: bf16 K/V at head_dim 128 -> ping-pong kernel (256-row
+// tiles; the softcap variant is 3% faster on C4's shape than a 4-wave,
+// two-per-CU kernel that ran the tanh beside its own MFMAs); fp8 pools and
+// head_dim 256 -> register-staged kernel.
 static bool use_pingpong(const fw_prefill_params *p) {
-  return p->kv_dtype == FW_BF16;
+  return p->kv_dtype == FW_BF16 && p->head_dim == 128;
 }
 
 template <int MODE>
-static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype,
+static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int head_dim,
                         hipStream_t s) {
+  if (head_dim == 256) {
+    switch (kv_dtype) {
+      case FW_BF16: fw_prefill_staged_kernel<MODE, FW_BF16, 256><<<grid, 256, 0, s>>>(a); break;
+      case FW_FP8_E4M3:
+        if constexpr (MODE == FW_KV_PAGED)
+          fw_prefill_staged_kernel<MODE, FW_FP8_E4M3, 256><<<grid, 256, 0, s>>>(a);
+        break;
+      default:
+        if constexpr (MODE == FW_KV_PAGED)
+          fw_prefill_staged_kernel<MODE, FW_FP8_E5M2, 256><<<grid, 256, 0, s>>>(a);
+        break;
+    }
+    return;
+  }
   switch (kv_dtype) {
     case FW_BF16:
       if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
       else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
       break;
     case FW_FP8_E4M3:
-      if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E4M3><<<grid, 256, 0, s>>>(a);
+      if constexpr (MODE == FW_KV_PAGED)
+        fw_prefill_staged_kernel<MODE, FW_FP8_E4M3, 128><<<grid, 256, 0, s>>>(a);
       break;
     default:
-      if constexpr (MODE == FW_KV_PAGED) fw_prefill_staged_kernel<MODE, FW_FP8_E5M2><<<grid, 256, 0, s>>>(a);
+      if constexpr (MODE == FW_KV_PAGED)
+        fw_prefill_staged_kernel<MODE, FW_FP8_E5M2, 128><<<grid, 256, 0, s>>>(a);
       break;
   }
 }
 
 extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
-  FW_REQUIRE(p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 prefill kernel takes head_dim 128; got %d", p->head_dim);
+  FW_REQUIRE(p->head_dim == 128 || p->head_dim == 256, FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 prefill kernels take head_dim 128 or 256; got %d", p->head_dim);
+  FW_REQUIRE(!p->rotary_cos || p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
+             "the fused RoPE takes head_dim 128; got %d", p->head_dim);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads=%d must be a multiple of nheads_k=%d", p->nheads, p->nheads_k);
   FW_REQUIRE(p->kv_mode >= FW_KV_DENSE && p->kv_mode <= FW_KV_PAGED, FW_ERR_VALUE,
@@ -1173,7 +1221,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, s);
+    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, p->head_dim, s);
     return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -1201,7 +1249,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (st != FW_OK) return st;
   // one workgroup per (schedule slot, query head); see sched_slot
   dim3 grid(max_tiles * p->nheads);
-  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, s);
-  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, s);
+  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, p->head_dim, s);
+  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, s);
   return check_launch("fw_prefill");
 }

@@ -214,7 +214,8 @@ def flash_attn_func(
             reason = f"{what} is forward-only; backward is unsupported."
         else:
             unsupported = ("window_size" if window_size != (-1, -1) else
-                           "softcap" if softcap != 0.0 else None)
+                           "softcap" if softcap != 0.0 else
+                           f"head_dim {d}" if d != 128 else None)
             if unsupported:
                 reason = (f"The backward kernel does not support {unsupported}; that"
                           " configuration is forward-only.")

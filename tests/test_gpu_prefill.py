@@ -227,3 +227,95 @@ def test_prefill_bitwise_repeat():
     ref = flash_attn_func(q, k, v, causal=True)
     for _ in range(20):
         assert torch.equal(flash_attn_func(q, k, v, causal=True), ref)
+
+
+# ---------------------------------------------------------------- head_dim 256
+# The reference benchmarks and accepts head_dim 256 (multiples of 128,
+# inputs.py:100-140, fwd_paged.py:1186); its published shapes are d256
+# (docs/v7x.md:49-60, 157-169).
+
+
+@pytest.mark.parametrize(
+    "b,h,hk,sq,sk,causal,window,softcap",
+    [
+        (1, 8, 2, 512, 512, True, (-1, -1), 0.0),
+        (2, 4, 4, 200, 333, True, (-1, -1), 0.0),
+        (1, 4, 1, 333, 200, True, (-1, -1), 0.0),
+        (1, 4, 2, 257, 257, False, (64, 17), 0.0),
+        (1, 8, 1, 384, 384, True, (100, -1), 30.0),
+    ],
+)
+def test_flash_attn_func_d256(b, h, hk, sq, sk, causal, window, softcap):
+    announce(f"dense d256 b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window}")
+    rng = np.random.default_rng(70)
+    q, k, v = randn(rng, (b, sq, h, 256)), randn(rng, (b, sk, hk, 256)), randn(rng, (b, sk, hk, 256))
+    out, lse = flash_attn_func(
+        to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)), to_dev_bf16(head_major(v)),
+        causal=causal, window_size=window, softcap=softcap, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    ro, rl = A.attention_ref(q, k, v, causal=causal, window_size=window, softcap=softcap,
+                             round_scaled_q=True)
+    assert_close(out.float().cpu().numpy(), head_major(ro))
+    assert_lse(lse.cpu().numpy(), rl)
+
+
+def test_flash_attn_varlen_d256():
+    announce("varlen packed d256")
+    rng = np.random.default_rng(71)
+    qlens, klens = [1, 130, 77, 256], [1, 200, 77, 300]
+    h, hk, d = 4, 2, 256
+    cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    q = randn(rng, (h, cu_q[-1] + 5, d))
+    k = randn(rng, (hk, cu_k[-1], d))
+    v = randn(rng, (hk, cu_k[-1], d))
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), torch.tensor(cu_q, device=DEV),
+        torch.tensor(cu_k, device=DEV), max(qlens), max(klens), causal=True,
+        return_softmax_lse=True)
+    torch.cuda.synchronize()
+    outs, lses = out.float().cpu().numpy(), lse.cpu().numpy()
+    for s in range(4):
+        qs = q[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2)[None]
+        ks = k[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        vs = v[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        ro, rl = A.attention_ref(qs, ks, vs, causal=True, round_scaled_q=True)
+        assert_close(outs[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2), ro[0], what=f"seq {s}")
+        assert_lse(lses[:, cu_q[s]:cu_q[s + 1]], rl[0])
+    assert not outs[:, cu_q[-1]:].any()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
+def test_chunked_prefill_kvcache_d256(dtype):
+    """The chunked-prefill call (append + paged varlen, window, softcap,
+    num_active) at head_dim 256."""
+    announce(f"chunked prefill d256 {dtype}")
+    rng = np.random.default_rng(72)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (1.5, 0.7)
+    chunks = [256, 300, 1, 129]
+    prior = [0, 1000, 17, 500]
+    case = PagedCase(rng, batch=4, nheads=8, nheads_k=2, lengths=prior, new_tokens=chunks,
+                     head_dim=256, dtype=dt, k_descale=ks, v_descale=vs)
+    cu = case.cu
+    q = randn(rng, (cu[-1], 8, 256))
+    pool = case.pool()
+    out, lse, pool2 = flash_attn_with_kvcache(
+        to_dev_bf16(q), pool, None, dev_from_codes(case.k_codes, dt),
+        dev_from_codes(case.v_codes, dt),
+        cache_seqlens=torch.tensor(prior, dtype=torch.int32, device=DEV),
+        block_table=torch.tensor(case.table, device=DEV),
+        cu_seqlens_q=torch.tensor(cu, device=DEV), max_seqlen_q=max(chunks), causal=True,
+        window_size=(400, 0), softcap=30.0, return_softmax_lse=True, num_active=3,
+        k_descale=ks, v_descale=vs)
+    torch.cuda.synchronize()
+    assert pool2 is pool
+    exp_pool = case.expected_pool(num_active=3)
+    np.testing.assert_array_equal(codes_of(pool), exp_pool)
+    kp, vp = case.kv_pages(exp_pool)
+    totals = case.lengths + case.new_tokens
+    ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True, window_left=400,
+                                softcap=30.0, k_descale=ks, v_descale=vs, round_scaled_q=True,
+                                num_active=3)
+    assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
