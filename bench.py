@@ -498,8 +498,65 @@ def workload_rope(args, device):
         cpu=None)
 
 
+def workload_c2d256(args, device):
+    """The reference's published dense prefill shape (docs/v7x.md:60):
+    flash_attn_func causal, 1 x 32q/4kv x 4096 x head_dim 256, bf16."""
+    from flywheel_tpu import flash_attn_func
+    b, h, hk, s, d = 1, 32, 4, 4096, 256
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    flops = 4.0 * s * s * h * d / 2 * b
+    ms = timed(lambda: flash_attn_func(q, k, v, causal=True), args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(
+        name="c2d256", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_func causal GQA prefill, head_dim 256", "batch": b,
+                "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d,
+                "published": "653 TFLOP/s, TPU v7x one core (docs/v7x.md:60)"},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "kernel": "fw_prefill_staged_kernel<DENSE, bf16, 256>",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=None)
+
+
+def workload_dec256(args, device):
+    """The reference's published decode shape (docs/v7x.md:165): paged bf16
+    decode with the fused append, 32q/4kv, head_dim 256, 256 sequences of
+    15360 cached tokens, page 128."""
+    from flywheel_tpu import flash_attn_with_kvcache
+    b, h, hk, d, page, ctx = 256, 32, 4, 256, 128, 15360
+    rng = np.random.default_rng(0)
+    lengths = np.full(b, ctx)
+    gen = torch.Generator(device=device).manual_seed(0)
+    pool, table, _ = paged_pool(gen, rng, lengths, 1, hk, d, page, torch.bfloat16, device)
+    q = torch.randn((b, 1, h, d), generator=gen, device=device, dtype=torch.bfloat16)
+    kn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    vn = torch.randn((b, 1, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    step = lambda: flash_attn_with_kvcache(q, pool, None, kn, vn, cache_seqlens=lens,
+                                           block_table=table)
+    ms = timed(step, args.steps, args.warmup)
+    nbytes = float(np.sum(lengths + 1)) * 2 * hk * d * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(
+        name="dec256", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
+        config={"workload": "flash_attn_with_kvcache paged decode + fused append, head_dim 256",
+                "batch": b, "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
+                "ctx": ctx, "published": "5.023 ms/step, 3.31 TB/s, TPU v7x one core"
+                " (docs/v7x.md:165)"},
+        roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                  "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                  "kernel": "fw_decode_kernel<bf16, 256> + fw_decode_combine (whole step)",
+                  "algorithmic_per_launch": f"{nbytes:.4e} B"},
+        cpu=None)
+
+
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
 EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope,
+         "c2d256": workload_c2d256, "dec256": workload_dec256,
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 
 
@@ -545,7 +602,26 @@ def trace_summary(csv_path, last):
               f"{np.median(tail):>9.2f} {tail.mean():>9.2f} {tail.min():>9.2f} {tail.max():>9.2f}")
 
 
+def pmc_summary(csv_path):
+    """Average value per dispatch of each counter of a rocprofv3 --pmc
+    counter_collection CSV, per (kernel, grid)."""
+    import csv
+    vals = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            key = (short_kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""), r["Counter_Name"])
+            vals.setdefault(key, []).append(float(r["Counter_Value"]))
+    print(f"# {'kernel':<44} {'grid':>10} {'counter':<24} {'avg/dispatch':>16} {'n':>6}")
+    for (name, grid, ctr), v in sorted(vals.items()):
+        print(f"{name[:46]:<46} {grid:>10} {ctr:<24} {sum(v) / len(v):>16.1f} {len(v):>6}")
+
+
 def main():
+    if "--pmc-summary" in sys.argv:
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--pmc-summary", required=True, help="rocprofv3 counter_collection.csv")
+        pmc_summary(ap.parse_args().pmc_summary)
+        return
     if "--trace-summary" in sys.argv:
         ap = argparse.ArgumentParser()
         ap.add_argument("--trace-summary", required=True, help="rocprofv3 kernel_trace.csv")
