@@ -540,9 +540,9 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 // tile j+2 in its softmax slot of tile j.  With softcap (SOFTCAP) the tanh
 // runs in the softmax slot too.
 constexpr int kPPWaves = 8;
-// One zero K row and V row (256 B each): the copy source for the keys of an
-// invalid page id.
-__device__ __attribute__((aligned(256))) uint8_t kZeroKV[512];
+// Zero K and V rows (256 B each at head_dim 128, 512 B at 256): the copy
+// source for the keys of an invalid page id.
+__device__ __attribute__((aligned(256))) uint8_t kZeroKV[1024];
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
 
@@ -1012,6 +1012,399 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 256, bf16 K/V: one wave per SIMD.  Workgroup = 4 waves = 128 q
+// rows of one query head (wave w owns rows 32w .. 32w+31).  At head_dim 256 a
+// score costs twice the MFMA work it does at 128, so one wave per SIMD can
+// hide its own softmax under its matrix work: each tile step runs
+//   [softcap / masks of tile t]  [QK(t+1) MFMAs interleaved with the
+//   exponentials, sums and packing of tile t]  [PV(t) MFMAs]
+// and the PV MFMAs of step t keep the matrix pipe busy while step t+1 starts
+// its VALU work.  K/V tiles of 32 keys (16 KiB each at 512 B a row) rotate
+// through four LDS buffers and arrive by direct global->LDS copies issued
+// three steps ahead; each wave copies 8 key rows of every tile.  One barrier
+// per step.  The LDS rows use the same 16-byte chunk swizzle swz(row) as the
+// head_dim-128 kernels (on the low 4 bits of the 32-chunk row).
+constexpr int kD2Waves = 4;
+constexpr int kD2Rows = 32 * kD2Waves;        // q rows per workgroup
+constexpr int kD2Keys = 32;                   // keys per K/V tile
+constexpr int kD2RowB = 512;                  // LDS bytes of one key row
+constexpr int kD2TileB = kD2Keys * kD2RowB;   // 16 KiB per K or V tile
+constexpr int kD2Bufs = 4;
+
+template <int MODE, bool SOFTCAP>
+__global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kD2Bufs * kD2TileB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31;
+  const int hh = lane >> 5;
+
+  // ------------------------------------------------------------ tile decode
+  int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
+  if constexpr (MODE == FW_KV_DENSE) {
+    const int nbh = a.B * a.H;
+    const int bid = blockIdx.x;
+    int qt, bh;
+    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
+      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
+      qt = a.n_qt - 1 - wi / hx;
+      bh = x * hx + wi % hx;
+    } else {
+      qt = a.n_qt - 1 - bid / nbh;
+      bh = bid % nbh;
+    }
+    b = bh / a.H;
+    h = bh % a.H;
+    q0 = qt * kD2Rows;
+    sq_len = a.Sq;
+    sk_len = a.Sk;
+  } else {
+    int slot;
+    sched_slot(a, slot, h);
+    if (slot >= a.sched[0]) return;
+    seq = a.sched[1 + 2 * slot];
+    q0 = a.sched[2 + 2 * slot];
+    if (seq < 0) {  // packed padding rows: out 0, lse -inf
+      const int r0 = q0 + w * 32 + n;
+      if (r0 < a.Sq) {
+        uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
+        for (int d = hh * 128; d < hh * 128 + 128; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
+        if (a.lse && hh == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
+      }
+      return;
+    }
+    qtok0 = a.cu_q[seq];
+    sq_len = a.cu_q[seq + 1] - qtok0;
+    if constexpr (MODE == FW_KV_VARLEN) {
+      kbase = a.cu_k[seq];
+      sk_len = a.cu_k[seq + 1] - kbase;
+    } else {
+      sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
+    }
+  }
+  const int hk = h / a.G;
+  const int off = sk_len - sq_len;  // bottom-right alignment
+  auto row_hi = [&](int r) {
+    const int p = r + off;
+    return a.wr >= 0 ? min(sk_len, p + a.wr + 1) : sk_len;
+  };
+  auto row_lo = [&](int r) {
+    const int p = r + off;
+    return a.wl >= 0 ? max(0, p - a.wl) : 0;
+  };
+  const int last_row = min(q0 + kD2Rows, sq_len) - 1;
+  const int wg_lo = row_lo(q0);
+  const int wg_hi = row_hi(last_row);
+  const int w_first = q0 + 32 * w;
+  const int w_last = min(w_first + 31, sq_len - 1);
+  const bool w_any = w_first <= w_last;
+  const int w_lo = w_any ? row_lo(w_first) : 0;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < sq_len;
+  const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
+
+  const int t_begin = wg_hi > wg_lo ? wg_lo / kD2Keys : 0;
+  const int t_end = wg_hi > wg_lo ? (wg_hi + kD2Keys - 1) / kD2Keys : 0;
+  const int T = t_end - t_begin;
+
+  // ---- copies: tile j (relative) lands in buffer j % 4; this wave moves key
+  // rows 8w .. 8w+7, two 512-byte rows per instruction: lane l writes
+  // physical chunk l % 32 of row 8w + 2i + l / 32, which holds logical chunk
+  // (l % 32) ^ swz(row).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)lds;
+  const uint32_t ldsV = lds0 + kD2Bufs * kD2TileB;
+  const uint32_t lr = lane >> 5, pc = lane & 31;
+  uint32_t kstB, vstB;
+  const uint8_t *kbase_p = nullptr, *vbase_p = nullptr;
+  if constexpr (MODE == FW_KV_PAGED) {
+    kstB = vstB = (uint32_t)a.CH * kD2RowB;
+  } else {
+    kstB = 2u * (uint32_t)a.kst;
+    vstB = 2u * (uint32_t)a.vst;
+    kbase_p = a.k + 2 * ((size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kbase * a.kst);
+    vbase_p = a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kbase * a.vst);
+  }
+  uint32_t dsrc[4];  // per copy instruction: this lane's chunk offset in the source row
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dsrc[i] = 16u * (pc ^ (uint32_t)swz(8 * w + 2 * i + lr));
+  // A page id outside [0, num_pages) is never dereferenced: its rows are
+  // copied from the zero rows kZeroKV (the keys read as zero K and V rows).
+  auto dma = [&](int j, int buf) __attribute__((always_inline)) {
+    const int kmax = sk_len - 1;
+    int key0 = min((t_begin + j) * kD2Keys + 8 * w, kmax);
+    const uint8_t *kp, *vp;
+    bool bad = false;
+    if constexpr (MODE == FW_KV_PAGED) {
+      key0 &= ~7;  // an 8-row group never straddles a page (P % 16 == 0)
+      const int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
+      bad = page < 0 || page >= a.num_pages;
+      kp = a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * kD2RowB;
+      if (bad) kp = kZeroKV;
+      vp = kp + kD2RowB;
+    } else {
+      kp = kbase_p + (size_t)key0 * kstB;
+      vp = vbase_p + (size_t)key0 * vstB;
+    }
+    const uint32_t lim = bad ? 0u : (uint32_t)(kmax - key0);
+    const uint32_t d = (uint32_t)(8 * w * kD2RowB) + (uint32_t)buf * kD2TileB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t rl = min(2u * i + lr, lim);  // rows past the last key re-read it
+      lds_dma16(kp, __umul24(rl, kstB) + dsrc[i], lds0 + d + 2 * i * kD2RowB);
+      lds_dma16(vp, __umul24(rl, vstB) + dsrc[i], ldsV + d + 2 * i * kD2RowB);
+    }
+  };
+  // Tiles 0-2 go out before the Q loads so the latencies overlap.
+  if (T > 0) dma(0, 0);
+  if (T > 1) dma(1, 1);
+  if (T > 2) dma(2, 2);
+
+  // ------------------------------------------------------------ Q^T operand
+  bf16x8_t qop[16];
+  {
+    const uint16_t *qp = a.q + (size_t)b * a.qsb + (size_t)h * a.qsh +
+                         (size_t)(qtok0 + (row_ok ? qrow : 0)) * a.qst;
+    const float qs = row_ok ? q_scale_of(a) : 0.f;  // rows past the end get q = 0
+    load_q_operand<256>(a, qp, hh, qs, qrow + off, qop);
+  }
+  // Q^T lives in AGPRs (an MFMA reads its B operand from there directly),
+  // leaving the VGPRs to the K / V operand rings and the softmax.
+#pragma unroll
+  for (int j = 0; j < 16; ++j) asm volatile("" : "+a"(qop[j]));
+
+  f32x16_t oacc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // ---- LDS operand addressing (per-lane byte offsets within a buffer).
+  // K (A of S^T, 32 keys x 16 dims of step j): row n, logical chunk 2j + hh;
+  // steps j and j + 8 are 256 bytes apart.
+  uint32_t kofs[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kofs[j] = lds0 + n * kD2RowB + 16 * ((2 * j + hh) ^ swz(n));
+  // V^T (A of O^T, 32 dims x 16 keys of step u, dim block c): read r (0, 1)
+  // of lane (G = lane/16, a, b) addresses key 16u + 8r + 4(G/2) + a and dims
+  // 32c + 16(G%2) + 4b; blocks c and c + 4 are 256 bytes apart, steps u 8 KiB.
+  const int tr_G = lane >> 4, tr_a = (lane >> 2) & 3, tr_b = lane & 3;
+  uint32_t vofs[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 8 * r + 4 * (tr_G >> 1) + tr_a;
+      const int chunk = 4 * c + 2 * (tr_G & 1) + (tr_b >> 1);
+      vofs[c][r] = ldsV + row * kD2RowB + 16 * (chunk ^ swz(row)) + 8 * (tr_b & 1);
+    }
+
+  // S^T of a tile (32 keys x 32 rows, one f32x16 per lane: element 4j + k is
+  // key 8j + 4hh + k of row n).  The QK starts from zero (an inline constant
+  // of the first MFMA): the softmax of the previous tile may still move the
+  // anchor after this QK is issued, so the anchor is subtracted at the
+  // exponentials instead.  One wave per SIMD leaves nothing to hide LDS
+  // latency or VALU work but the wave's own MFMAs, so the QK is a pinned
+  // software pipeline: K operands are read four MFMA steps ahead, and each
+  // step also exponentiates one score of the previous tile (p[j] =
+  // exp2(sp[j] - m_use), summed into psum).
+  auto qk_exp = [&](f32x16_t &s, const uint32_t buf, const f32x16_t &sp, float m_use,
+                    float (&p)[16], float &psum) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.f;
+    constexpr int KP = 4;
+    bf16x8_t kop[KP];
+    auto kread = [&](int j) {
+      kop[j % KP] = __builtin_bit_cast(
+          bf16x8_t, *(const FW_LDS u32x4_t *)(kofs[j & 7] + buf + 256 * (j >> 3)));
+    };
+#pragma unroll
+    for (int j = 0; j < KP; ++j) kread(j);
+    psum = 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bf16x8_t op = kop[j % KP];
+      if (j + KP < 16) kread(j + KP);
+      s = mfma32(op, qop[j], s);
+      p[j] = fast_exp2(sp[j] - m_use);
+      psum += p[j];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto pack_p = [&](const float (&p)[16], bf16x8_t (&pop)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4_t pw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pw[e] = pack_bf16(p[8 * u + 2 * e], p[8 * u + 2 * e + 1]);
+      pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+    }
+  };
+  // PV of a tile: O^T += V^T P^T over its two 16-key steps, the transposing V
+  // reads three MFMA steps ahead, pinned.
+  auto pv = [&](const bf16x8_t (&pop)[2], const uint32_t buf) __attribute__((always_inline)) {
+    auto vread = [&](int u, int c) {
+      const uint32_t o = buf + 8192u * u + 256u * (c >> 2);
+      const v4i16_t p0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(vofs[c & 3][0] + o));
+      const v4i16_t p1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(vofs[c & 3][1] + o));
+      return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    constexpr int VP = 3;
+    bf16x8_t vop[VP + 1];
+#pragma unroll
+    for (int i = 0; i < VP; ++i) vop[i] = vread(i >> 3, i & 7);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {  // i = 8u + c
+      if (i + VP < 16) vop[(i + VP) % (VP + 1)] = vread((i + VP) >> 3, (i + VP) & 7);
+      oacc[i & 7] = mfma32(vop[i % (VP + 1)], pop[i >> 3], oacc[i & 7]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Softmax of a tile (log2 units, lane = query row n), static anchor as in
+  // the ping-pong kernel: exponentiate against m_run; only when a lane's
+  // partial row sum overflows 2^16 or a row meets its first valid key does
+  // the wave take the slow path (row max, new anchor, O / l rescale).
+  // Afterwards s holds score - m_sub (returned): 0, or with softcap the
+  // anchor of now, subtracted after the tanh.
+  auto softmax_pre = [&](f32x16_t &s, int t) __attribute__((always_inline)) {
+    const int kb = t * kD2Keys;
+    const float m_now = m_run == -INFINITY ? 0.f : m_run;
+    if constexpr (SOFTCAP) {
+      f32x16_t *sp = &s;
+      softcap_scores<1, 16, true>(sp, a.softcap_log2, m_now);
+    }
+    const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kD2Keys <= row_hi(w_first) &&
+                      kb + kD2Keys <= sk_len;
+    if (!full) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kb + 8 * (e >> 2) + 4 * hh + (e & 3);
+        s[e] = (key >= r_lo && key < r_hi) ? s[e] : -INFINITY;
+      }
+    }
+    return SOFTCAP ? m_now : 0.f;
+  };
+  auto exponentiate = [&](const f32x16_t &s, float m_use, bf16x8_t (&pop)[2]) __attribute__((always_inline)) {
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4_t pw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(s[8 * u + 2 * e] - m_use);
+        const float p1 = fast_exp2(s[8 * u + 2 * e + 1] - m_use);
+        psum += p0 + p1;
+        pw[e] = pack_bf16(p0, p1);
+      }
+      asm volatile("" : "+v"(pw));  // packed here, not after the slow path's join
+      pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+    }
+    return psum;
+  };
+  auto softmax_fix = [&](f32x16_t &s, int t, float m_sub, float &psum, bf16x8_t (&pop)[2]) __attribute__((always_inline)) {
+    const int kb = t * kD2Keys;
+    const bool row_has_key = max(r_lo, kb) < min(r_hi, kb + kD2Keys);
+    if (__any(!(psum <= kPsumTrigger) || (m_run == -INFINITY && row_has_key))) {
+      asm volatile("" ::: "memory");  // a real branch: never if-converted
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[e]);
+      tmax = wave_max_xor(tmax, 32) + m_sub;
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      psum = exponentiate(s, (m_new == -INFINITY ? 0.f : m_new) - m_sub, pop);
+      l_run *= alpha;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) oacc[c] *= alpha;
+    }
+    l_run += psum;
+  };
+
+  if (T > 0) {
+    // waits: a step's copies (8 instructions) complete two steps later
+    if (T > 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (T > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // tile 0 complete
+    f32x16_t sa, sb;
+    {
+      float p[16], psum;
+      const f32x16_t z = {};
+      qk_exp(sa, 0, z, 0.f, p, psum);  // QK(0); its exponentials are unused
+    }
+    // One step: softmax of tile t (scores in s0) and PV(t); QK(t+1) into s1.
+    auto step = [&](int t, f32x16_t &s0, f32x16_t &s1, const auto bi) __attribute__((always_inline)) {
+      constexpr int B = decltype(bi)::value;  // t % 4
+      // tile t+1 complete (tile t+2's copies may still be in flight), and
+      // every wave is done with tile t-1's buffer
+      if (t + 2 < T) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      if (t + 3 < T) dma(t + 3, (B + 3) % 4);
+      const float m_sub = softmax_pre(s0, t_begin + t);
+      float p[16], psum;
+      // QK(t+1) with the exponentials of tile t; at t = T-1 the QK reads a
+      // stale buffer and is never used
+      qk_exp(s1, ((B + 1) % 4) * kD2TileB, s0, (m_run == -INFINITY ? 0.f : m_run) - m_sub, p,
+             psum);
+      bf16x8_t pop[2];
+      pack_p(p, pop);
+      softmax_fix(s0, t_begin + t, m_sub, psum, pop);
+      pv(pop, B * kD2TileB);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    for (int t = 0; t < T; t += 4) {
+      step(t, sa, sb, I0());
+      if (t + 1 >= T) break;
+      step(t + 1, sb, sa, I1());
+      if (t + 2 >= T) break;
+      step(t + 2, sa, sb, I2());
+      if (t + 3 >= T) break;
+      step(t + 3, sb, sa, I3());
+    }
+  }
+
+  // ------------------------------------------------------------ epilogue
+  l_run += __shfl_xor(l_run, 32, 64);
+  float M = m_run, Lsum = l_run, oscale = 1.f;
+  if (a.sinks) {
+    const float sk = a.sinks[h] * kLog2e;
+    if (sk != -INFINITY) {
+      const float Mn = fmaxf(M, sk);
+      const float c_old = fast_exp2(M - Mn);
+      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
+      oscale = c_old;
+      M = Mn;
+    }
+  }
+  if (!row_ok) return;
+  const bool any = Lsum > 0.f && l_run > 0.f;
+  const float scale = any ? oscale * v_descale_of(a) / Lsum : 0.f;
+  uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
+                          pack_bf16(oacc[c][4 * rr + 2] * scale, oacc[c][4 * rr + 3] * scale)};
+      *(u32x2_t *)(op + 32 * c + 8 * rr + 4 * hh) = wv;
+    }
+  if (a.lse && hh == 0) {
+    a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qtok0 + qrow] =
+        Lsum > 0.f ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
+  }
+}
+
 // One workgroup: per-sequence q tiles from cu_seqlens_q, then padding tiles
 // for the packed rows past cu_seqlens_q[num_active] (schedule.py:617-717).
 // When there are at most kSortTiles sequence tiles they are ordered by cost,
@@ -1115,8 +1508,8 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 
 // Kernel choice: bf16 K/V at head_dim 128 -> ping-pong kernel (256-row
 // tiles; the softcap variant is 3% faster on C4's shape than a 4-wave,
-// two-per-CU kernel that ran the tanh beside its own MFMAs); fp8 pools and
-// head_dim 256 -> register-staged kernel.
+// two-per-CU kernel that ran the tanh beside its own MFMAs); bf16 at 256 ->
+// the one-wave-per-SIMD d256 kernel; fp8 pools -> register-staged kernel.
 static bool use_pingpong(const fw_prefill_params *p) {
   return p->kv_dtype == FW_BF16 && p->head_dim == 128;
 }
@@ -1126,7 +1519,10 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int head_
                         hipStream_t s) {
   if (head_dim == 256) {
     switch (kv_dtype) {
-      case FW_BF16: fw_prefill_staged_kernel<MODE, FW_BF16, 256><<<grid, 256, 0, s>>>(a); break;
+      case FW_BF16:
+        if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true><<<grid, 256, 0, s>>>(a);
+        else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
+        break;
       case FW_FP8_E4M3:
         if constexpr (MODE == FW_KV_PAGED)
           fw_prefill_staged_kernel<MODE, FW_FP8_E4M3, 256><<<grid, 256, 0, s>>>(a);
