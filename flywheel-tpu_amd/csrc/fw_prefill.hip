@@ -51,22 +51,27 @@ struct PrefillArgs {
   const void *rcos, *rsin;  // fused Q RoPE tables, or null
   int rrows, rf32, ril;
   int seqused_plus_q;  // paged: kv length = seqused_k + the sequence's q length
+  // log2 of the query heads one workgroup serves (the ping-pong kernel: heads
+  // of one GQA group over the same q rows; 0 for the other kernels)
+  int hpw_shift;
 };
 
-// Varlen/paged workgroup -> (schedule slot, query head).  The heads of a slot
-// are consecutive workgroups, so slots start in schedule order (heaviest
-// first).  Workgroup bid runs on XCD bid % 8; when H % 8 == 0 XCD x takes
-// heads x*H/8 .. (x+1)*H/8 - 1 of every slot, i.e. whole GQA groups whenever
-// H/8 is a multiple of the group size, so their K/V stay in that XCD's L2.
-__device__ __forceinline__ void sched_slot(const PrefillArgs &a, int &slot, int &h) {
+// Varlen/paged workgroup -> (schedule slot, head group of 2^hpw_shift
+// consecutive query heads).  The head groups of a slot are consecutive
+// workgroups, so slots start in schedule order (heaviest first).  Workgroup
+// bid runs on XCD bid % 8; when the group count NG is a multiple of 8, XCD x
+// takes groups x*NG/8 .. (x+1)*NG/8 - 1 of every slot, i.e. whole GQA groups
+// whenever NG/8 groups hold whole GQA groups, so their K/V stay in that XCD's L2.
+__device__ __forceinline__ void sched_slot(const PrefillArgs &a, int &slot, int &hg) {
   const int bid = blockIdx.x;
-  if (a.H % 8 == 0) {
-    const int x = bid & 7, wi = bid >> 3, hx = a.H >> 3;
+  const int ng = a.H >> a.hpw_shift;
+  if (ng % 8 == 0) {
+    const int x = bid & 7, wi = bid >> 3, hx = ng >> 3;
     slot = wi / hx;
-    h = x * hx + wi % hx;
+    hg = x * hx + wi % hx;
   } else {
-    slot = bid / a.H;
-    h = bid % a.H;
+    slot = bid / ng;
+    hg = bid % ng;
   }
 }
 
@@ -525,8 +530,9 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define FW_LDS __attribute__((address_space(3)))
 
 // ---------------------------------------------------------------------------
-// bf16 K/V, ping-pong schedule.  Workgroup = 8 waves = 256 q rows of one query
-// head (wave w owns rows 32w .. 32w+31), one workgroup per CU, so each SIMD
+// bf16 K/V, ping-pong schedule.  Workgroup = 8 waves of 32 q rows each: 256
+// rows of one query head, or 256 / 2^k rows of 2^k query heads that share a KV
+// head (head packing, below), one workgroup per CU, so each SIMD
 // runs one wave of group 0 (waves 0-3) and one of group 1 (waves 4-7).  Time
 // is cut into barrier-delimited slots and group 1 runs one slot behind group
 // 0, so in every slot one wave of each SIMD does matrix work (PV of tile j-1,
@@ -565,11 +571,20 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   const int grp = w >> 2;
   const int n = lane & 31;
   const int g = lane >> 5;
+  // Head packing: the workgroup serves 2^hpw_shift query heads of one GQA
+  // group over the same R = 256 >> hpw_shift q rows; wave w takes head
+  // hg * 2^hpw_shift + (w >> wph_shift) and rows q0 + 32 rb .. q0 + 32 rb + 31.
+  // The heads share every K/V tile, and the narrower row span visits fewer
+  // partly masked tiles on the causal diagonal and the window edge.
+  const int wph_shift = 3 - a.hpw_shift;
+  const int rb = w & ((1 << wph_shift) - 1);
+  const int R = kPPRows >> a.hpw_shift;
 
   // ------------------------------------------------------------ tile decode
-  int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
+  int b = 0, hg, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
   if constexpr (MODE == FW_KV_DENSE) {
-    const int nbh = a.B * a.H;
+    const int ng = a.H >> a.hpw_shift;
+    const int nbh = a.B * ng;
     const int bid = blockIdx.x;
     int qt, bh;
     if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
@@ -580,23 +595,24 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       qt = a.n_qt - 1 - bid / nbh;
       bh = bid % nbh;
     }
-    b = bh / a.H;
-    h = bh % a.H;
-    q0 = qt * kPPRows;
+    b = bh / ng;
+    hg = bh % ng;
+    q0 = qt * R;
     sq_len = a.Sq;
     sk_len = a.Sk;
   } else {
     int slot;
-    sched_slot(a, slot, h);
+    sched_slot(a, slot, hg);
     if (slot >= a.sched[0]) return;
     seq = a.sched[1 + 2 * slot];
     q0 = a.sched[2 + 2 * slot];
     if (seq < 0) {  // packed padding rows: out 0, lse -inf
-      const int r0 = q0 + w * 32 + n;
+      const int hp = (hg << a.hpw_shift) + (w >> wph_shift);
+      const int r0 = q0 + 32 * rb + n;
       if (r0 < a.Sq) {
-        uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
+        uint16_t *o = a.out + (size_t)hp * a.osh + (size_t)r0 * a.ost;
         for (int d = g * 64; d < g * 64 + 64; d += 8) *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
-        if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
+        if (a.lse && g == 0) a.lse[(size_t)hp * a.lsh + r0] = -INFINITY;
       }
       return;
     }
@@ -609,6 +625,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       sk_len = a.seqused_k[seq] + (a.seqused_plus_q ? sq_len : 0);
     }
   }
+  const int h = (hg << a.hpw_shift) + (w >> wph_shift);  // this wave's query head
   const int hk = h / a.G;
   const int off = sk_len - sq_len;  // bottom-right alignment
   auto row_hi = [&](int r) {
@@ -619,14 +636,14 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     const int p = r + off;
     return a.wl >= 0 ? max(0, p - a.wl) : 0;
   };
-  const int last_row = min(q0 + kPPRows, sq_len) - 1;
+  const int last_row = min(q0 + R, sq_len) - 1;
   const int wg_lo = row_lo(q0);
   const int wg_hi = row_hi(last_row);
-  const int w_first = q0 + 32 * w;
+  const int w_first = q0 + 32 * rb;
   const int w_last = min(w_first + 31, sq_len - 1);
   const bool w_any = w_first <= w_last;
   const int w_lo = w_any ? row_lo(w_first) : 0;
-  const int qrow = q0 + 32 * w + n;
+  const int qrow = q0 + 32 * rb + n;
   const bool row_ok = qrow < sq_len;
   const int r_lo = row_lo(qrow), r_hi = row_hi(qrow);
 
@@ -999,7 +1016,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     for (int i = 0; i < 8; ++i) {
       const int r = 4 * i + (lane >> 4);
       const u32x4_t v = *(const FW_LDS u32x4_t *)(wbase + r * kRowB + 16 * (cc ^ (r & 15)));
-      const int grow = q0 + 32 * w + r;
+      const int grow = q0 + 32 * rb + r;
       if (grow < sq_len)
         // non-temporal: whole rows that no later launch step re-reads here
         __builtin_nontemporal_store(v, (u32x4_t *)(a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + grow) * a.ost + 8 * cc));
@@ -1497,21 +1514,36 @@ static int max_sched_tiles(const fw_prefill_params *p, int qt) {
   return 2 * ((p->seqlen_q + qt - 1) / qt) + p->batch + 1;
 }
 
-}  // namespace fw
-
-using namespace fw;
-
-extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
-  if (p->kv_mode == FW_KV_DENSE) return 0;
-  return align_up((size_t)(1 + 2 * max_sched_tiles(p, kQT)) * sizeof(int32_t), 256);
-}
-
 // Kernel choice: bf16 K/V at head_dim 128 -> ping-pong kernel (256-row
 // tiles; the softcap variant is 3% faster on C4's shape than a 4-wave,
 // two-per-CU kernel that ran the tanh beside its own MFMAs); bf16 at 256 ->
 // the one-wave-per-SIMD d256 kernel; fp8 pools -> register-staged kernel.
 static bool use_pingpong(const fw_prefill_params *p) {
   return p->kv_dtype == FW_BF16 && p->head_dim == 128;
+}
+
+// log2 of the query heads per ping-pong workgroup: the largest power of two
+// up to 8 that divides the GQA group size (1 for MHA).
+static int pp_head_shift(const fw_prefill_params *p) {
+  const int G = p->nheads_k > 0 ? p->nheads / p->nheads_k : 1;
+  int sh = 0;
+  while (sh < 3 && G % (2 << sh) == 0) ++sh;
+  return sh;
+}
+
+// q rows per schedule slot (and per dense q tile).
+static int prefill_tile_rows(const fw_prefill_params *p) {
+  return use_pingpong(p) ? kPPRows >> pp_head_shift(p) : kQT;
+}
+
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
+  if (p->kv_mode == FW_KV_DENSE) return 0;
+  return align_up((size_t)(1 + 2 * max_sched_tiles(p, prefill_tile_rows(p))) * sizeof(int32_t),
+                  256);
 }
 
 template <int MODE>
@@ -1589,7 +1621,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.Sq = p->seqlen_q;
   a.Sk = p->seqlen_k;
   const bool pingpong = use_pingpong(p);
-  const int qt_rows = pingpong ? kPPRows : kQT;
+  a.hpw_shift = pingpong ? pp_head_shift(p) : 0;
+  const int qt_rows = prefill_tile_rows(p);
+  const int head_groups = p->nheads >> a.hpw_shift;
   a.n_qt = (p->seqlen_q + qt_rows - 1) / qt_rows;
   a.P = p->page_size;
   a.max_pages = p->max_pages;
@@ -1617,7 +1651,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * p->nheads), p->kv_dtype, p->head_dim, s);
+    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * head_groups), p->kv_dtype, p->head_dim, s);
     return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -1643,8 +1677,8 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
                                          a.wl, a.wr);
   int st = check_launch("fw_prefill_schedule");
   if (st != FW_OK) return st;
-  // one workgroup per (schedule slot, query head); see sched_slot
-  dim3 grid(max_tiles * p->nheads);
+  // one workgroup per (schedule slot, head group); see sched_slot
+  dim3 grid(max_tiles * head_groups);
   if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, p->head_dim, s);
   else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, s);
   return check_launch("fw_prefill");

@@ -35,6 +35,12 @@ def head_major(x):  # (B, S, H, D) -> (B, H, S, D)
         (1, 4, 1, 512, 512, True, (-1, -1), 20.0, False),
         (1, 4, 1, 512, 512, True, (-1, -1), 50.0, False),
         (1, 4, 2, 130, 130, True, (-1, -1), 0.0, True),
+        # head packing: 3 (one head per workgroup), 6 (two), 16 (8 per workgroup, two
+        # workgroups per KV head) query heads per KV head
+        (1, 6, 2, 300, 300, True, (-1, -1), 0.0, False),
+        (2, 12, 2, 200, 260, True, (40, -1), 0.0, True),
+        (1, 16, 1, 100, 400, True, (-1, -1), 50.0, False),
+        (1, 16, 2, 77, 77, False, (-1, -1), 0.0, False),
     ],
 )
 def test_flash_attn_func(b, h, hk, sq, sk, causal, window, softcap, sinks):
