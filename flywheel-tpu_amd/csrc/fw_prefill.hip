@@ -544,7 +544,7 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 // K/V tiles rotate through four LDS buffers (tile j in buffer j % 4) and
 // arrive by direct global->LDS copies; every wave copies its own 8 key rows of
 // tile j+2 in its softmax slot of tile j.  With softcap (SOFTCAP) the tanh
-// runs in the softmax slot too.
+// runs in the MFMA slot, beside the PV MFMAs that follow the QK.
 constexpr int kPPWaves = 8;
 // Zero K and V rows (256 B each at head_dim 128, 512 B at 256): the copy
 // source for the keys of an invalid page id.
@@ -773,7 +773,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // MFMAs stalls its own MFMA issue (measured 50-55 cycles per MFMA against
   // 35-38 when reads and MFMAs alternate).
   // The operands of the first kPipe PV steps (V of tile j-1, whose buffer is
-  // complete) are read before the barrier that opens the MFMA slot.
+  // complete) are read at the end of the previous MFMA slot.
   constexpr int kPipe = 3;
   bf16x8_t opr[32], qr[8];
   auto rd = [&](const int st, const uint32_t bufq, const uint32_t bufp) __attribute__((always_inline)) {
@@ -794,14 +794,22 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
     for (int st = 0; st < kPipe; ++st) rd(st, 0, bp * kTileB);
   };
+  constexpr bool kCapInM = SOFTCAP;
+  // Issue order of the slot's steps (0-15 PV, 16-31 QK).  With the softcap in
+  // the MFMA slot: three PV steps (operands read before the slot), the 16 QK
+  // steps, then the other 13 PV steps with the tanh of this tile's scores
+  // spread over them.
+  auto slot_step = [&](const int pos) __attribute__((always_inline)) {
+    if constexpr (!kCapInM) return pos;
+    return pos < 3 ? pos : pos < 19 ? pos + 13 : pos - 16;
+  };
   auto mslot = [&](const int bq, const int bp, const bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
     const uint32_t bufq = bq * kTileB, bufp = bp * kTileB;
     // the QK accumulates onto -anchor (with softcap onto 0: the anchor is
     // subtracted after the tanh)
     const float m_init = (SOFTCAP || m_run == -INFINITY) ? 0.f : -m_run;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int st = 0; st < 32; ++st) {
+    auto step = [&](const int pos) __attribute__((always_inline)) {
+      const int st = slot_step(pos);
       if (st < 16) {
         const int u = st >> 2, c = st & 3;
         oacc[c] = mfma32(opr[st], pop[u], oacc[c]);
@@ -819,8 +827,55 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
         const int j = (st - 16) >> 1, hh = (st - 16) & 1;
         sacc[hh] = mfma32(opr[st], qr[j], sacc[hh]);
       }
-      if (st + kPipe < 32) rd(st + kPipe, bufq, bufp);
-      __builtin_amdgcn_sched_barrier(0);  // MFMA, then the reads of step st+kPipe
+      if (pos + kPipe < 32) rd(slot_step(pos + kPipe), bufq, bufp);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kCapInM) {
+#pragma unroll
+      for (int pos = 0; pos < 19; ++pos) {
+        step(pos);
+        __builtin_amdgcn_sched_barrier(0);  // MFMA, then the reads kPipe steps on
+      }
+      // softcap_log2 * tanh(s) - anchor, by the wave's largest |s| as in
+      // softcap_scores: the degree-3 or degree-5 polynomial, three scores per
+      // remaining PV step (the degree-3 one as the degree-5 form with c2 = 0,
+      // bit-identical); beyond 0.3 the steps apply the identity and the exact
+      // tanh follows the MFMAs.  No branch around the MFMAs: a branch there
+      // makes the compiler copy the O accumulators at the join.
+      const float m_qk = m_run == -INFINITY ? 0.f : m_run;
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(sacc[i][e]));
+      const float cl = a.softcap_log2;
+      const bool exact = __any(amax > kTanhPolyBound);
+      const bool deg5 = __any(amax > kTanhPoly3Bound);
+      const float c0 = exact ? 1.f : cl * (deg5 ? kTanhC0 : kTanhD0);
+      const float c1 = exact ? 0.f : cl * (deg5 ? kTanhC1 : kTanhD1);
+      const float c2 = exact || !deg5 ? 0.f : cl * kTanhC2;
+      const float an = exact ? 0.f : m_qk;
+#pragma unroll
+      for (int pos = 19; pos < 32; ++pos) {
+        step(pos);
+#pragma unroll
+        for (int k = 3 * (pos - 19); k < 3 * (pos - 19) + 3 && k < 32; ++k)
+          sacc[k >> 4][k & 15] = tanh_poly_scaled<true>(sacc[k >> 4][k & 15], c0, c1, c2, an);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (exact) {
+        asm volatile("" ::: "memory");  // a real branch: never if-converted
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sacc[i][e] = fmaf(fast_tanh(sacc[i][e]), cl, -m_qk);
+      }
+    } else {
+#pragma unroll
+      for (int pos = 0; pos < 32; ++pos) {
+        step(pos);
+        __builtin_amdgcn_sched_barrier(0);  // MFMA, then the reads kPipe steps on
+      }
     }
   };
 
@@ -834,7 +889,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     // the scores arrive as s - anchor (the MFMA accumulated onto -anchor, or
     // the softcap subtracts it)
     const float m_qk = m_run == -INFINITY ? 0.f : m_run;
-    if constexpr (SOFTCAP) softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
+    if constexpr (SOFTCAP && !kCapInM) softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
     const bool full = kb >= w_lo && kb >= row_lo(w_last) && kb + kKT <= row_hi(w_first) &&
                       kb + kKT <= sk_len;
     bool row_has_key = true;
@@ -944,6 +999,10 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       // issues copies.
       __builtin_amdgcn_s_setprio(2);
       mslot(B, (B + 3) % 4, pops);
+      // V of tile j for the first PV steps of the next MFMA slot, read while
+      // this wave would otherwise wait at the barrier (the buffer has been
+      // complete since before this slot and is not rewritten until tile j+4)
+      mslot_pre(B);
       __builtin_amdgcn_s_setprio(0);
       if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       slot_barrier();
@@ -959,7 +1018,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
         }
       }
       if (j < T) softmax(t_begin + j, pops);
-      mslot_pre(B);  // V of tile j for the PV of the next MFMA slot
       if (grp == 0) {
         if (copy) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // tile j+1 in
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
