@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void fw_write_pages_kernel(
 using namespace fw;
 
 extern "C" const char *fw_last_error(void) { return g_last_error.c_str(); }
-extern "C" int fw_abi_version(void) { return 5; }
+extern "C" int fw_abi_version(void) { return 6; }
 
 extern "C" int fw_append_ragged(void *kv_cache, const void *k, const void *v,
                                 const int32_t *cu_seqlens, const int32_t *cache_seqlens,

@@ -24,7 +24,8 @@
 //                             rows, transposed in registers by v_perm)
 //                             x P^T (B operand, the S^T registers as bf16).
 // Both products use v_mfma_f32_16x16x32_bf16; nothing goes through LDS.
-// head_dim D is 128 or 256 (D / 128 "halves" of V and O).
+// head_dim D is 64, 128 or 256 (max(1, D / 128) "halves" of 128 V and O dims;
+// at 64 the lanes of dims 64-127 carry zero V and nothing is stored for them).
 #include "fw_common.h"
 
 #include <algorithm>
@@ -185,9 +186,12 @@ __device__ __forceinline__ int qk_dim(int j, int g) {
   else return 64 * (j >> 1) + 16 * g + 8 * (j & 1);
 }
 
+// 128-dim halves of V and O (one, partly used, at head_dim 64)
+template <int D> constexpr int kVH = D >= 128 ? D / 128 : 1;
+
 template <int KV, int D>
 struct DecodeTile {
-  static constexpr int VH = D / 128;
+  static constexpr int VH = kVH<D>;
   KRow<KV, D> krow[2];  // K of the two 16-key sub-tiles (lane row n)
   // V of keys 4g+i / 16+4g+i, dims 128h + 8n .. +7 (16 or 8 bytes a key)
   typename std::conditional<KV == FW_BF16, u32x4_t, u32x2_t>::type vraw[8][VH];
@@ -201,7 +205,7 @@ template <int KV, int D> constexpr int kDecodeOcc = D > 128 ? 1 : 2;
 template <int KV, int D>
 __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_decode_kernel(DecodeArgs a) {
   constexpr int EB = KV == FW_BF16 ? 2 : 1;  // bytes per cache element
-  constexpr int VH = D / 128;
+  constexpr int VH = kVH<D>;
   constexpr int VB = KV == FW_BF16 ? 16 : 8;  // bytes of one lane's V piece
   __shared__ __attribute__((aligned(16))) float stage[kMaxWaves][16 * kStageRow];
   const int lane = threadIdx.x & 63;
@@ -468,9 +472,11 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
 #pragma unroll
             for (int vh = 0; vh < VH; ++vh) {
               if constexpr (KV == FW_BF16)
-                tl.vraw[4 * sub + i][vh] = *(const u32x4_t *)(vrow + vo + 128 * EB * vh);
+                tl.vraw[4 * sub + i][vh] = 8 * n < D ? *(const u32x4_t *)(vrow + vo + 128 * EB * vh)
+                                                     : u32x4_t{0, 0, 0, 0};
               else
-                tl.vraw[4 * sub + i][vh] = *(const u32x2_t *)(vrow + vo + 128 * EB * vh);
+                tl.vraw[4 * sub + i][vh] = 8 * n < D ? *(const u32x2_t *)(vrow + vo + 128 * EB * vh)
+                                                     : u32x2_t{0, 0};
             }
           }
         }
@@ -503,8 +509,10 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       for (int k8 = 0; k8 < 8; ++k8)
 #pragma unroll
         for (int vh = 0; vh < VH; ++vh) {
-          if constexpr (KV == FW_BF16) tn.vraw[k8][vh] = *(const u32x4_t *)(vp + 128 * EB * vh);
-          else tn.vraw[k8][vh] = *(const u32x2_t *)(vp + 128 * EB * vh);
+          if constexpr (KV == FW_BF16)
+            tn.vraw[k8][vh] = 8 * n < D ? *(const u32x4_t *)(vp + 128 * EB * vh) : u32x4_t{0, 0, 0, 0};
+          else
+            tn.vraw[k8][vh] = 8 * n < D ? *(const u32x2_t *)(vp + 128 * EB * vh) : u32x2_t{0, 0};
         }
       compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true);
     }
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int row = 2 * k + (lane >> 5), col = 4 * (lane & 31);
-        if (row < rows_valid)
+        if (row < rows_valid && col < D)
           *(f32x4_t *)(po + row * D + col) = *(const f32x4_t *)(st + row * kStageRow + col);
       }
     }
@@ -559,7 +567,8 @@ struct CombineArgs {
 // LDS.
 template <int D>
 __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
-  constexpr int VH = D / 128;
+  constexpr int VH = kVH<D>;
+  const bool dims_ok = 8 * (threadIdx.x & 15) < D;  // head_dim 64: parts 8-15 hold no dims
   const DecodeArgs &a = c.d;
   __shared__ float s_acc[4][4][16][8 * VH];
   __shared__ float2 s_ml[4][4];
@@ -618,8 +627,8 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
         const float *po = a.ws_o + slot * D + part * 8;
 #pragma unroll
         for (int vh = 0; vh < VH; ++vh) {
-          v[i][2 * vh] = *(const f32x4_t *)(po + 128 * vh);
-          v[i][2 * vh + 1] = *(const f32x4_t *)(po + 128 * vh + 4);
+          v[i][2 * vh] = dims_ok ? *(const f32x4_t *)(po + 128 * vh) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+          v[i][2 * vh + 1] = dims_ok ? *(const f32x4_t *)(po + 128 * vh + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
       }
 #pragma unroll
@@ -676,6 +685,7 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
   const float scale = any ? vdesc / Lt : 0.f;
 #pragma unroll
   for (int vh = 0; vh < VH; ++vh) {
+    if (!dims_ok) break;
     uint16_t *op = c.out + (((size_t)b * a.Sq + tok) * a.H + hq) * D + 128 * vh + part * 8;
     u32x4_t w;
 #pragma unroll
@@ -718,8 +728,9 @@ struct DecodeLayout {
 static int decode_layout(const fw_decode_params *p, DecodeLayout *L) {
   FW_REQUIRE(p->nheads_k > 0 && p->nheads > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads=%d must be a multiple of nheads_k=%d", p->nheads, p->nheads_k);
-  FW_REQUIRE(p->head_dim == 128 || p->head_dim == 256, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 decode kernel takes head_dim 128 or 256; got %d", p->head_dim);
+  FW_REQUIRE(p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256,
+             FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 decode kernel takes head_dim 64, 128 or 256; got %d", p->head_dim);
   FW_REQUIRE(p->page_size > 0 && p->page_size % 16 == 0, FW_ERR_VALUE,
              "page_size must be a positive multiple of 16; got %d", p->page_size);
   FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->max_pages > 0, FW_ERR_VALUE,
@@ -830,17 +841,16 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
   a.sm_scale = p->softmax_scale;
   a.softcap = p->softcap;
   hipStream_t s = (hipStream_t)stream;
-  const bool d256 = p->head_dim == 256;
+  auto launch_kv = [&](auto kv) {
+    constexpr int KV = decltype(kv)::value;
+    if (p->head_dim == 256) launch_decode<KV, 256>(a, L, s);
+    else if (p->head_dim == 64) launch_decode<KV, 64>(a, L, s);
+    else launch_decode<KV, 128>(a, L, s);
+  };
   switch (p->kv_dtype) {
-    case FW_BF16:
-      d256 ? launch_decode<FW_BF16, 256>(a, L, s) : launch_decode<FW_BF16, 128>(a, L, s);
-      break;
-    case FW_FP8_E4M3:
-      d256 ? launch_decode<FW_FP8_E4M3, 256>(a, L, s) : launch_decode<FW_FP8_E4M3, 128>(a, L, s);
-      break;
-    default:
-      d256 ? launch_decode<FW_FP8_E5M2, 256>(a, L, s) : launch_decode<FW_FP8_E5M2, 128>(a, L, s);
-      break;
+    case FW_BF16: launch_kv(std::integral_constant<int, FW_BF16>()); break;
+    case FW_FP8_E4M3: launch_kv(std::integral_constant<int, FW_FP8_E4M3>()); break;
+    default: launch_kv(std::integral_constant<int, FW_FP8_E5M2>()); break;
   }
   st = check_launch("fw_decode_kernel");
   if (st != FW_OK) return st;
@@ -853,7 +863,8 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
   c.vd = p->v_descale_ptr;
   const int row_groups = (L.rows_item + 3) / 4;
   const dim3 grid(row_groups, p->nheads_k * L.n_qtiles, p->batch);
-  if (d256) fw_decode_combine<256><<<grid, 256, 0, s>>>(c);
+  if (p->head_dim == 256) fw_decode_combine<256><<<grid, 256, 0, s>>>(c);
+  else if (p->head_dim == 64) fw_decode_combine<64><<<grid, 256, 0, s>>>(c);
   else fw_decode_combine<128><<<grid, 256, 0, s>>>(c);
   return check_launch("fw_decode_combine");
 }

@@ -26,7 +26,7 @@ constexpr int kKT = 64;      // keys per kv tile
 constexpr int kVS = 68;      // Vt row stride (bf16 elements)
 // Staged kernel LDS for head_dim D: Ks [64 keys][D + 8], Vt [D dims][68].
 template <int D> constexpr int kKS = D + 8;  // Ks row stride (bf16 elements)
-template <int D> constexpr int kStagedLds = (kKT * kKS<D> + D * kVS) * 2;
+template <int D, int DV> constexpr int kStagedLds = (kKT * kKS<D> + DV * kVS) * 2;
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -204,11 +204,14 @@ struct KvAddr {
 // with the next tile's global loads issued before the current tile's math.
 // head_dim D = 128 runs two waves per SIMD; D = 256 one (O and Q^T alone
 // take 192 registers per lane).
-template <int MODE, int KV, int D>
-__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel(PrefillArgs a) {
+template <int MODE, int KV, int D, int DV>
+__global__ __launch_bounds__(256, D > 128 || DV > 128 ? 1 : 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   constexpr int KS = kKS<D>;
-  constexpr int CPR = D / 128;  // 8-element chunks of a row per staging thread
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kStagedLds<D>];
+  // 8-element chunks of a K / V row per staging thread (16 threads a row; at
+  // head dim 64 threads 8-15 of a row have none)
+  constexpr int CPR = D >= 128 ? D / 128 : 1;
+  constexpr int CPRV = DV >= 128 ? DV / 128 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStagedLds<D, DV>];
   uint16_t *Ks = (uint16_t *)smem;
   uint16_t *Vt = (uint16_t *)(smem + kKT * KS * 2);
 
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
       for (int rr = 0; rr < 1; ++rr) {
         if (r0 < a.Sq) {
           uint16_t *o = a.out + (size_t)h * a.osh + (size_t)r0 * a.ost;
-          for (int d = g * (D / 2); d < (g + 1) * (D / 2); d += 8)
+          for (int d = g * (DV / 2); d < (g + 1) * (DV / 2); d += 8)
             *(u32x4_t *)(o + d) = u32x4_t{0, 0, 0, 0};
           if (a.lse && g == 0) a.lse[(size_t)h * a.lsh + r0] = -INFINITY;
         }
@@ -298,9 +301,9 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
     load_q_operand<D>(a, qp, g, qs, qrow + off, qop);
   }
 
-  f32x16_t oacc[D / 32];
+  f32x16_t oacc[DV / 32];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c)
+  for (int c = 0; c < DV / 32; ++c)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
@@ -313,7 +316,9 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
   // of each row, thread column sc takes the 8-element chunks sc + 16c
   const int sc = tid & 15;
   const int sr = tid >> 4;
-  u32x4_t kst[4][CPR], vst[4][CPR];
+  u32x4_t kst[4][CPR], vst[4][CPRV];
+  auto kchunk = [&](int c) { return 8 * (sc + 16 * c) < D; };
+  auto vchunk = [&](int c) { return 8 * (sc + 16 * c) < DV; };
   uint32_t kbad = 0;  // byte p: K row group p came from an invalid page id
   // The keys of an invalid page id read as zero K and V rows (the page 0 the
   // loads used may hold anything).  Every 16-key group of a tile lies on one
@@ -327,7 +332,8 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
     for (int p = 0; p < 4; ++p) {
       const int key = min(kb + sr + 16 * p, kmax);
 #pragma unroll
-      for (int c = 0; c < CPR; ++c) kst[p][c] = load_row8<KV>(addr.k_row(key), sc + 16 * c);
+      for (int c = 0; c < CPR; ++c)
+        if (kchunk(c)) kst[p][c] = load_row8<KV>(addr.k_row(key), sc + 16 * c);
       // wave-uniform: the page of the group's first key <= kmax
       if (addr.bad(min(kb + 16 * p, kmax))) kbad |= 1u << (8 * p);
     }
@@ -336,10 +342,11 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
       const int k0 = min(kb + 2 * (sr + 16 * p), kmax);
       const int k1 = min(kb + 2 * (sr + 16 * p) + 1, kmax);
 #pragma unroll
-      for (int c = 0; c < CPR; ++c) {
-        vst[2 * p][c] = load_row8<KV>(addr.v_row(k0), sc + 16 * c);
-        vst[2 * p + 1][c] = load_row8<KV>(addr.v_row(k1), sc + 16 * c);
-      }
+      for (int c = 0; c < CPRV; ++c)
+        if (vchunk(c)) {
+          vst[2 * p][c] = load_row8<KV>(addr.v_row(k0), sc + 16 * c);
+          vst[2 * p + 1][c] = load_row8<KV>(addr.v_row(k1), sc + 16 * c);
+        }
     }
   };
   auto lds_store = [&]() {
@@ -353,20 +360,21 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
       for (int p = 0; p < 2; ++p)
         if ((kbad >> (8 * ((2 * sr + 32 * p) >> 4))) & 1u)
 #pragma unroll
-          for (int c = 0; c < CPR; ++c) vst[2 * p][c] = vst[2 * p + 1][c] = u32x4_t{0, 0, 0, 0};
+          for (int c = 0; c < CPRV; ++c) vst[2 * p][c] = vst[2 * p + 1][c] = u32x4_t{0, 0, 0, 0};
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p)
 #pragma unroll
       for (int c = 0; c < CPR; ++c)
-        *(u32x4_t *)(Ks + (sr + 16 * p) * KS + 8 * (sc + 16 * c)) = kst[p][c];
+        if (kchunk(c)) *(u32x4_t *)(Ks + (sr + 16 * p) * KS + 8 * (sc + 16 * c)) = kst[p][c];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int kp = sr + 16 * p;  // key pair
 #pragma unroll
-      for (int c = 0; c < CPR; ++c)
+      for (int c = 0; c < CPRV; ++c)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+          if (!vchunk(c)) break;
           const uint32_t x0 = vst[2 * p][c][e], x1 = vst[2 * p + 1][c][e];
           const int d0 = 8 * (sc + 16 * c) + 2 * e;
           *(uint32_t *)(Vt + d0 * kVS + 2 * kp) = perm_lo(x0, x1);
@@ -452,14 +460,14 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
     l_run = l_run * alpha + psum;
     if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) oacc[c] *= alpha;
+      for (int c = 0; c < DV / 32; ++c) oacc[c] *= alpha;
     }
     // ---------------- O^T += V^T P^T : 4 k-steps of 16 keys x D/32 dim
     // tiles; the V operands of step u+1 are read while step u's MFMAs run.
-    bf16x8_t vop[2][D / 32];
-    auto read_v = [&](int u, bf16x8_t (&dst)[D / 32]) {
+    bf16x8_t vop[2][DV / 32];
+    auto read_v = [&](int u, bf16x8_t (&dst)[DV / 32]) {
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
+      for (int c = 0; c < DV / 32; ++c) {
         const uint16_t *vr = Vt + (n + 32 * c) * kVS + 16 * u + 4 * g;
         const u32x2_t lo = *(const u32x2_t *)vr;
         const u32x2_t hi = *(const u32x2_t *)(vr + 8);
@@ -472,7 +480,7 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
       if (u + 1 < 4) read_v(u + 1, vop[(u + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
+      for (int c = 0; c < DV / 32; ++c) oacc[c] = mfma32(vop[u & 1][c], pop[u], oacc[c]);
     }
   }
 
@@ -494,7 +502,7 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void fw_prefill_staged_kernel
   const float scale = any ? oscale * v_descale_of(a) / Lsum : 0.f;
   uint16_t *op = a.out + (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(qtok0 + qrow) * a.ost;
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c)
+  for (int c = 0; c < DV / 32; ++c)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const u32x2_t wv = {pack_bf16(oacc[c][4 * rr] * scale, oacc[c][4 * rr + 1] * scale),
@@ -1576,8 +1584,11 @@ static int max_sched_tiles(const fw_prefill_params *p, int qt) {
 // tiles; the softcap variant is 3% faster on C4's shape than a 4-wave,
 // two-per-CU kernel that ran the tanh beside its own MFMAs); bf16 at 256 ->
 // the one-wave-per-SIMD d256 kernel; fp8 pools -> register-staged kernel.
+static int head_dim_v_of(const fw_prefill_params *p) {
+  return p->head_dim_v > 0 ? p->head_dim_v : p->head_dim;
+}
 static bool use_pingpong(const fw_prefill_params *p) {
-  return p->kv_dtype == FW_BF16 && p->head_dim == 128;
+  return p->kv_dtype == FW_BF16 && p->head_dim == 128 && head_dim_v_of(p) == 128;
 }
 
 // log2 of the query heads per ping-pong workgroup: the largest power of two
@@ -1604,47 +1615,54 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
                   256);
 }
 
+// Kernel choice (the host has checked the head dims): bf16 128/128 -> the
+// ping-pong kernel, bf16 256/256 -> the d256 kernel, everything else (fp8
+// pools, head dim 64, head_dim_v != head_dim) -> the register-staged kernel.
+template <int MODE, int KV, int D, int DV>
+static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
+  fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
+}
 template <int MODE>
-static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int head_dim,
+static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, int dv,
                         hipStream_t s) {
-  if (head_dim == 256) {
-    switch (kv_dtype) {
-      case FW_BF16:
-        if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true><<<grid, 256, 0, s>>>(a);
-        else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
-        break;
-      case FW_FP8_E4M3:
-        if constexpr (MODE == FW_KV_PAGED)
-          fw_prefill_staged_kernel<MODE, FW_FP8_E4M3, 256><<<grid, 256, 0, s>>>(a);
-        break;
-      default:
-        if constexpr (MODE == FW_KV_PAGED)
-          fw_prefill_staged_kernel<MODE, FW_FP8_E5M2, 256><<<grid, 256, 0, s>>>(a);
-        break;
+  if (kv_dtype == FW_BF16) {
+    if (d == 128 && dv == 128) {
+      if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
+      else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
+    } else if (d == 256 && dv == 256) {
+      if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true><<<grid, 256, 0, s>>>(a);
+      else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
+    } else if (d == 64) {
+      launch_staged<MODE, FW_BF16, 64, 64>(a, grid, s);
+    } else if constexpr (MODE != FW_KV_PAGED) {  // a paged pool has one head dim
+      if (d == 128) launch_staged<MODE, FW_BF16, 128, 256>(a, grid, s);
+      else launch_staged<MODE, FW_BF16, 256, 128>(a, grid, s);
     }
     return;
   }
-  switch (kv_dtype) {
-    case FW_BF16:
-      if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
-      else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
-      break;
-    case FW_FP8_E4M3:
-      if constexpr (MODE == FW_KV_PAGED)
-        fw_prefill_staged_kernel<MODE, FW_FP8_E4M3, 128><<<grid, 256, 0, s>>>(a);
-      break;
-    default:
-      if constexpr (MODE == FW_KV_PAGED)
-        fw_prefill_staged_kernel<MODE, FW_FP8_E5M2, 128><<<grid, 256, 0, s>>>(a);
-      break;
+  if constexpr (MODE == FW_KV_PAGED) {  // fp8: paged pools only, one head dim
+    auto run = [&](auto kv) {
+      constexpr int KV = decltype(kv)::value;
+      if (d == 64) launch_staged<MODE, KV, 64, 64>(a, grid, s);
+      else if (d == 256) launch_staged<MODE, KV, 256, 256>(a, grid, s);
+      else launch_staged<MODE, KV, 128, 128>(a, grid, s);
+    };
+    if (kv_dtype == FW_FP8_E4M3) run(std::integral_constant<int, FW_FP8_E4M3>());
+    else run(std::integral_constant<int, FW_FP8_E5M2>());
   }
 }
 
 extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
-  FW_REQUIRE(p->head_dim == 128 || p->head_dim == 256, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 prefill kernels take head_dim 128 or 256; got %d", p->head_dim);
-  FW_REQUIRE(!p->rotary_cos || p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
-             "the fused RoPE takes head_dim 128; got %d", p->head_dim);
+  const int dv = head_dim_v_of(p);
+  const bool dims_ok = (p->head_dim == dv && (dv == 64 || dv == 128 || dv == 256)) ||
+                       (p->head_dim == 128 && dv == 256) || (p->head_dim == 256 && dv == 128);
+  FW_REQUIRE(dims_ok, FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 prefill kernels take head_dim / head_dim_v 64/64, 128/128, 256/256,"
+             " 128/256 or 256/128; got %d/%d", p->head_dim, dv);
+  FW_REQUIRE(p->kv_mode != FW_KV_PAGED || dv == p->head_dim, FW_ERR_VALUE,
+             "a paged pool has one head dim; got head_dim %d, head_dim_v %d", p->head_dim, dv);
+  FW_REQUIRE(!p->rotary_cos || (p->head_dim == 128 && dv == 128), FW_ERR_NOT_IMPLEMENTED,
+             "the fused RoPE takes head_dim 128; got %d/%d", p->head_dim, dv);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads=%d must be a multiple of nheads_k=%d", p->nheads, p->nheads_k);
   FW_REQUIRE(p->kv_mode >= FW_KV_DENSE && p->kv_mode <= FW_KV_PAGED, FW_ERR_VALUE,
@@ -1709,7 +1727,8 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * head_groups), p->kv_dtype, p->head_dim, s);
+    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * head_groups), p->kv_dtype, p->head_dim,
+                             dv, s);
     return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -1737,7 +1756,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (st != FW_OK) return st;
   // one workgroup per (schedule slot, head group); see sched_slot
   dim3 grid(max_tiles * head_groups);
-  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, p->head_dim, s);
-  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, s);
+  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, p->head_dim, dv, s);
+  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, dv, s);
   return check_launch("fw_prefill");
 }

@@ -68,6 +68,7 @@ class PrefillParams(ctypes.Structure):
         ("rotary_rows", _i32), ("rotary_f32", _i32), ("rotary_interleaved", _i32),
         ("seqused_k_excludes_q", _i32),
         ("k_descale_ptr", _c_p), ("v_descale_ptr", _c_p),
+        ("head_dim_v", _i32),
     ]
 
 

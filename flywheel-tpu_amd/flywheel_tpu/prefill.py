@@ -47,7 +47,7 @@ def _split_token_major(x, head_dim):
 
 def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads, nheads_k,
                  head_dim, seqlen_q, seqlen_k, causal, window_size, softmax_scale, softcap,
-                 sinks, cu_q=None, cu_k=None, max_seqlen_q=0, q_rotary=None):
+                 sinks, cu_q=None, cu_k=None, max_seqlen_q=0, q_rotary=None, head_dim_v=0):
     left, right = effective_window(causal, window_size)
     p = N.PrefillParams()
     p.kv_mode = mode
@@ -59,6 +59,7 @@ def _run_prefill(mode, q, k, v, out, lse, *, qs, ks, vs, os_, ls, batch, nheads,
     p.o_stride_b, p.o_stride_h, p.o_stride_t = os_
     p.lse_stride_b, p.lse_stride_h = ls
     p.batch, p.nheads, p.nheads_k, p.head_dim = batch, nheads, nheads_k, head_dim
+    p.head_dim_v = head_dim_v
     p.seqlen_q, p.seqlen_k, p.max_seqlen_q = seqlen_q, seqlen_k, max_seqlen_q
     p.kv_dtype = N.FW_BF16
     p.softmax_scale, p.softcap = softmax_scale, float(softcap)
@@ -102,10 +103,13 @@ def flash_attn_func(
 ):
     """flash_attn.flash_attn_func, `prefill.py:62-341`.
 
-    Head-major: q (batch, nheads, seqlen_q, d), k / v (batch, nheads_k,
-    seqlen_k, d), out like q; token-major (token_major=True): (batch, seqlen,
-    nheads * head_dim) with head_dim given; heads_outer_fold: (nheads, batch,
-    seqlen, d).  causal is bottom-right aligned: query i sees key j iff
+    Head-major: q (batch, nheads, seqlen_q, d), k (batch, nheads_k, seqlen_k,
+    d), v (batch, nheads_k, seqlen_k, dv), out (batch, nheads, seqlen_q, dv);
+    token-major (token_major=True): (batch, seqlen, nheads * head_dim) with
+    head_dim given (v's head dim from its width); heads_outer_fold: (nheads,
+    batch, seqlen, d).  d / dv: 64/64, 128/128, 256/256, 128/256 or 256/128
+    (inputs.py:154-207; token-major 64 is the reference's paired form: MHA
+    with an even head count, inputs.py:106-147).  causal is bottom-right aligned: query i sees key j iff
     j <= i + seqlen_k - seqlen_q.  Rows with no reachable key return out 0 and
     lse -inf (or the sink).  lse (batch, nheads, seqlen_q) f32.
 
@@ -140,15 +144,37 @@ def flash_attn_func(
             )
         if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
             raise ValueError(f"q/k/v ranks must be 3; got {q.shape=}, {k.shape=}, {v.shape=}.")
+        if type(head_dim) is not int:
+            raise ValueError(f"head_dim must be a static python int; got {head_dim!r}.")
+        if head_dim <= 0 or (head_dim % 128 and head_dim != 64):
+            raise ValueError("token-major inputs require head_dim % 128 == 0 or head_dim == 64"
+                             f" (paired); got {head_dim}.")
         batch, seqlen_q = q.shape[:2]
         seqlen_k = k.shape[1]
         nheads = _split_token_major(q, head_dim)
         nheads_k = _split_token_major(k, head_dim)
-        if v.shape[-1] != nheads_k * head_dim or v.shape[:2] != k.shape[:2]:
-            raise ValueError(f"v must be (batch, seqlen_k, {nheads_k * head_dim}); got {v.shape}.")
+        if v.shape[:2] != k.shape[:2] or v.shape[-1] % nheads_k:
+            raise ValueError(f"v fused width {v.shape[-1]} must be a multiple of nheads_k"
+                             f" {nheads_k}; got {tuple(v.shape)=}, {tuple(k.shape)=}.")
+        dv = v.shape[-1] // nheads_k
+        if dv % 128 and dv != 64:
+            raise ValueError("token-major requires head_dim_v % 128 == 0 or head_dim_v == 64"
+                             f" (paired); got {dv}.")
+        if head_dim % 128 or dv % 128:
+            if dv != head_dim:
+                raise NotImplementedError("token-major d64 requires head_dim_v == head_dim;"
+                                          f" got {head_dim} vs {dv}.")
+            if nheads_k != nheads:
+                raise NotImplementedError("token-major d64 is MHA-only; pass 4-D head-major"
+                                          " inputs instead.")
+            if nheads % 2:
+                raise ValueError(f"token-major d64 requires an even head count; got {nheads}.")
         d = head_dim
         qs = (seqlen_q * nheads * d, d, nheads * d)
         ks = (seqlen_k * nheads_k * d, d, nheads_k * d)
+        vs = (seqlen_k * nheads_k * dv, dv, nheads_k * dv)
+        os_ = (seqlen_q * nheads * dv, dv, nheads * dv)
+        out_shape = (batch, seqlen_q, nheads * dv)
     else:
         if head_dim is not None:
             raise ValueError("head_dim is only meaningful for token-major inputs.")
@@ -157,20 +183,33 @@ def flash_attn_func(
                 f"q/k/v must be 4-D head-major; got {tuple(q.shape)=}, {tuple(k.shape)=},"
                 f" {tuple(v.shape)=}."
             )
+        if q.shape[-1] != k.shape[-1]:
+            raise ValueError(f"Incompatible shapes: {tuple(q.shape)=} vs {tuple(k.shape)=}.")
+        # v may differ from k in head_dim only (inputs.py:201-207)
+        if k.shape[:-1] != v.shape[:-1]:
+            raise ValueError(f"k and v must share every axis but head_dim; got"
+                             f" {tuple(k.shape)=}, {tuple(v.shape)=}.")
+        dv = v.shape[-1]
         if heads_outer_fold:
             nheads, batch, seqlen_q, d = q.shape
             nheads_k, _, seqlen_k, _ = k.shape
             qs = (seqlen_q * d, batch * seqlen_q * d, d)
             ks = (seqlen_k * d, batch * seqlen_k * d, d)
+            vs = (seqlen_k * dv, batch * seqlen_k * dv, dv)
+            os_ = (seqlen_q * dv, batch * seqlen_q * dv, dv)
+            out_shape = (nheads, batch, seqlen_q, dv)
             kb = k.shape[1]
         else:
             batch, nheads, seqlen_q, d = q.shape
             _, nheads_k, seqlen_k, _ = k.shape
             qs = (nheads * seqlen_q * d, seqlen_q * d, d)
             ks = (nheads_k * seqlen_k * d, seqlen_k * d, d)
+            vs = (nheads_k * seqlen_k * dv, seqlen_k * dv, dv)
+            os_ = (nheads * seqlen_q * dv, seqlen_q * dv, dv)
+            out_shape = (batch, nheads, seqlen_q, dv)
             kb = k.shape[0]
-        if kb != batch or v.shape != k.shape or k.shape[-1] != d:
-            raise ValueError(f"k / v must match q's batch and head_dim; got {k.shape=}, {v.shape=}.")
+        if kb != batch:
+            raise ValueError(f"Incompatible shapes: {tuple(q.shape)=} vs {tuple(k.shape)=}.")
     if nheads_k <= 0 or nheads % nheads_k:
         raise ValueError(f"{nheads=} must be a multiple of {nheads_k=}.")
     tables = R.check_tables(rotary_cos, rotary_sin, head_dim=d, dtype=q.dtype,
@@ -192,14 +231,15 @@ def flash_attn_func(
             # rotated by the kernel as it loads it.
             k = R.rotate(k, tables, rotary_interleaved, strides=ks, batch_rows=batch,
                          nheads=nheads_k, ntokens=seqlen_k)
-        out = torch.empty_like(q)
+        out = q.new_empty(out_shape)
         lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if with_lse else None
-        _run_prefill(N.FW_KV_DENSE, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+        _run_prefill(N.FW_KV_DENSE, q, k, v, out, lse, qs=qs, ks=ks, vs=vs, os_=os_,
                      ls=(nheads * seqlen_q, seqlen_q), batch=batch, nheads=nheads,
                      nheads_k=nheads_k, head_dim=d, seqlen_q=seqlen_q, seqlen_k=seqlen_k,
                      causal=causal, window_size=window_size, softmax_scale=softmax_scale,
                      softcap=softcap, sinks=sinks,
-                     q_rotary=None if tables is None else (tables, rotary_interleaved))
+                     q_rotary=None if tables is None else (tables, rotary_interleaved),
+                     head_dim_v=dv)
         return out, lse
 
     if not grad:
@@ -215,7 +255,8 @@ def flash_attn_func(
         else:
             unsupported = ("window_size" if window_size != (-1, -1) else
                            "softcap" if softcap != 0.0 else
-                           f"head_dim {d}" if d != 128 else None)
+                           f"head_dim {d}" if d != 128 else
+                           f"head_dim_v {dv}" if dv != 128 else None)
             if unsupported:
                 reason = (f"The backward kernel does not support {unsupported}; that"
                           " configuration is forward-only.")
@@ -269,8 +310,9 @@ def flash_attn_varlen_func(
 ):
     """flash_attn.flash_attn_varlen_func for packed sequences, `prefill.py:664-963`.
 
-    Packed K/V: q (nheads, total_q, d), k / v (nheads_k, total_k, d) with
-    cu_seqlens_q / cu_seqlens_k (token-major: (total, nheads * head_dim)).
+    Packed K/V: q (nheads, total_q, d), k (nheads_k, total_k, d), v
+    (nheads_k, total_k, dv), out (nheads, total_q, dv), with cu_seqlens_q /
+    cu_seqlens_k (token-major: (total, nheads * head_dim)).
     Paged KV cache (block_table given, read-only): k is the merged pool, v None,
     cu_seqlens_k None, seqused_k (batch,) each sequence's kv length.  Padding q
     rows return out 0, lse -inf; lse is (nheads, total_q).  block_sizes and
@@ -414,9 +456,15 @@ def flash_attn_varlen_func(
         total_q, total_k = q.shape[0], k.shape[0]
         nheads = _split_token_major(q, head_dim)
         nkv = _split_token_major(k, head_dim)
-        d = head_dim
+        if v.shape[0] != total_k or v.shape[-1] % nkv:
+            raise ValueError(f"v fused width {v.shape[-1]} must be a multiple of nheads_k {nkv};"
+                             f" got {tuple(v.shape)=}, {tuple(k.shape)=}.")
+        d, dv = head_dim, v.shape[-1] // nkv
         qs = (0, d, nheads * d)
         ks = (0, d, nkv * d)
+        vs = (0, dv, nkv * dv)
+        os_ = (0, dv, nheads * dv)
+        out_shape = (total_q, nheads * dv)
     else:
         if head_dim is not None:
             raise ValueError("head_dim is only meaningful for token-major inputs.")
@@ -424,10 +472,15 @@ def flash_attn_varlen_func(
             raise ValueError(f"q/k/v must be (heads, total, d); got {q.shape=}, {k.shape=}.")
         nheads, total_q, d = q.shape
         nkv, total_k, _ = k.shape
+        if q.shape[-1] != k.shape[-1] or k.shape[:-1] != v.shape[:-1]:
+            raise ValueError("k and v must share every axis but head_dim, and q and k their"
+                             f" head_dim; got {tuple(q.shape)=}, {tuple(k.shape)=}, {tuple(v.shape)=}.")
+        dv = v.shape[-1]
         qs = (0, total_q * d, d)
         ks = (0, total_k * d, d)
-    if tuple(v.shape) != tuple(k.shape):
-        raise ValueError(f"v must match k's shape; got {k.shape=}, {v.shape=}.")
+        vs = (0, total_k * dv, dv)
+        os_ = (0, total_q * dv, dv)
+        out_shape = (nheads, total_q, dv)
     if nkv <= 0 or nheads % nkv:
         raise ValueError(f"{nheads=} must be a multiple of nheads_k={nkv}.")
     tables = R.check_tables(rotary_cos, rotary_sin, head_dim=d, dtype=q.dtype,
@@ -450,16 +503,17 @@ def flash_attn_varlen_func(
     sinks = check_sinks(learnable_sink, nheads, device)
 
     def run_packed(q, k, v):
-        out = torch.empty_like(q)
+        out = q.new_empty(out_shape)
         lse = (torch.empty((nheads, total_q), dtype=torch.float32, device=device)
                if return_softmax_lse else None)
-        _run_prefill(N.FW_KV_VARLEN, q, k, v, out, lse, qs=qs, ks=ks, vs=ks, os_=qs,
+        _run_prefill(N.FW_KV_VARLEN, q, k, v, out, lse, qs=qs, ks=ks, vs=vs, os_=os_,
                      ls=(0, total_q), batch=batch, nheads=nheads, nheads_k=nkv, head_dim=d,
                      seqlen_q=total_q, seqlen_k=total_k, causal=causal,
                      window_size=window_size, softmax_scale=resolve_scale(softmax_scale, d),
                      softcap=softcap, sinks=sinks, cu_q=cu_q_dev, cu_k=cu_k_dev,
                      max_seqlen_q=int(max_seqlen_q),
-                     q_rotary=None if tables is None else (tables, rotary_interleaved))
+                     q_rotary=None if tables is None else (tables, rotary_interleaved),
+                     head_dim_v=dv)
         return out, lse
 
     if grad:

@@ -169,7 +169,8 @@ int fw_write_kv_cache_pages(const void *k, const void *v, void *kv_cache,
  *
  * q / out addressed as base + b*stride_b + h*stride_h + t*stride_t (elements,
  * bf16); for varlen modes b is 0 and t the packed token index.
- * Dense:   k / v (batch, nheads_k, seqlen_k, head_dim) with strides.
+ * Dense:   k (batch, nheads_k, seqlen_k, head_dim), v (..., head_dim_v) with
+ *          strides; q is (..., head_dim), out (..., head_dim_v).
  * Varlen:  k / v packed by cu_seqlens_k, same stride convention (b = 0).
  * Paged:   k = merged pool, v = NULL; seqused_k (batch,) gives each
  *          sequence's kv length; block_table (batch, max_pages).
@@ -223,6 +224,11 @@ typedef struct fw_prefill_params {
   /* Device f32 descale scalars, or NULL; as in fw_decode_params. */
   const float *k_descale_ptr;
   const float *v_descale_ptr;
+  /* Head dim of v and out, 0 = head_dim (prefill.py's head_dim_v,
+   * inputs.py:193-207).  head_dim / head_dim_v: 64/64, 128/128, 256/256,
+   * 128/256 or 256/128; a paged pool has one head dim; the fused RoPE takes
+   * 128/128. */
+  int32_t head_dim_v;
 } fw_prefill_params;
 
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);

@@ -290,20 +290,21 @@ def test_contiguous_cache_num_active_softcap():
     assert_lse(lse[:2], rl[:2])
 
 
+@pytest.mark.parametrize("hd", [256, 64])
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
 @pytest.mark.parametrize("seqlen_q", [1, 4])
-def test_decode_head_dim_256(dtype, seqlen_q):
-    """head_dim 256 (the reference's DECODE_HEAD_DIMS, traits.py:50): single
-    token with the fused append, and a causal 4-token verify window."""
-    announce(f"decode d256 {dtype} seqlen_q={seqlen_q}")
+def test_decode_head_dims(dtype, seqlen_q, hd):
+    """head_dim 256 and 64 (the reference's DECODE_HEAD_DIMS, traits.py:50):
+    single token with the fused append, and a causal 4-token verify window."""
+    announce(f"decode d{hd} {dtype} seqlen_q={seqlen_q}")
     rng = np.random.default_rng(60)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
     ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.8, 1.3)
     lengths = [0, 17, 1000, 5000, 129]
     b = len(lengths)
     case = PagedCase(rng, batch=b, nheads=16, nheads_k=4, lengths=lengths,
-                     new_tokens=[seqlen_q] * b, head_dim=256, dtype=dt, k_descale=ks, v_descale=vs)
-    q = randn(rng, (b, seqlen_q, 16, 256))
+                     new_tokens=[seqlen_q] * b, head_dim=hd, dtype=dt, k_descale=ks, v_descale=vs)
+    q = randn(rng, (b, seqlen_q, 16, hd))
     out, lse, pool = run_decode(case, q, causal=seqlen_q > 1)
     exp_pool = case.expected_pool()
     np.testing.assert_array_equal(codes_of(pool), exp_pool)

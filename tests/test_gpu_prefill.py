@@ -241,6 +241,12 @@ def test_prefill_bitwise_repeat():
 # (docs/v7x.md:49-60, 157-169).
 
 
+# Head dims of q/k and v: the d256 kernel, the register-staged kernel at 64 and
+# with head_dim_v != head_dim (inputs.py:193-207).
+HEAD_DIMS = [(256, 256), (64, 64), (128, 256), (256, 128)]
+
+
+@pytest.mark.parametrize("d,dv", HEAD_DIMS)
 @pytest.mark.parametrize(
     "b,h,hk,sq,sk,causal,window,softcap",
     [
@@ -251,10 +257,10 @@ def test_prefill_bitwise_repeat():
         (1, 8, 1, 384, 384, True, (100, -1), 30.0),
     ],
 )
-def test_flash_attn_func_d256(b, h, hk, sq, sk, causal, window, softcap):
-    announce(f"dense d256 b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window}")
+def test_flash_attn_func_head_dims(d, dv, b, h, hk, sq, sk, causal, window, softcap):
+    announce(f"dense d{d}/{dv} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window}")
     rng = np.random.default_rng(70)
-    q, k, v = randn(rng, (b, sq, h, 256)), randn(rng, (b, sk, hk, 256)), randn(rng, (b, sk, hk, 256))
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, dv))
     out, lse = flash_attn_func(
         to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)), to_dev_bf16(head_major(v)),
         causal=causal, window_size=window, softcap=softcap, return_softmax_lse=True)
@@ -265,16 +271,32 @@ def test_flash_attn_func_d256(b, h, hk, sq, sk, causal, window, softcap):
     assert_lse(lse.cpu().numpy(), rl)
 
 
-def test_flash_attn_varlen_d256():
-    announce("varlen packed d256")
+def test_flash_attn_func_token_major_paired_d64():
+    """Token-major head_dim 64 (the reference's paired form: MHA, even head
+    count, inputs.py:106-147)."""
+    announce("dense token-major d64")
+    rng = np.random.default_rng(73)
+    b, h, s, d = 2, 6, 300, 64
+    q, k, v = randn(rng, (b, s, h, d)), randn(rng, (b, s, h, d)), randn(rng, (b, s, h, d))
+    out = flash_attn_func(to_dev_bf16(q.reshape(b, s, h * d)), to_dev_bf16(k.reshape(b, s, h * d)),
+                          to_dev_bf16(v.reshape(b, s, h * d)), causal=True, head_dim=d,
+                          token_major=True)
+    torch.cuda.synchronize()
+    ro, _ = A.attention_ref(q, k, v, causal=True, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy().reshape(b, s, h, d), ro)
+
+
+@pytest.mark.parametrize("d,dv", HEAD_DIMS)
+def test_flash_attn_varlen_head_dims(d, dv):
+    announce(f"varlen packed d{d}/{dv}")
     rng = np.random.default_rng(71)
     qlens, klens = [1, 130, 77, 256], [1, 200, 77, 300]
-    h, hk, d = 4, 2, 256
+    h, hk = 4, 2
     cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
     cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
     q = randn(rng, (h, cu_q[-1] + 5, d))
     k = randn(rng, (hk, cu_k[-1], d))
-    v = randn(rng, (hk, cu_k[-1], d))
+    v = randn(rng, (hk, cu_k[-1], dv))
     out, lse = flash_attn_varlen_func(
         to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), torch.tensor(cu_q, device=DEV),
         torch.tensor(cu_k, device=DEV), max(qlens), max(klens), causal=True,
@@ -291,20 +313,21 @@ def test_flash_attn_varlen_d256():
     assert not outs[:, cu_q[-1]:].any()
 
 
+@pytest.mark.parametrize("hd", [256, 64])
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
-def test_chunked_prefill_kvcache_d256(dtype):
+def test_chunked_prefill_kvcache_head_dims(dtype, hd):
     """The chunked-prefill call (append + paged varlen, window, softcap,
-    num_active) at head_dim 256."""
-    announce(f"chunked prefill d256 {dtype}")
+    num_active) at head_dim 256 and 64."""
+    announce(f"chunked prefill d{hd} {dtype}")
     rng = np.random.default_rng(72)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
     ks, vs = (1.0, 1.0) if dtype == "bf16" else (1.5, 0.7)
     chunks = [256, 300, 1, 129]
     prior = [0, 1000, 17, 500]
     case = PagedCase(rng, batch=4, nheads=8, nheads_k=2, lengths=prior, new_tokens=chunks,
-                     head_dim=256, dtype=dt, k_descale=ks, v_descale=vs)
+                     head_dim=hd, dtype=dt, k_descale=ks, v_descale=vs)
     cu = case.cu
-    q = randn(rng, (cu[-1], 8, 256))
+    q = randn(rng, (cu[-1], 8, hd))
     pool = case.pool()
     out, lse, pool2 = flash_attn_with_kvcache(
         to_dev_bf16(q), pool, None, dev_from_codes(case.k_codes, dt),

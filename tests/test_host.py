@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} is declared but not exported"
     assert set(names) == set(N.SIGNATURES), "ctypes bindings and header disagree"
-    assert lib.fw_abi_version() == 5
+    assert lib.fw_abi_version() == 6
 
 
 def test_struct_layouts_match_header_fields():
@@ -95,7 +95,7 @@ def test_struct_offsets_and_widths_match_c(tmp_path):
 def test_capi_validation_status_codes():
     lib = N.lib()
     p = N.DecodeParams()
-    p.batch, p.seqlen_q, p.nheads, p.nheads_k, p.head_dim = 2, 1, 8, 2, 64
+    p.batch, p.seqlen_q, p.nheads, p.nheads_k, p.head_dim = 2, 1, 8, 2, 96
     p.page_size, p.max_pages, p.num_pages = 16, 4, 8
     assert lib.fw_paged_decode_workspace_bytes(p) == 0
     assert lib.fw_paged_decode(p, None) == N.FW_ERR_NOT_IMPLEMENTED
@@ -110,6 +110,11 @@ def test_capi_validation_status_codes():
     q = N.PrefillParams()
     q.kv_mode, q.head_dim, q.nheads, q.nheads_k = N.FW_KV_DENSE, 96, 4, 2
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
+    q.head_dim, q.head_dim_v = 64, 128  # d64 takes head_dim_v 64 only
+    assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
+    q.head_dim, q.head_dim_v, q.kv_mode = 128, 256, N.FW_KV_PAGED  # one head dim in a pool
+    assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE
+    q.kv_mode, q.head_dim_v = N.FW_KV_DENSE, 0
     q.head_dim, q.kv_dtype = 128, N.FW_FP8_E4M3
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED  # fp8 only for a paged pool
     assert lib.fw_append_ragged(None, None, None, None, None, None, None, 1, 0, 2, 128, 16, 1, 1,
@@ -157,6 +162,18 @@ def test_flash_attn_func_errors():
         flash_attn_func(q.float(), k.float(), k.float())
     with pytest.raises(ValueError):
         flash_attn_func(bf(1, 8, 512), bf(1, 8, 256), bf(1, 8, 256), token_major=True)
+    # inputs.py:106-147: token-major head dims, the paired d64 form
+    with pytest.raises(ValueError, match="head_dim % 128"):
+        flash_attn_func(bf(1, 8, 384), bf(1, 8, 384), bf(1, 8, 384), token_major=True, head_dim=96)
+    with pytest.raises(NotImplementedError, match="MHA"):
+        flash_attn_func(bf(1, 8, 256), bf(1, 8, 128), bf(1, 8, 128), token_major=True, head_dim=64)
+    with pytest.raises(NotImplementedError, match="head_dim_v == head_dim"):
+        flash_attn_func(bf(1, 8, 256), bf(1, 8, 256), bf(1, 8, 512), token_major=True, head_dim=64)
+    with pytest.raises(ValueError, match="even head count"):
+        flash_attn_func(bf(1, 8, 192), bf(1, 8, 192), bf(1, 8, 192), token_major=True, head_dim=64)
+    # inputs.py:193-207: v differs from k in head_dim only
+    with pytest.raises(ValueError, match="every axis but head_dim"):
+        flash_attn_func(q, k, bf(1, 2, 9, 128))
     with pytest.raises(TypeError):
         flash_attn_func(q, k, k, heads_outer_fold=1)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
