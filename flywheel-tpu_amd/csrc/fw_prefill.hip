@@ -17,6 +17,7 @@
 //   O^T (32 dims x 32 rows) += V^T x P^T     (P^T = the S^T registers, bf16)
 // with v_mfma_f32_32x32x16_bf16 over 64-key tiles staged through LDS.
 #include "fw_common.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace fw {
@@ -1541,28 +1542,19 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
     }
   }
   if (sort) {
-    int n = 1;
-    while (n < real) n <<= 1;
-    for (int i = real + tid; i < n; i += nt) key[i] = 0;  // below every real key
+    // Rank sort, descending: a tile's slot is the number of larger keys (keys
+    // are distinct: the low word is the tile's index).  Every thread reads
+    // the same key at the same time (an LDS broadcast), so one pass over the
+    // keys replaces the log^2 barrier-separated stages of a sorting network.
     __syncthreads();
-    for (int k = 2; k <= n; k <<= 1)  // bitonic sort, descending
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < n; i += nt) {
-          const int ixj = i ^ j;
-          if (ixj > i) {
-            const unsigned long long x = key[i], y = key[ixj];
-            if ((i & k) == 0 ? x < y : x > y) {
-              key[i] = y;
-              key[ixj] = x;
-            }
-          }
-        }
-        __syncthreads();
+    for (int i = tid; i < real; i += nt) {
+      const unsigned long long x = key[i];
+      int rank = 0;
+      for (int j = 0; j < real; ++j) rank += key[j] > x;
+      if (rank < max_tiles) {
+        sched[1 + 2 * rank] = eseq[i];
+        sched[2 + 2 * rank] = eq0[i];
       }
-    for (int i = tid; i < real && i < max_tiles; i += nt) {
-      const int e = (int)(unsigned)(key[i] & 0xffffffffu) - 1;
-      sched[1 + 2 * i] = eseq[e];
-      sched[2 + 2 * i] = eq0[e];
     }
   }
   const int pad0 = nact > 0 ? cu_q[nact] : 0;
@@ -1744,9 +1736,11 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);
   const bool varlen = p->kv_mode == FW_KV_VARLEN;
-  // one wave per 64 sequences (at most 16): fewer waves, cheaper barriers
+  // a thread per sequence and per q tile (up to 1024): the rank sort's pass
   int sched_threads = 64;
-  while (sched_threads < 1024 && sched_threads < p->batch) sched_threads <<= 1;
+  while (sched_threads < 1024 &&
+         (sched_threads < p->batch || sched_threads < std::min(max_tiles, kSortTiles)))
+    sched_threads <<= 1;
   fw_prefill_schedule<<<1, sched_threads, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
                                          (int32_t *)p->workspace, max_tiles, qt_rows,
                                          varlen ? p->cu_seqlens_k : nullptr,
