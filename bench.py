@@ -430,6 +430,23 @@ def workload_copy(args, device):
                 cpu=None)
 
 
+def workload_gemm(args, device):
+    """Reference, not this library: torch.matmul (hipBLASLt) of two 8192 x 8192
+    bf16 matrices, the rate dense MFMA work reaches on the same box and clock
+    (the prefill kernels' practical ceiling, below the 2.5 PFLOP/s peak)."""
+    n = 8192
+    a = torch.randn((n, n), device=device, dtype=torch.bfloat16)
+    b = torch.randn((n, n), device=device, dtype=torch.bfloat16)
+    ms = timed(lambda: a @ b, args.steps, args.warmup)
+    tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    return dict(name="gemm", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+                config={"workload": "reference: torch.matmul bf16 8192^3 (hipBLASLt)"},
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                          "traffic": None},
+                cpu=None)
+
+
 def _c2_inputs(device):
     b, h, hk, s, d = 1, 32, 4, 4096, 128
     gen = torch.Generator(device=device).manual_seed(0)
@@ -555,7 +572,7 @@ def workload_dec256(args, device):
 
 
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
-EXTRA = {"copy": workload_copy, "bwd": workload_bwd, "rope": workload_rope,
+EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "bwd": workload_bwd, "rope": workload_rope,
          "c2d256": workload_c2d256, "dec256": workload_dec256,
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 

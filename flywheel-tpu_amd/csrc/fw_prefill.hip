@@ -703,7 +703,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // Paged: a page id outside [0, num_pages) is never dereferenced: its keys
   // read as zero K and V rows.  The wave still issues its four copies (the
   // vmcnt waits count them), all from the zero row kZeroKV.
-  auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
+  struct CopyPlan {
+    const uint8_t *kp, *vp;
+    uint32_t ka, va, kb, vb, d;
+  };
+  auto copy_plan = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
     const int kmax = sk_len - 1;
     int key0 = min((t_begin + j) * kKT + 8 * wv, kmax);
     const uint8_t *kp, *vp;
@@ -722,10 +726,20 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     const uint32_t lra = min(lr0, lim), lrb = min(lr0 + 4u, lim);
     const uint32_t c16a = c16b ^ (16u * ((2 * wv) & 3)), c16c = c16b ^ (16u * ((2 * wv + 1) & 3));
     const uint32_t d = lds0 + (uint32_t)(8 * wv * kRowB) + (uint32_t)buf * kTileB;
-    lds_dma16(kp, __umul24(lra, kstB) + c16a, d);
-    lds_dma16(vp, __umul24(lra, vstB) + c16a, d + 4 * kTileB);
-    lds_dma16(kp, __umul24(lrb, kstB) + c16c, d + 4 * kRowB);
-    lds_dma16(vp, __umul24(lrb, vstB) + c16c, d + 4 * kRowB + 4 * kTileB);
+    return CopyPlan{kp, vp, __umul24(lra, kstB) + c16a, __umul24(lra, vstB) + c16a,
+                    __umul24(lrb, kstB) + c16c, __umul24(lrb, vstB) + c16c, d};
+  };
+  // Copy i (0-3) of a plan: K rows 0-3, V rows 0-3, K rows 4-7, V rows 4-7.
+  auto copy_issue = [&](const CopyPlan &c, const int i) __attribute__((always_inline)) {
+    if (i == 0) lds_dma16(c.kp, c.ka, c.d);
+    if (i == 1) lds_dma16(c.vp, c.va, c.d + 4 * kTileB);
+    if (i == 2) lds_dma16(c.kp, c.kb, c.d + 4 * kRowB);
+    if (i == 3) lds_dma16(c.vp, c.vb, c.d + 4 * kRowB + 4 * kTileB);
+  };
+  auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
+    const CopyPlan c = copy_plan(j, buf, wv, page);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) copy_issue(c, i);
   };
   auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
     int page = 0;
