@@ -570,8 +570,13 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
                :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
 }
 
-template <int MODE, bool SOFTCAP>
+template <int MODE, bool SOFTCAP, int KV = FW_BF16>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
+  // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile j+2 into
+  // registers in its softmax slot of tile j, and widens them to bf16 into the
+  // tile's LDS buffer at the end of its next MFMA slot, where it would
+  // otherwise wait at the barrier; the rest is the bf16 kernel.
+  constexpr bool kFp8 = KV != FW_BF16;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kPPBuf];
 
   const int tid = threadIdx.x;
@@ -746,8 +751,48 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     if constexpr (MODE == FW_KV_PAGED) page = *table_entry(j, wv);
     dma_tile_pg(j, buf, wv, page);
   };
+  // fp8: this wave's 8 key rows of tile j, lane l holding row l/8, dims
+  // 16(l%8) .. +15 of K and of V (an invalid page id reads the zero rows).
+  struct Fp8Rows {
+    u32x4_t k, v;
+  };
+  auto fp8_load = [&](int j, int page) __attribute__((always_inline)) {
+    const int kmax = sk_len - 1;
+    const int key0 = min((t_begin + j) * kKT + 8 * w, kmax) & ~7;
+    const bool bad = page < 0 || page >= a.num_pages;
+    const uint32_t lim = bad ? 0u : (uint32_t)(kmax - key0);
+    const uint32_t r = min((uint32_t)lane >> 3, lim);
+    const uint8_t *kp =
+        bad ? kZeroKV
+            : a.k + (((size_t)page * a.P + key0 % a.P) * a.CH + 2 * hk) * 128 +
+                  (size_t)r * a.CH * 128;
+    kp += 16 * (lane & 7);
+    return Fp8Rows{*(const u32x4_t *)kp, *(const u32x4_t *)(kp + 128)};
+  };
+  // ... widened to bf16 into LDS buffer buf (the swizzled bf16 row layout)
+  auto fp8_store = [&](const Fp8Rows &f, const int buf) __attribute__((always_inline)) {
+    const int r = 8 * w + (lane >> 3);
+    const int c = lane & 7;
+    const uint32_t rowb = lds0 + (uint32_t)buf * kTileB + (uint32_t)r * kRowB;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const u32x4_t x = kv ? f.v : f.k;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x4_t o = {fp8x2_to_bf16x2<KV>(x[2 * hh], false), fp8x2_to_bf16x2<KV>(x[2 * hh], true),
+                           fp8x2_to_bf16x2<KV>(x[2 * hh + 1], false),
+                           fp8x2_to_bf16x2<KV>(x[2 * hh + 1], true)};
+        *(FW_LDS u32x4_t *)(rowb + 4u * kTileB * kv + 16u * ((2 * c + hh) ^ swz(r))) = o;
+      }
+    }
+  };
+  Fp8Rows fr{};  // fp8: rows loaded in a softmax slot, stored in the next MFMA slot
   // Tile 0's copy goes out before the Q loads so the two latencies overlap.
-  if (T > 0) dma_tile(0, 0, w);
+  if constexpr (kFp8) {
+    if (T > 0) fr = fp8_load(0, *table_entry(0, w));
+  } else {
+    if (T > 0) dma_tile(0, 0, w);
+  }
 
   // ------------------------------------------------------------ Q^T operand
   bf16x8_t qop[8];
@@ -988,7 +1033,11 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     if constexpr (MODE == FW_KV_PAGED) {
       if (T > 2) page_next = table_sload(2, w);  // complete at the barrier below
     }
-    if (T > 1) {
+    if constexpr (kFp8) {
+      const Fp8Rows f1 = T > 1 ? fp8_load(1, *table_entry(1, w)) : Fp8Rows{};
+      fp8_store(fr, 0);
+      if (T > 1) fp8_store(f1, 1);
+    } else if (T > 1) {
       dma_tile(1, 1, w);
       asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
@@ -1027,7 +1076,15 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       // complete since before this slot and is not rewritten until tile j+4)
       mslot_pre(B);
       __builtin_amdgcn_s_setprio(0);
-      if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if constexpr (kFp8) {
+        // tile j+1's rows, loaded in the previous softmax slot
+        if (j + 1 < T && j >= 1) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          fp8_store(fr, (B + 1) % 4);
+        }
+      } else {
+        if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
       slot_barrier();
       const bool copy = j + 2 < T;
       if (copy) {
@@ -1035,13 +1092,14 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
         // compiler cannot see: it is complete at the lgkmcnt(0) of the
         // barrier above, and this wait ties its use to after that point.
         asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(page_next));
-        dma_tile_pg(j + 2, (B + 2) % 4, w, page_next);
+        if constexpr (kFp8) fr = fp8_load(j + 2, page_next);
+        else dma_tile_pg(j + 2, (B + 2) % 4, w, page_next);
         if constexpr (MODE == FW_KV_PAGED) {
           if (j + 3 < T) page_next = table_sload(j + 3, w);  // for the next body
         }
       }
       if (j < T) softmax(t_begin + j, pops);
-      if (grp == 0) {
+      if (!kFp8 && grp == 0) {
         if (copy) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // tile j+1 in
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
@@ -1586,15 +1644,15 @@ static int max_sched_tiles(const fw_prefill_params *p, int qt) {
   return 2 * ((p->seqlen_q + qt - 1) / qt) + p->batch + 1;
 }
 
-// Kernel choice: bf16 K/V at head_dim 128 -> ping-pong kernel (256-row
-// tiles; the softcap variant is 3% faster on C4's shape than a 4-wave,
-// two-per-CU kernel that ran the tanh beside its own MFMAs); bf16 at 256 ->
-// the one-wave-per-SIMD d256 kernel; fp8 pools -> register-staged kernel.
+// The ping-pong kernel takes head dim 128 (bf16, or an fp8 pool); its softcap
+// variant is 3% faster on C4's shape than a 4-wave, two-per-CU kernel that ran
+// the tanh beside its own MFMAs.
 static int head_dim_v_of(const fw_prefill_params *p) {
   return p->head_dim_v > 0 ? p->head_dim_v : p->head_dim;
 }
 static bool use_pingpong(const fw_prefill_params *p) {
-  return p->kv_dtype == FW_BF16 && p->head_dim == 128 && head_dim_v_of(p) == 128;
+  return (p->kv_dtype == FW_BF16 || p->kv_mode == FW_KV_PAGED) && p->head_dim == 128 &&
+         head_dim_v_of(p) == 128;
 }
 
 // log2 of the query heads per ping-pong workgroup: the largest power of two
@@ -1621,9 +1679,10 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
                   256);
 }
 
-// Kernel choice (the host has checked the head dims): bf16 128/128 -> the
-// ping-pong kernel, bf16 256/256 -> the d256 kernel, everything else (fp8
-// pools, head dim 64, head_dim_v != head_dim) -> the register-staged kernel.
+// Kernel choice (the host has checked the head dims): 128/128 -> the ping-pong
+// kernel (fp8 pools widened as they land in LDS), bf16 256/256 -> the d256
+// kernel, everything else (head dim 64, head_dim_v != head_dim, fp8 at 64 and
+// 256) -> the register-staged kernel.
 template <int MODE, int KV, int D, int DV>
 static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
   fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
@@ -1649,9 +1708,14 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
   if constexpr (MODE == FW_KV_PAGED) {  // fp8: paged pools only, one head dim
     auto run = [&](auto kv) {
       constexpr int KV = decltype(kv)::value;
-      if (d == 64) launch_staged<MODE, KV, 64, 64>(a, grid, s);
-      else if (d == 256) launch_staged<MODE, KV, 256, 256>(a, grid, s);
-      else launch_staged<MODE, KV, 128, 128>(a, grid, s);
+      if (d == 64) {
+        launch_staged<MODE, KV, 64, 64>(a, grid, s);
+      } else if (d == 256) {
+        launch_staged<MODE, KV, 256, 256>(a, grid, s);
+      } else {
+        if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true, KV><<<grid, 512, 0, s>>>(a);
+        else fw_prefill_pp_kernel<MODE, false, KV><<<grid, 512, 0, s>>>(a);
+      }
     };
     if (kv_dtype == FW_FP8_E4M3) run(std::integral_constant<int, FW_FP8_E4M3>());
     else run(std::integral_constant<int, FW_FP8_E5M2>());
