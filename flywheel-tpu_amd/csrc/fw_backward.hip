@@ -95,6 +95,20 @@ __device__ __forceinline__ bf16x8_t tr_operand(const uint16_t *T, int r, int u, 
   return __builtin_bit_cast(bf16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
 }
 
+// The same operand read from a row-major tile R (stride kBS) with two
+// transposing reads: within each 16-lane group, lane 4a + b addresses row
+// K0 + a, dims D0 + 4b .. + 3, and receives dim D0 + (lane % 16) of rows
+// K0 .. K0 + 3 (K0 = 16u + 4g, then 16u + 8 + 4g; D0 = r - lane % 16).
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+#define FW_LDS __attribute__((address_space(3)))
+__device__ __forceinline__ bf16x8_t tr_operand_rm(uint32_t Rb, int c, int u, int lane) {
+  const int g = lane >> 5, grp = lane >> 4, i = lane & 15;
+  const uint32_t o = Rb + 2u * ((16 * u + 4 * g + (i >> 2)) * kBS + 32 * c + 16 * (grp & 1) + 4 * (i & 3));
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)o);
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(o + 16u * kBS));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Stores rows 2(sr+16p) and 2(sr+16p)+1 (p = 0, 1), dims 8sc .. 8sc+7, of a
 // 64-row tile held in x[2p], x[2p+1]: row-major into R (optional) and
 // transposed, rows in pairs, into T (optional).
@@ -124,12 +138,15 @@ __device__ __forceinline__ void store_pairs(uint16_t *R, uint16_t *T, const u32x
 // query tiles that can see its keys.
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kRowTileB + 2 * kTrTileB + 2 * kBT * 4];
+  // q_s rows, dout rows and raw q rows; the transposed operands of dV and dK
+  // come from the dout and raw q rows by transposing reads
+  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * kRowTileB + 2 * kBT * 4];
   uint16_t *Qs = (uint16_t *)smem;                            // q_s rows
   uint16_t *Ds = (uint16_t *)(smem + kRowTileB);              // dout rows
-  uint16_t *Qt = (uint16_t *)(smem + 2 * kRowTileB);          // q^T (raw)
-  uint16_t *Dt = (uint16_t *)(smem + 2 * kRowTileB + kTrTileB);  // dout^T
-  float *Ls = (float *)(smem + 2 * kRowTileB + 2 * kTrTileB);   // lse_log2
+  uint16_t *Qr = (uint16_t *)(smem + 2 * kRowTileB);          // q rows (raw)
+  float *Ls = (float *)(smem + 3 * kRowTileB);                // lse_log2
+  const uint32_t lds_ds = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)(smem + kRowTileB);
+  const uint32_t lds_qr = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)(smem + 2 * kRowTileB);
   float *Dl = Ls + kBT;                                         // delta
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
@@ -200,8 +217,8 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qsx[i] = scale_words(qx[i], a.qscale);
         store_pairs(Qs, nullptr, qsx, sr, sc);
-        store_pairs(nullptr, Qt, qx, sr, sc);
-        store_pairs(Ds, Dt, dx, sr, sc);
+        store_pairs(Qr, nullptr, qx, sr, sc);
+        store_pairs(Ds, nullptr, dx, sr, sc);
         if (tid < kBT) {
           Ls[tid] = lx;
           Dl[tid] = dl;
@@ -274,8 +291,8 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
           const int u = 2 * st + uu;
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            dvacc[c] = mfma32(tr_operand(Dt, n + 32 * c, u, g), pop[uu], dvacc[c]);
-            dkacc[c] = mfma32(tr_operand(Qt, n + 32 * c, u, g), dsop[uu], dkacc[c]);
+            dvacc[c] = mfma32(tr_operand_rm(lds_ds, c, u, lane), pop[uu], dvacc[c]);
+            dkacc[c] = mfma32(tr_operand_rm(lds_qr, c, u, lane), dsop[uu], dkacc[c]);
           }
         }
       }
