@@ -156,26 +156,29 @@ def test_flash_attn_varlen_many_sequences(nseq):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3", "e5m2"])
-def test_paged_varlen_read_only(dtype):
+@pytest.mark.parametrize("h,hk", [(4, 2), (8, 1), (16, 2), (6, 3)])
+def test_paged_varlen_read_only(dtype, h, hk):
     """flash_attn_varlen_func(block_table=...) over a merged pool; reference
-    edge case random_ragged_case lengths (3, 0, 5) on prefixes (127, 0, 251)."""
-    announce(f"paged varlen {dtype}")
+    edge case random_ragged_case lengths (3, 0, 5) on prefixes (127, 0, 251).
+    Heads: 2 or 8 query heads per KV head (one workgroup serves 2 or 8), and
+    an odd KV head count (the fp8 pool's zero pad head)."""
+    announce(f"paged varlen {dtype} h{h}/{hk}")
     rng = np.random.default_rng(14)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
     ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.5, 2.0)
     qlens = [3, 0, 5, 200]
     prefix = [127, 0, 251, 1000]
     totals = np.array(qlens) + np.array(prefix)
-    case = PagedCase(rng, batch=4, nheads=4, nheads_k=2, lengths=totals, new_tokens=[0] * 4,
+    case = PagedCase(rng, batch=4, nheads=h, nheads_k=hk, lengths=totals, new_tokens=[0] * 4,
                      dtype=dt, k_descale=ks, v_descale=vs)
     cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
-    q = randn(rng, (cu[-1] + 7, 4, 128))
+    q = randn(rng, (cu[-1] + 7, h, 128))
     out, lse = flash_attn_varlen_func(
         to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
         torch.tensor(cu, device=DEV), None, max(qlens), int(totals.max()), causal=True,
         return_softmax_lse=True, block_table=torch.tensor(case.table, device=DEV),
         seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), k_descale=ks,
-        v_descale=vs, nheads_k=2)
+        v_descale=vs, nheads_k=hk)
     torch.cuda.synchronize()
     kp, vp = case.kv_pages(case.pool_codes)
     ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True, k_descale=ks,
