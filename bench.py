@@ -529,6 +529,7 @@ def workload_c2d256(args, device):
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(
         name="c2d256", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        vs_baseline=round(tflops / 653.0, 3),
         config={"workload": "flash_attn_func causal GQA prefill, head_dim 256", "batch": b,
                 "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d,
                 "published": "653 TFLOP/s, TPU v7x one core (docs/v7x.md:60)"},
@@ -536,6 +537,74 @@ def workload_c2d256(args, device):
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                   "kernel": "fw_prefill_d256_kernel<DENSE, false>",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=None)
+
+
+def workload_c2d256mha(args, device):
+    """docs/v7x.md:49's dense shape: as c2d256 with 32 KV heads."""
+    from flywheel_tpu import flash_attn_func
+    b, h, hk, s, d = 1, 32, 32, 4096, 256
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
+    flops = 4.0 * s * s * h * d / 2 * b
+    ms = timed(lambda: flash_attn_func(q, k, v, causal=True), args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(
+        name="c2d256mha", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        vs_baseline=round(tflops / 630.0, 3),
+        config={"workload": "flash_attn_func causal MHA prefill, head_dim 256", "batch": b,
+                "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d,
+                "published": "630 TFLOP/s, TPU v7x one core (docs/v7x.md:49)"},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "kernel": "fw_prefill_d256_kernel<DENSE, false>",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP"},
+        cpu=None)
+
+
+def workload_cp256(args, device, hk=4):
+    """The reference's published serving scenario (docs/v7x.md:131-157): one
+    16K-token sequence prefilled in 1K chunks through flash_attn_with_kvcache
+    (each chunk appends its K/V to the paged cache and attends causally to the
+    chunks before it and itself), 32 query heads, head_dim 256, bf16, 128-token
+    pages shuffled; one step = the whole prefill, 16 calls."""
+    from flywheel_tpu import flash_attn_with_kvcache
+    h, d, page, total, chunk = 32, 256, 128, 16384, 1024
+    rng = np.random.default_rng(0)
+    gen = torch.Generator(device=device).manual_seed(0)
+    pool, table, _ = paged_pool(gen, rng, np.array([0]), total, hk, d, page, torch.bfloat16,
+                                device)
+    q = torch.randn((total, h, d), generator=gen, device=device, dtype=torch.bfloat16)
+    kn = torch.randn((total, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    vn = torch.randn((total, hk, d), generator=gen, device=device, dtype=torch.bfloat16)
+    cu = torch.tensor([0, chunk], dtype=torch.int32, device=device)
+    lens = [torch.tensor([c * chunk], dtype=torch.int32, device=device)
+            for c in range(total // chunk)]
+
+    def step():
+        for c in range(total // chunk):
+            sl = slice(c * chunk, (c + 1) * chunk)
+            flash_attn_with_kvcache(q[sl], pool, None, kn[sl], vn[sl], cache_seqlens=lens[c],
+                                    block_table=table, cu_seqlens_q=cu, max_seqlen_q=chunk,
+                                    causal=True)
+    ms = timed(step, args.steps, args.warmup)
+    flops = 4.0 * total * total * h * d / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    pub = {4: "9.66 ms (455 TFLOP/s)", 32: "11.21 ms (392 TFLOP/s)"}[hk]
+    pub_ms = {4: 9.66, 32: 11.21}[hk]
+    return dict(
+        name=f"cp256{'' if hk == 4 else 'mha'}", unit="TFLOP/s", value=tflops, ms=ms,
+        dtype="bf16", vs_baseline=round(pub_ms / ms, 3),
+        config={"workload": "chunked prefill over a paged cache, 16K tokens in 1K chunks",
+                "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
+                "published": f"{pub}, TPU v7x one core (docs/v7x.md:155-157)"},
+        roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_d256_kernel"
+                            "<PAGED, false> (16 calls)",
+                  "algorithmic_per_launch": f"{flops:.4e} FLOP per 16 calls (causal count)"},
         cpu=None)
 
 
@@ -560,6 +629,7 @@ def workload_dec256(args, device):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return dict(
         name="dec256", unit="GB/s", value=gbs, ms=ms, dtype="bf16",
+        vs_baseline=round(gbs / 3310.0, 3),
         config={"workload": "flash_attn_with_kvcache paged decode + fused append, head_dim 256",
                 "batch": b, "nheads": h, "nheads_k": hk, "head_dim": d, "page_size": page,
                 "ctx": ctx, "published": "5.023 ms/step, 3.31 TB/s, TPU v7x one core"
@@ -573,7 +643,8 @@ def workload_dec256(args, device):
 
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
 EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "bwd": workload_bwd, "rope": workload_rope,
-         "c2d256": workload_c2d256, "dec256": workload_dec256,
+         "c2d256": workload_c2d256, "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
+         "cp256": workload_cp256, "cp256mha": lambda args, device: workload_cp256(args, device, hk=32),
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 
 
@@ -686,7 +757,9 @@ def main():
         "ms_per_step": round(head["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        # a published reference number for this exact shape and metric
+        # (the d256 extras), else None
+        "vs_baseline": head.get("vs_baseline"),
         "dtype": head["dtype"],
         "data": "synthetic (seeded N(0,1) inputs resident in HBM)",
         "config": head["config"],
@@ -696,7 +769,8 @@ def main():
     also = []
     for r in results[1:]:
         also.append({"workload": r["name"], "value": round(r["value"], 3), "unit": r["unit"],
-                     "ms_per_step": round(r["ms"], 5), "dtype": r["dtype"], "config": r["config"],
+                     "ms_per_step": round(r["ms"], 5), "vs_baseline": r.get("vs_baseline"),
+                     "dtype": r["dtype"], "config": r["config"],
                      "roofline": r["roofline"], "cpu_baseline": r["cpu_baseline"]})
     if also:
         line["also"] = also
