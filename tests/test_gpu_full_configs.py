@@ -1,4 +1,5 @@
-"""GPU parity at the full size of BASELINE configs C3, C4 and C5: the exact
+"""GPU parity at the full size of BASELINE configs C3, C4 (bf16 and over an e4m3
+pool) and C5: the exact
 seeded draws bench.py times (bench.inputs_c3 / inputs_c4 / inputs_c5; shapes
 from the reference's scenario generator, benchmarks/softmax_attention/
 kvcache_scenarios.py:313-329,682).
@@ -106,6 +107,44 @@ def test_c4_full_size():
                                     np.array([total]), np.zeros((1, 1), np.int64), causal=True,
                                     window_left=window - 1, softcap=50.0, round_scaled_q=True)
         assert_close(o[rows], ro, what=f"request {s} (prior {prior[s]}, chunk {chunks[s]})")
+        assert_lse(ls[:, rows], rl)
+
+
+def test_c4_fp8_full_size():
+    """C4's draw over an e4m3 pool (descales 0.8 / 1.25; bench.py's c4fp8):
+    the fp8 rows widened into LDS by the ping-pong kernel, at full size."""
+    announce("C4 full size over an e4m3 pool")
+    x = bench.inputs_c4(DEV, fp8=True)
+    hk, window = x["hk"], x["window"]
+    chunks, prior = x["chunks"], x["prior"]
+    kd, vd = x["extra"]["k_descale"], x["extra"]["v_descale"]
+    before = codes_of(x["pool"])
+    out, lse, pool = flash_attn_with_kvcache(
+        x["q"], x["pool"], None, x["kn"], x["vn"], cache_seqlens=x["lens"], block_table=x["tab"],
+        cu_seqlens_q=x["cu"], max_seqlen_q=int(chunks.max()), causal=True,
+        window_size=(window - 1, 0), softcap=50.0, k_descale=kd, v_descale=vd,
+        return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert pool is x["pool"]
+    after = codes_of(pool)
+    cu = x["cu"].cpu().numpy()
+    expected = P.append_to_pages(before, new_rows_codes(x["kn"]), new_rows_codes(x["vn"]), cu,
+                                 prior, x["table_np"])
+    del before
+    np.testing.assert_array_equal(after, expected)
+    del expected
+    q = x["q"].float().cpu().numpy()
+    o = out.float().cpu().numpy()
+    ls = lse.cpu().numpy()
+    for s in sorted({int(np.argmax(prior)), int(np.argmax(chunks))}):
+        total = int(prior[s] + chunks[s])
+        k, v = seq_rows(after, x["table_np"][s], total, hk, torch.float8_e4m3fn)
+        rows = slice(int(cu[s]), int(cu[s + 1]))
+        ro, rl = A.ragged_reference(q[rows], k[None], v[None], np.array([0, chunks[s]]),
+                                    np.array([total]), np.zeros((1, 1), np.int64), causal=True,
+                                    window_left=window - 1, softcap=50.0, k_descale=kd,
+                                    v_descale=vd, round_scaled_q=True)
+        assert_close(o[rows], ro, fp8=True, what=f"request {s} (prior {prior[s]}, chunk {chunks[s]})")
         assert_lse(ls[:, rows], rl)
 
 
