@@ -1188,8 +1188,12 @@ constexpr int kD2RowB = 512;                  // LDS bytes of one key row
 constexpr int kD2TileB = kD2Keys * kD2RowB;   // 16 KiB per K or V tile
 constexpr int kD2Bufs = 4;
 
-template <int MODE, bool SOFTCAP>
+template <int MODE, bool SOFTCAP, int KV = FW_BF16>
 __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) {
+  // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile t+3 into
+  // registers in step t and widens them to bf16 into the tile's LDS buffer in
+  // step t+1, one step before the QK that reads them; the rest is the bf16 kernel.
+  constexpr bool kFp8 = KV != FW_BF16;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kD2Bufs * kD2TileB];
 
   const int tid = threadIdx.x;
@@ -1313,10 +1317,54 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
       lds_dma16(vp, __umul24(rl, vstB) + dsrc[i], ldsV + d + 2 * i * kD2RowB);
     }
   };
+  // fp8: lane l holds row 8w + l/8, dims 32(l%8) .. +31 of K and V (32 bytes
+  // each; an invalid page id reads the zero rows).
+  struct F8Rows {
+    u32x4_t k0, k1, v0, v1;
+  };
+  auto f8_load = [&](int j) __attribute__((always_inline)) {
+    const int kmax = sk_len - 1;
+    const int key0 = min((t_begin + j) * kD2Keys + 8 * w, kmax) & ~7;
+    const int page = a.table[(size_t)seq * a.max_pages + key0 / a.P];
+    const bool bad = page < 0 || page >= a.num_pages;
+    const uint32_t lim = bad ? 0u : (uint32_t)(kmax - key0);
+    const uint32_t r = min((uint32_t)lane >> 3, lim);
+    const uint8_t *kp =
+        bad ? kZeroKV
+            : a.k + (((size_t)page * a.P + key0 % a.P + r) * a.CH + 2 * hk) * (kD2RowB / 2);
+    kp += 32 * (lane & 7);
+    const uint8_t *vp = kp + kD2RowB / 2;
+    return F8Rows{*(const u32x4_t *)kp, *(const u32x4_t *)(kp + 16), *(const u32x4_t *)vp,
+                  *(const u32x4_t *)(vp + 16)};
+  };
+  auto f8_store = [&](const F8Rows &f, const int buf) __attribute__((always_inline)) {
+    const int r = 8 * w + (lane >> 3), c = lane & 7;
+    const uint32_t off = (uint32_t)buf * kD2TileB + (uint32_t)r * kD2RowB;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const u32x4_t x0 = kv ? f.v0 : f.k0, x1 = kv ? f.v1 : f.k1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // bf16 chunk 4c + q: fp8 words 2q, 2q + 1
+        const u32x4_t &x = q < 2 ? x0 : x1;
+        const uint32_t w0 = x[2 * (q & 1)], w1 = x[2 * (q & 1) + 1];
+        const u32x4_t o = {fp8x2_to_bf16x2<KV>(w0, false), fp8x2_to_bf16x2<KV>(w0, true),
+                           fp8x2_to_bf16x2<KV>(w1, false), fp8x2_to_bf16x2<KV>(w1, true)};
+        *(FW_LDS u32x4_t *)((kv ? ldsV : lds0) + off + 16u * ((4 * c + q) ^ swz(r))) = o;
+      }
+    }
+  };
+  F8Rows fr{};  // fp8: the rows loaded in the previous step (tile t+2 at step t)
+  F8Rows fr0{}, fr1{};
   // Tiles 0-2 go out before the Q loads so the latencies overlap.
-  if (T > 0) dma(0, 0);
-  if (T > 1) dma(1, 1);
-  if (T > 2) dma(2, 2);
+  if constexpr (kFp8) {
+    if (T > 0) fr0 = f8_load(0);
+    if (T > 1) fr1 = f8_load(1);
+    if (T > 2) fr = f8_load(2);
+  } else {
+    if (T > 0) dma(0, 0);
+    if (T > 1) dma(1, 1);
+    if (T > 2) dma(2, 2);
+  }
 
   // ------------------------------------------------------------ Q^T operand
   bf16x8_t qop[16];
@@ -1483,10 +1531,17 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
   };
 
   if (T > 0) {
-    // waits: a step's copies (8 instructions) complete two steps later
-    if (T > 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (T > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (kFp8) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      f8_store(fr0, 0);
+      if (T > 1) f8_store(fr1, 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else {
+      // waits: a step's copies (8 instructions) complete two steps later
+      if (T > 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else if (T > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();  // tile 0 complete
     f32x16_t sa, sb;
     {
@@ -1499,11 +1554,23 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
       constexpr int B = decltype(bi)::value;  // t % 4
       // tile t+1 complete (tile t+2's copies may still be in flight), and
       // every wave is done with tile t-1's buffer
-      if (t + 2 < T) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (!kFp8) {
+        if (t + 2 < T) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
-      if (t + 3 < T) dma(t + 3, (B + 3) % 4);
+      if constexpr (kFp8) {
+        // tile t+2 into the buffer tile t-2 left (its PV ran before the last
+        // barrier), then tile t+3's rows for the next step
+        if (t + 2 < T) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          f8_store(fr, (B + 2) % 4);
+        }
+        if (t + 3 < T) fr = f8_load(t + 3);
+      } else {
+        if (t + 3 < T) dma(t + 3, (B + 3) % 4);
+      }
       const float m_sub = softmax_pre(s0, t_begin + t);
       float p[16], psum;
       // QK(t+1) with the exponentials of tile t; at t = T-1 the QK reads a
@@ -1680,9 +1747,9 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 }
 
 // Kernel choice (the host has checked the head dims): 128/128 -> the ping-pong
-// kernel (fp8 pools widened as they land in LDS), bf16 256/256 -> the d256
-// kernel, everything else (head dim 64, head_dim_v != head_dim, fp8 at 64 and
-// 256) -> the register-staged kernel.
+// kernel, 256/256 -> the d256 kernel (fp8 pools widened as they land in LDS in
+// both), everything else (head dim 64, head_dim_v != head_dim) -> the
+// register-staged kernel.
 template <int MODE, int KV, int D, int DV>
 static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
   fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
@@ -1711,7 +1778,8 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
       if (d == 64) {
         launch_staged<MODE, KV, 64, 64>(a, grid, s);
       } else if (d == 256) {
-        launch_staged<MODE, KV, 256, 256>(a, grid, s);
+        if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true, KV><<<grid, 256, 0, s>>>(a);
+        else fw_prefill_d256_kernel<MODE, false, KV><<<grid, 256, 0, s>>>(a);
       } else {
         if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true, KV><<<grid, 512, 0, s>>>(a);
         else fw_prefill_pp_kernel<MODE, false, KV><<<grid, 512, 0, s>>>(a);

@@ -85,24 +85,26 @@ def test_decode_ignores_nan_in_unused_slots(dtype, append):
     assert_lse(lse.cpu().numpy(), rl)
 
 
+@pytest.mark.parametrize("hd", [128, 256])
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
-def test_verify_window_and_chunked_prefill_ignore_nan(dtype):
+def test_verify_window_and_chunked_prefill_ignore_nan(dtype, hd):
     """The folded verify window (decode kernel after an append) and the paged
-    varlen prefill kernels (bf16 ping-pong, fp8 staged) over a pool whose
-    unused slots hold NaN."""
-    announce(f"verify window + chunked prefill NaN slots {dtype}")
+    varlen prefill kernels (the ping-pong kernel at head_dim 128, the d256
+    kernel at 256; bf16 and fp8 pools) over a pool whose unused slots hold
+    NaN."""
+    announce(f"verify window + chunked prefill NaN slots {dtype} d{hd}")
     rng = np.random.default_rng(41)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
     lengths = [3, 100, 700, 2047]
     case = PagedCase(rng, batch=4, nheads=32, nheads_k=8, lengths=lengths, new_tokens=[4] * 4,
-                     dtype=dt, k_descale=0.5, v_descale=2.0, extra_pages=2)
+                     head_dim=hd, dtype=dt, k_descale=0.5, v_descale=2.0, extra_pages=2)
     poison_unused_slots(case, case.lengths)
     totals = case.lengths + 4
-    q = randn(rng, (4, 4, 32, 128))
+    q = randn(rng, (4, 4, 32, hd))
     pool = case.pool()
     out, lse, _ = flash_attn_with_kvcache(
-        to_dev_bf16(q), pool, None, dev_from_codes(case.k_codes.reshape(4, 4, 8, 128), dt),
-        dev_from_codes(case.v_codes.reshape(4, 4, 8, 128), dt),
+        to_dev_bf16(q), pool, None, dev_from_codes(case.k_codes.reshape(4, 4, 8, hd), dt),
+        dev_from_codes(case.v_codes.reshape(4, 4, 8, hd), dt),
         cache_seqlens=torch.tensor(lengths, device=DEV), causal=True,
         block_table=torch.tensor(case.table, device=DEV), return_softmax_lse=True,
         k_descale=0.5, v_descale=2.0)
@@ -117,7 +119,7 @@ def test_verify_window_and_chunked_prefill_ignore_nan(dtype):
     # sequence on top of the appended lengths
     qlens = np.array([1, 100, 77, 300])
     cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
-    qp = randn(rng, (int(cu[-1]), 32, 128))
+    qp = randn(rng, (int(cu[-1]), 32, hd))
     used = totals  # kv lengths: the appended lengths
     out2, lse2 = flash_attn_varlen_func(
         to_dev_bf16(np.ascontiguousarray(qp.transpose(1, 0, 2))), pool, None,
@@ -134,29 +136,30 @@ def test_verify_window_and_chunked_prefill_ignore_nan(dtype):
     assert_lse(lse2.cpu().numpy(), rl2)
 
 
+@pytest.mark.parametrize("hd", [128, 256])
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
 @pytest.mark.parametrize("bad_id", [-1, 1 << 30])
-def test_invalid_page_ids_read_as_zero_rows(dtype, bad_id):
+def test_invalid_page_ids_read_as_zero_rows(dtype, bad_id, hd):
     """Decode (with the fused append), the folded verify window and the paged
     varlen prefill over a table with out-of-range entries: nothing is read or
     written through them, and their keys act as zero K and V rows.  Expected:
     the oracle over the same table with those entries pointing at a page of
     zeros."""
-    announce(f"invalid page ids {dtype} id={bad_id}")
+    announce(f"invalid page ids {dtype} id={bad_id} d{hd}")
     rng = np.random.default_rng(42)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
     lengths = [64, 700, 333, 1500]
     case = PagedCase(rng, batch=4, nheads=8, nheads_k=2, lengths=lengths, new_tokens=[1] * 4,
-                     dtype=dt, extra_pages=2)
+                     head_dim=hd, dtype=dt, extra_pages=2)
     poison_unused_slots(case, case.lengths)
     bad = {0: [1], 1: [0, 5, 6, 30], 2: [19], 3: [92]}  # full pages before each row's append page
     table = case.table.copy()
     for r, idx in bad.items():
         table[r, idx] = bad_id
-    q = randn(rng, (4, 1, 8, 128))
+    q = randn(rng, (4, 1, 8, hd))
     pool = case.pool()
-    kn = dev_from_codes(case.k_codes.reshape(4, 1, 2, 128), dt)
-    vn = dev_from_codes(case.v_codes.reshape(4, 1, 2, 128), dt)
+    kn = dev_from_codes(case.k_codes.reshape(4, 1, 2, hd), dt)
+    vn = dev_from_codes(case.v_codes.reshape(4, 1, 2, hd), dt)
     out, lse, _ = flash_attn_with_kvcache(
         to_dev_bf16(q), pool, None, kn, vn, cache_seqlens=torch.tensor(lengths, device=DEV),
         block_table=torch.tensor(table, device=DEV), return_softmax_lse=True)
@@ -176,7 +179,7 @@ def test_invalid_page_ids_read_as_zero_rows(dtype, bad_id):
     # paged varlen prefill over the same table, causal with a window
     qlens = np.array([5, 300, 1, 64])
     cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
-    qp = randn(rng, (int(cu[-1]), 8, 128))
+    qp = randn(rng, (int(cu[-1]), 8, hd))
     out2, lse2 = flash_attn_varlen_func(
         to_dev_bf16(np.ascontiguousarray(qp.transpose(1, 0, 2))), pool, None,
         torch.tensor(cu, device=DEV), None, int(qlens.max()), int(totals.max()), causal=True,
