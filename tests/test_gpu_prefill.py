@@ -274,6 +274,24 @@ def test_flash_attn_func_head_dims(d, dv, b, h, hk, sq, sk, causal, window, soft
     assert_lse(lse.cpu().numpy(), rl)
 
 
+@pytest.mark.parametrize("d,dv", HEAD_DIMS)
+def test_flash_attn_func_head_dims_sinks(d, dv):
+    """learnable_sink through the d256 and register-staged kernels (rows that
+    see no key return the sink-only result: out 0, lse = the sink)."""
+    announce(f"dense d{d}/{dv} sinks")
+    rng = np.random.default_rng(74)
+    b, h, hk, sq, sk = 1, 8, 2, 200, 150
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, dv))
+    sinks = rng.standard_normal(h).astype(np.float32)
+    out, lse = flash_attn_func(
+        to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)), to_dev_bf16(head_major(v)),
+        causal=True, return_softmax_lse=True, learnable_sink=torch.tensor(sinks, device=DEV))
+    torch.cuda.synchronize()
+    ro, rl = A.attention_ref(q, k, v, causal=True, sinks=sinks, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy(), head_major(ro))
+    assert_lse(lse.cpu().numpy(), rl)
+
+
 def test_flash_attn_func_token_major_paired_d64():
     """Token-major head_dim 64 (the reference's paired form: MHA, even head
     count, inputs.py:106-147)."""
