@@ -905,11 +905,12 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
         __builtin_amdgcn_sched_barrier(0);  // MFMA, then the reads kPipe steps on
       }
       // softcap_log2 * tanh(s) - anchor, by the wave's largest |s| as in
-      // softcap_scores: the degree-3 or degree-5 polynomial, three scores per
-      // remaining PV step (the degree-3 one as the degree-5 form with c2 = 0,
-      // bit-identical); beyond 0.3 the steps apply the identity and the exact
-      // tanh follows the MFMAs.  No branch around the MFMAs: a branch there
-      // makes the compiler copy the O accumulators at the join.
+      // softcap_scores: when every |s| <= kTanhPoly3Bound (the common case:
+      // |s / softcap| is small) the degree-3 polynomial, three scores per
+      // remaining PV step; otherwise the steps apply the identity and
+      // softcap_scores (degree 5 or exact) follows the MFMAs.  No branch around
+      // the MFMAs: a branch there makes the compiler copy the O accumulators at
+      // the join.
       const float m_qk = m_run == -INFINITY ? 0.f : m_run;
       float amax = 0.f;
 #pragma unroll
@@ -917,26 +918,33 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(sacc[i][e]));
       const float cl = a.softcap_log2;
-      const bool exact = __any(amax > kTanhPolyBound);
-      const bool deg5 = __any(amax > kTanhPoly3Bound);
-      const float c0 = exact ? 1.f : cl * (deg5 ? kTanhC0 : kTanhD0);
-      const float c1 = exact ? 0.f : cl * (deg5 ? kTanhC1 : kTanhD1);
-      const float c2 = exact || !deg5 ? 0.f : cl * kTanhC2;
-      const float an = exact ? 0.f : m_qk;
+      const bool later = __any(amax > kTanhPoly3Bound);
+      const float d0 = later ? 1.f : cl * kTanhD0;
+      const float d1 = later ? 0.f : cl * kTanhD1;
+      const float an = later ? 0.f : m_qk;
 #pragma unroll
       for (int pos = 19; pos < 32; ++pos) {
         step(pos);
 #pragma unroll
         for (int k = 3 * (pos - 19); k < 3 * (pos - 19) + 3 && k < 32; ++k)
-          sacc[k >> 4][k & 15] = tanh_poly_scaled<true>(sacc[k >> 4][k & 15], c0, c1, c2, an);
+          sacc[k >> 4][k & 15] = tanh_poly3_scaled<true>(sacc[k >> 4][k & 15], d0, d1, an);
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (exact) {
+      if (later) {
         asm volatile("" ::: "memory");  // a real branch: never if-converted
+        if (__any(amax > kTanhPolyBound)) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sacc[i][e] = fmaf(fast_tanh(sacc[i][e]), cl, -m_qk);
+            for (int e = 0; e < 16; ++e) sacc[i][e] = fmaf(fast_tanh(sacc[i][e]), cl, -m_qk);
+        } else {
+          const float c0 = cl * kTanhC0, c1 = cl * kTanhC1, c2 = cl * kTanhC2;
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              sacc[i][e] = tanh_poly_scaled<true>(sacc[i][e], c0, c1, c2, m_qk);
+        }
       }
     } else {
 #pragma unroll
