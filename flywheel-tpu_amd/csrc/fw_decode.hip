@@ -373,7 +373,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       uint32_t pw[4];
       auto exponentiate = [&]() {
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        psum = 0.f;
+        psum = -0.f;  // x + -0 = x exactly: the first add folds away
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const float p0 = fast_exp2(sc[2 * p] - m_use);

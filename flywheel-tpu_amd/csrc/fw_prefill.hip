@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256, D > 128 || DV > 128 ? 1 : 2) void fw_prefill_s
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
-    float psum = 0.f;
+    float psum = -0.f;  // x + -0 = x exactly: the first add folds away
     bf16x8_t pop[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -981,7 +981,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
     float psum;
     auto exponentiate = [&](float m_use) {
-      psum = 0.f;
+      psum = -0.f;  // x + -0 = x exactly: the first add folds away
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         u32x4_t pw;
@@ -1435,7 +1435,7 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
     };
 #pragma unroll
     for (int j = 0; j < KP; ++j) kread(j);
-    psum = 0.f;
+    psum = -0.f;  // x + -0 = x exactly: the first add folds away
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -1502,7 +1502,7 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
     return SOFTCAP ? m_now : 0.f;
   };
   auto exponentiate = [&](const f32x16_t &s, float m_use, bf16x8_t (&pop)[2]) __attribute__((always_inline)) {
-    float psum = 0.f;
+    float psum = -0.f;  // x + -0 = x exactly: the first add folds away
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       u32x4_t pw;
