@@ -274,6 +274,34 @@ def test_flash_attn_func_head_dims(d, dv, b, h, hk, sq, sk, causal, window, soft
     assert_lse(lse.cpu().numpy(), rl)
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("jump", [40.0, 600.0])
+def test_flash_attn_func_anchor_rescale(d, jump):
+    """The slow path of the static anchor (new row maximum, O and l rescaled)
+    taken twice per row: keys in thirds score 0, J/2 and J (log2 units), values
+    1, 2, 3.  J = 40 rescales by 2^-20 twice (the rescale must reach every O
+    register: one left unscaled moves out by ~1); J = 600 underflows the
+    factor to 0 (as the reference's anchor-change test,
+    test_regression.py:1035-1063).  Out is ~3 in closed form."""
+    announce(f"dense d{d} anchor rescale jump {jump}")
+    sk, sq, h = 768, 256, 2
+    y = jump / (math.sqrt(d) * A.LOG2E)  # q = 1: score(log2) = y * sqrt(d) * log2(e)
+    q = np.ones((1, sq, h, d), np.float32)
+    k = np.zeros((1, sk, 1, d), np.float32)
+    v = np.ones((1, sk, 1, d), np.float32)
+    k[:, 256:512], k[:, 512:] = y / 2, y
+    v[:, 256:512], v[:, 512:] = 2.0, 3.0
+    q, k, v = (np.asarray(torch.tensor(x).to(torch.bfloat16).float()) for x in (q, k, v))
+    out, lse = flash_attn_func(to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)),
+                               to_dev_bf16(head_major(v)), return_softmax_lse=True)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    np.testing.assert_allclose(o, 3.0, atol=2e-2)
+    ro, rl = A.attention_ref(q, k, v, round_scaled_q=True)
+    assert_close(o, head_major(ro))
+    assert_lse(lse.cpu().numpy(), rl)
+
+
 @pytest.mark.parametrize("d,dv", HEAD_DIMS)
 def test_flash_attn_func_head_dims_sinks(d, dv):
     """learnable_sink through the d256 and register-staged kernels (rows that
