@@ -148,6 +148,28 @@ __device__ __forceinline__ void softcap_scores(Acc &sc, float softcap_log2, floa
   }
 }
 
+// acc *= s on an MFMA accumulator kept in AGPRs: each register is read,
+// scaled and written back in place.  Written as plain VALU code, the rescale
+// makes the compiler keep a VGPR copy of every accumulator live across the
+// loop around it (an AGPR read per register per iteration).  Callers run it
+// where every MFMA that wrote acc has long completed; the s_nop covers the
+// next MFMA's read of the rewritten AGPRs.
+template <typename Vec>
+__device__ __forceinline__ void scale_in_agprs(Vec &acc, float s) {
+  constexpr int N = sizeof(Vec) / sizeof(float);
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    float t;
+    asm volatile(
+        "v_accvgpr_read_b32 %1, %0\n\t"
+        "v_mul_f32 %1, %1, %2\n\t"
+        "v_accvgpr_write_b32 %0, %1"
+        : "+a"(acc[e]), "=&v"(t)
+        : "v"(s));
+  }
+  asm volatile("s_nop 4" ::: "memory");
+}
+
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }

@@ -1189,26 +1189,6 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 // three steps ahead; each wave copies 8 key rows of every tile.  One barrier
 // per step.  The LDS rows use the same 16-byte chunk swizzle swz(row) as the
 // head_dim-128 kernels (on the low 4 bits of the 32-chunk row).
-// acc *= s on an accumulator that lives in AGPRs, read, scaled and written
-// back in place.  Written as VALU code, the rescale makes the compiler keep a
-// VGPR copy of all the O accumulators live across the loop (128 AGPR reads on
-// every tile step).  Every MFMA that wrote acc is long complete here (a barrier
-// and a full QK step lie between them), and the s_nop covers the next MFMA's
-// read of the rewritten AGPRs.
-__device__ __forceinline__ void scale_in_agprs(f32x16_t &acc, float s) {
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    float t;
-    asm volatile(
-        "v_accvgpr_read_b32 %1, %0\n\t"
-        "v_mul_f32 %1, %1, %2\n\t"
-        "v_accvgpr_write_b32 %0, %1"
-        : "+a"(acc[e]), "=&v"(t)
-        : "v"(s));
-  }
-  asm volatile("s_nop 4" ::: "memory");
-}
-
 constexpr int kD2Waves = 4;
 constexpr int kD2Rows = 32 * kD2Waves;        // q rows per workgroup
 constexpr int kD2Keys = 32;                   // keys per K/V tile
