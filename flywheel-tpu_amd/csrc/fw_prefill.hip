@@ -946,6 +946,10 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
               sacc[i][e] = tanh_poly_scaled<true>(sacc[i][e], c0, c1, c2, m_qk);
         }
       }
+      // pinned at the join: without it the common path (no branch taken)
+      // copies all 32 scores into the registers the branch wrote
+#pragma unroll
+      for (int i = 0; i < 2; ++i) asm volatile("" : "+v"(sacc[i]));
     } else {
 #pragma unroll
       for (int pos = 0; pos < 32; ++pos) {
