@@ -260,18 +260,33 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
           }
         }
         // value e: query row qb + 32st + 8(e>>2) + 4g + (e&3), key `key`
+        float pe[16];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          const f32x4_t l4 = *(const f32x4_t *)(Ls + 32 * st + 8 * blk + 4 * g);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pe[4 * blk + i] = fast_exp2(sacc[4 * blk + i] - l4[i]);
+        }
+        // the causal mask only on tiles that cross the diagonal (a real
+        // branch: the select on every tile cost four instructions a score)
+        if (!full) {
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int r = 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+            pe[e] = qb + r + off >= key ? pe[e] : 0.f;
+          }
+        }
         bf16x8_t pop[2], dsop[2];
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
           const int r0 = 32 * st + 8 * blk + 4 * g;
-          const f32x4_t l4 = *(const f32x4_t *)(Ls + r0);
           const f32x4_t d4 = *(const f32x4_t *)(Dl + r0);
           float pv[4], dv4[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = 4 * blk + i;
-            const bool vis = full || qb + r0 + i + off >= key;
-            const float p = vis ? fast_exp2(sacc[e] - l4[i]) : 0.f;
+            const float p = pe[e];
             pv[i] = p;
             dv4[i] = p * (dpacc[e] - d4[i]);
           }

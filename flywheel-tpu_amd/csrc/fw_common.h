@@ -35,11 +35,13 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // Two f32 -> packed bf16 pair (round to nearest even; v_cvt_pk_bf16_f32).
+// One v_cvt_pk_bf16_f32 (round to nearest even): written as a two-lane vector
+// conversion, since two scalar conversions are sometimes selected as two
+// half-used converts and a v_perm_b32 that merges them.
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  bf16x2_t r;
-  r[0] = (__bf16)a;
-  r[1] = (__bf16)b;
-  return __builtin_bit_cast(uint32_t, r);
+  typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+  const f32x2v_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // Columns i .. i + 3 (i a multiple of 4) of a RoPE table held as f32 or bf16,
