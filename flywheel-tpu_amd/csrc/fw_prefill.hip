@@ -569,6 +569,17 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
 }
+// Two copies into LDS at lds_addr and lds_addr + 1024 under one M0 value: the
+// second instruction's immediate offset (1024) moves both its LDS and its
+// global address, so its base is passed 1024 lower (the sum is the address
+// voff2 names; nothing is read below base).
+__device__ __forceinline__ void lds_dma16x2(const uint8_t *base, uint32_t voff1, uint32_t voff2,
+                                            uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
+               "global_load_lds_dwordx4 %2, %4 offset:1024"
+               :: "s"(lds_addr), "v"(voff1), "v"(voff2), "s"(base), "s"(base - 1024)
+               : "memory", "m0");
+}
 
 template <int MODE, bool SOFTCAP, int KV = FW_BF16>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
@@ -734,17 +745,15 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     return CopyPlan{kp, vp, __umul24(lra, kstB) + c16a, __umul24(lra, vstB) + c16a,
                     __umul24(lrb, kstB) + c16c, __umul24(lrb, vstB) + c16c, d};
   };
-  // Copy i (0-3) of a plan: K rows 0-3, V rows 0-3, K rows 4-7, V rows 4-7.
+  // Copy i (0-1) of a plan: K rows 0-7, then V rows 0-7 (four instructions).
   auto copy_issue = [&](const CopyPlan &c, const int i) __attribute__((always_inline)) {
-    if (i == 0) lds_dma16(c.kp, c.ka, c.d);
-    if (i == 1) lds_dma16(c.vp, c.va, c.d + 4 * kTileB);
-    if (i == 2) lds_dma16(c.kp, c.kb, c.d + 4 * kRowB);
-    if (i == 3) lds_dma16(c.vp, c.vb, c.d + 4 * kRowB + 4 * kTileB);
+    if (i == 0) lds_dma16x2(c.kp, c.ka, c.kb, c.d);
+    if (i == 1) lds_dma16x2(c.vp, c.va, c.vb, c.d + 4 * kTileB);
   };
   auto dma_tile_pg = [&](int j, const int buf, const int wv, int page) __attribute__((always_inline)) {
     const CopyPlan c = copy_plan(j, buf, wv, page);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) copy_issue(c, i);
+    for (int i = 0; i < 2; ++i) copy_issue(c, i);
   };
   auto dma_tile = [&](int j, const int buf, const int wv) __attribute__((always_inline)) {
     int page = 0;
