@@ -1,4 +1,5 @@
-"""Randomised GPU parity of every prefill and decode path against the oracle:
+"""Randomised GPU parity of every prefill and decode path against the oracle
+(head_dim 128, and 64 and 256 in a second set of draws):
 dense (GQA ratios, any lengths, causal / windows / softcap / sinks / RoPE),
 packed varlen (empty sequences, padding rows), paged varlen over bf16 / e4m3 /
 e5m2 pools (page sizes 16-64, descales) and paged decode with the fused append
@@ -23,7 +24,7 @@ def run(name, fn):
     fn()
 
 
-def one_case(seed, kind):
+def one_case(seed, kind, d=128):
     rng = np.random.default_rng(seed)
     hk = int(rng.choice([1, 2, 4])); G = int(rng.choice([1, 2, 4, 8])); h = hk * G
     causal = bool(rng.integers(0, 2))
@@ -34,11 +35,11 @@ def one_case(seed, kind):
     sinks = rng.standard_normal(h).astype(np.float32) if rng.random() < 0.2 else None
     if kind == 0:
         b = int(rng.integers(1, 3)); sq = int(rng.integers(1, 700)); sk = int(rng.integers(1, 700))
-        rope = rng.random() < 0.25 and softcap == 0.0
+        rope = rng.random() < 0.25 and softcap == 0.0 and d == 128
         if rope and sq > sk: sq = sk
-        name = f"dense b{b} h{h}/{hk} sq{sq} sk{sk} c{causal} w{window} sc{softcap} sink{sinks is not None} rope{rope}"
+        name = f"dense d{d} b{b} h{h}/{hk} sq{sq} sk{sk} c{causal} w{window} sc{softcap} sink{sinks is not None} rope{rope}"
         def f():
-            q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
+            q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, d))
             kw = {}
             qr, kr = q, k
             if rope:
@@ -60,12 +61,12 @@ def one_case(seed, kind):
         nseq = int(rng.integers(1, 6))
         ql = rng.integers(0, 300, nseq); kl = ql + rng.integers(0, 300, nseq)
         if not causal: kl = np.maximum(kl, 1)
-        name = f"varlen h{h}/{hk} ql{ql.tolist()} kl{kl.tolist()} c{causal} w{window} sc{softcap}"
+        name = f"varlen d{d} h{h}/{hk} ql{ql.tolist()} kl{kl.tolist()} c{causal} w{window} sc{softcap}"
         def f():
             cu_q = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
             cu_k = np.concatenate([[0], np.cumsum(kl)]).astype(np.int32)
             pad = int(rng.integers(0, 9))
-            q = randn(rng, (h, cu_q[-1] + pad, 128)); k = randn(rng, (hk, max(cu_k[-1], 1), 128)); v = randn(rng, (hk, max(cu_k[-1], 1), 128))
+            q = randn(rng, (h, cu_q[-1] + pad, d)); k = randn(rng, (hk, max(cu_k[-1], 1), d)); v = randn(rng, (hk, max(cu_k[-1], 1), d))
             out, lse = flash_attn_varlen_func(to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), torch.tensor(cu_q, device=DEV),
                                               torch.tensor(cu_k, device=DEV), max(int(ql.max()), 1), max(int(kl.max()), 1),
                                               causal=causal, window_size=window, softcap=softcap, return_softmax_lse=True,
@@ -91,13 +92,13 @@ def one_case(seed, kind):
         page = int(rng.choice([16, 32, 64]))
         ks_, vs_ = (1.0, 1.0) if dt_name == "bf16" else (float(rng.uniform(0.5, 2)), float(rng.uniform(0.5, 2)))
         w2 = (window[0], 0) if window[0] >= 0 else (-1, -1)
-        name = f"paged {dt_name} P{page} h{h}/{hk} ql{ql.tolist()} pre{pre.tolist()} c{causal} w{w2} sc{softcap}"
+        name = f"paged d{d} {dt_name} P{page} h{h}/{hk} ql{ql.tolist()} pre{pre.tolist()} c{causal} w{w2} sc{softcap}"
         def f():
             totals = ql + pre
             case = PagedCase(rng, batch=nseq, nheads=h, nheads_k=hk, lengths=totals, new_tokens=[0] * nseq,
-                             dtype=dt, k_descale=ks_, v_descale=vs_, page_size=page)
+                             dtype=dt, k_descale=ks_, v_descale=vs_, page_size=page, head_dim=d)
             cu = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
-            q = randn(rng, (cu[-1] + 3, h, 128))
+            q = randn(rng, (cu[-1] + 3, h, d))
             out, lse = flash_attn_varlen_func(
                 to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
                 torch.tensor(cu, device=DEV), None, max(int(ql.max()), 1), int(max(totals.max(), 1)), causal=causal,
@@ -119,12 +120,12 @@ def one_case(seed, kind):
         dt = torch.bfloat16 if dt_name == "bf16" else FP8[dt_name]
         nq = int(rng.choice([1, 1, 2, 4]))
         w2 = window if not (nq > 1 and window[1] > 0) else (window[0], 0)
-        name = f"decode {dt_name} b{bsz} h{h}/{hk} nq{nq} lens{lens.tolist()} c{causal} w{w2} sc{softcap}"
+        name = f"decode d{d} {dt_name} b{bsz} h{h}/{hk} nq{nq} lens{lens.tolist()} c{causal} w{w2} sc{softcap}"
         def f():
             case = PagedCase(rng, batch=bsz, nheads=h, nheads_k=hk, lengths=lens, new_tokens=[nq] * bsz, dtype=dt,
-                             k_descale=1.0, v_descale=1.0)
-            q = randn(rng, (bsz, nq, h, 128))
-            shape = (bsz, nq, hk, 128)
+                             k_descale=1.0, v_descale=1.0, head_dim=d)
+            q = randn(rng, (bsz, nq, h, d))
+            shape = (bsz, nq, hk, d)
             res = flash_attn_with_kvcache(to_dev_bf16(q), case.pool(), None,
                                           dev_from_codes(case.k_codes.reshape(shape), dt), dev_from_codes(case.v_codes.reshape(shape), dt),
                                           cache_seqlens=torch.tensor(lens, dtype=torch.int32, device=DEV),
@@ -148,3 +149,12 @@ KINDS = ("dense", "varlen", "paged", "decode")
 @pytest.mark.parametrize("seed", range(20))
 def test_random_case(kind, seed):
     one_case(1000 * kind + seed, kind)
+
+
+@pytest.mark.parametrize("kind", range(4), ids=KINDS)
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("d", [64, 256])
+def test_random_case_head_dims(d, kind, seed):
+    """The same draws at head_dim 64 (register-staged prefill kernel, decode)
+    and 256 (the head_dim-256 prefill kernel over bf16 and fp8 pools, decode)."""
+    one_case(5000 + 100 * d + 1000 * kind + seed, kind, d)
