@@ -475,6 +475,16 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
           dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
         }
       }
+      // the causal mask only on tiles that cross the diagonal (a real
+      // branch; exp2(-inf) = 0 then zeroes p and ds)
+      if (!full) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kk = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[e] = kk < r_hi ? sacc[e] : -INFINITY;
+        }
+      }
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) {
         u32x4_t dw;
@@ -484,10 +494,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int e = 8 * u2 + 2 * e2 + i;
-            const int kk = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
-            const bool vis = full || kk < r_hi;
-            const float p = vis ? fast_exp2(sacc[e] - l2) : 0.f;
-            dsv[i] = p * (dpacc[e] - dl);
+            dsv[i] = fast_exp2(sacc[e] - l2) * (dpacc[e] - dl);
           }
           dw[e2] = pack_bf16(dsv[0], dsv[1]);
         }
