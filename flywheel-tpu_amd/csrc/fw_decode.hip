@@ -150,15 +150,20 @@ struct KRow {
   typename std::conditional<KV == FW_BF16, bf16x8_t, u32x4_t>::type w[KV == FW_BF16 ? D / 32 : D / 64];
 };
 
+// The pool is streamed once per call, so its loads are non-temporal: on this
+// chip random 64 KiB page reads stream ~13% faster that way than as ordinary
+// cached loads (7.07 against 6.23 TB/s for a plain read of C3's pool size).
 template <int KV, int D>
 __device__ __forceinline__ void load_k_row(const uint8_t *row, int g, KRow<KV, D> &k) {
   if constexpr (KV == FW_BF16) {
 #pragma unroll
     for (int j = 0; j < D / 32; ++j)
-      k.w[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t *)(row + 64 * j + 16 * g));
+      k.w[j] = __builtin_bit_cast(
+          bf16x8_t, __builtin_nontemporal_load((const u32x4_t *)(row + 64 * j + 16 * g)));
   } else {
 #pragma unroll
-    for (int hh = 0; hh < D / 64; ++hh) k.w[hh] = *(const u32x4_t *)(row + 64 * hh + 16 * g);
+    for (int hh = 0; hh < D / 64; ++hh)
+      k.w[hh] = __builtin_nontemporal_load((const u32x4_t *)(row + 64 * hh + 16 * g));
   }
 }
 
@@ -472,11 +477,13 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
 #pragma unroll
             for (int vh = 0; vh < VH; ++vh) {
               if constexpr (KV == FW_BF16)
-                tl.vraw[4 * sub + i][vh] = 8 * n < D ? *(const u32x4_t *)(vrow + vo + 128 * EB * vh)
-                                                     : u32x4_t{0, 0, 0, 0};
+                tl.vraw[4 * sub + i][vh] =
+                    8 * n < D ? __builtin_nontemporal_load((const u32x4_t *)(vrow + vo + 128 * EB * vh))
+                              : u32x4_t{0, 0, 0, 0};
               else
-                tl.vraw[4 * sub + i][vh] = 8 * n < D ? *(const u32x2_t *)(vrow + vo + 128 * EB * vh)
-                                                     : u32x2_t{0, 0};
+                tl.vraw[4 * sub + i][vh] =
+                    8 * n < D ? __builtin_nontemporal_load((const u32x2_t *)(vrow + vo + 128 * EB * vh))
+                              : u32x2_t{0, 0};
             }
           }
         }
