@@ -446,13 +446,14 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
 #pragma unroll
       for (int t = 0; t < kTblPerLane; ++t)
         tbl_lane[t] = table[min(first_page + 64 * t + lane, a.max_pages - 1)];
-      // The last key of the chunk: sub-tile starts are clamped onto it (a
-      // tile past the end re-reads the last sub-tile, an L2 hit, never used),
-      // and rows past it (slots not written yet, or the next chunk's) are
-      // clamped onto its row: their contents may be anything, NaN included,
-      // and 0 * NaN would poison the PV product; the masks hide them.
+      // The last key of the chunk: sub-tile starts are clamped onto it (the
+      // second sub-tile of the chunk's last tile, when past the end, re-reads
+      // the first; never used), and rows past it (slots not written yet, or
+      // the next chunk's) are clamped onto its row: their contents may be
+      // anything, NaN included, and 0 * NaN would poison the PV product; the
+      // masks hide them.
       const int last_key = ce - 1;
-      // Loads are branch-free so the compiler can count them.  A page id
+      // Loads are branch-free.  A page id
       // outside [0, num_pages) is never dereferenced: the loads read page 0
       // and the compute stage replaces the sub-tile by zero K and V rows.
       auto load_tile = [&](int tb, DecodeTile<KV, D> &tl) {
@@ -488,18 +489,15 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
           }
         }
       };
-      // Register ring of two tile buffers: the next tile's loads are in
-      // flight while the current tile is computed.
-      const int last_tile = (ce - 1) & ~31;
-      DecodeTile<KV, D> t0, t1;
-      load_tile(cb, t0);
-      for (int tb = cb;; tb += 64) {
-        load_tile(min(tb + 32, last_tile), t1);
+      // One tile at a time: its loads, then its compute.  Keeping the next
+      // tile's loads in flight during the compute (a two-stage register ring)
+      // was slower (C3 703 against 675 us): the same random page reads with
+      // more of them outstanding stream ~6% slower here, in a plain read probe
+      // as in this kernel.
+      for (int tb = cb; tb < ce; tb += 32) {
+        DecodeTile<KV, D> t0;
+        load_tile(tb, t0);
         compute_tile(tb, t0, key_lo, row_hi, edge(tb));
-        if (tb + 32 >= ce) break;
-        load_tile(min(tb + 64, last_tile), t0);
-        compute_tile(tb + 32, t1, key_lo, row_hi, edge(tb + 32));
-        if (tb + 64 >= ce) break;
       }
     }
     // The appended token's K/V, from k_new / v_new into every key slot (only
