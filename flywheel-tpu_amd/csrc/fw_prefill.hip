@@ -85,17 +85,17 @@ __device__ __forceinline__ float v_descale_of(const PrefillArgs &a) {
   return a.vd ? *a.vd : a.v_descale;
 }
 
-// RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7, at table
-// row tb / 64, in f32 with one rounding to bf16 (rotary.py:170-215).  Both
-// partners of every pair are in the lane: dims d and d + 64 are words j and
-// j + 4 (halves), dims 2i and 2i + 1 one packed word (interleaved).
-template <bool F32>
+// RoPE of one lane's Q words raw[j] = dims 16j + 8g .. 16j + 8g + 7 (j < D/16),
+// at table row tb / (D/2), in f32 with one rounding to bf16 (rotary.py:170-215).
+// Both partners of every pair are in the lane: dims d and d + D/2 are words j
+// and j + D/32 (halves), dims 2i and 2i + 1 one packed word (interleaved).
+template <bool F32, int D>
 __device__ __forceinline__ void rope_q_words(const PrefillArgs &a, size_t tb, int g,
-                                             u32x4_t (&raw)[8]) {
+                                             u32x4_t (&raw)[D / 16]) {
 #pragma clang fp contract(off)
   if (!a.ril) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < D / 32; ++j)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         float c[4], sn[4];
@@ -106,14 +106,14 @@ __device__ __forceinline__ void rope_q_words(const PrefillArgs &a, size_t tb, in
           const int e = 2 * hf + e2;
           const float ca = c[2 * e2], cb = c[2 * e2 + 1], sa = sn[2 * e2], sb = sn[2 * e2 + 1];
           const float la = bf16_lo(raw[j][e]), lb = bf16_hi(raw[j][e]);
-          const float ha = bf16_lo(raw[j + 4][e]), hb = bf16_hi(raw[j + 4][e]);
+          const float ha = bf16_lo(raw[j + D / 32][e]), hb = bf16_hi(raw[j + D / 32][e]);
           raw[j][e] = pack_bf16(la * ca - ha * sa, lb * cb - hb * sb);
-          raw[j + 4][e] = pack_bf16(ha * ca + la * sa, hb * cb + lb * sb);
+          raw[j + D / 32][e] = pack_bf16(ha * ca + la * sa, hb * cb + lb * sb);
         }
       }
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < D / 16; ++j) {
       float c[4], sn[4];
       rope_load4<F32>(a.rcos, tb + 8 * j + 4 * g, c);
       rope_load4<F32>(a.rsin, tb + 8 * j + 4 * g, sn);
@@ -126,7 +126,7 @@ __device__ __forceinline__ void rope_q_words(const PrefillArgs &a, size_t tb, in
   }
 }
 
-// One lane's Q^T operand: dims 16j + 8g .. 16j + 8g + 7 (j = 0..7) of the row
+// One lane's Q^T operand: dims 16j + 8g .. 16j + 8g + 7 (j < D/16) of the row
 // at qp, rotated at position pos when RoPE tables are given, then scaled by qs
 // and rounded to bf16.
 template <int D = 128>
@@ -135,12 +135,10 @@ __device__ __forceinline__ void load_q_operand(const PrefillArgs &a, const uint1
   u32x4_t raw[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) raw[j] = *(const u32x4_t *)(qp + 16 * j + 8 * g);
-  if constexpr (D == 128) {  // fused RoPE: head_dim 128 (the host checks)
-    if (a.rcos) {
-      const size_t tb = (size_t)min(max(pos, 0), a.rrows - 1) * 64;
-      if (a.rf32) rope_q_words<true>(a, tb, g, raw);
-      else rope_q_words<false>(a, tb, g, raw);
-    }
+  if (a.rcos) {  // fused RoPE (the host requires head_dim_v == head_dim)
+    const size_t tb = (size_t)min(max(pos, 0), a.rrows - 1) * (D / 2);
+    if (a.rf32) rope_q_words<true, D>(a, tb, g, raw);
+    else rope_q_words<false, D>(a, tb, g, raw);
   }
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
@@ -1820,8 +1818,8 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
              " 128/256 or 256/128; got %d/%d", p->head_dim, dv);
   FW_REQUIRE(p->kv_mode != FW_KV_PAGED || dv == p->head_dim, FW_ERR_VALUE,
              "a paged pool has one head dim; got head_dim %d, head_dim_v %d", p->head_dim, dv);
-  FW_REQUIRE(!p->rotary_cos || (p->head_dim == 128 && dv == 128), FW_ERR_NOT_IMPLEMENTED,
-             "the fused RoPE takes head_dim 128; got %d/%d", p->head_dim, dv);
+  FW_REQUIRE(!p->rotary_cos || p->head_dim == dv, FW_ERR_NOT_IMPLEMENTED,
+             "the fused RoPE takes head_dim_v == head_dim; got %d/%d", p->head_dim, dv);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads=%d must be a multiple of nheads_k=%d", p->nheads, p->nheads_k);
   FW_REQUIRE(p->kv_mode >= FW_KV_DENSE && p->kv_mode <= FW_KV_PAGED, FW_ERR_VALUE,

@@ -1,9 +1,10 @@
 // RoPE of bf16 rows at their prefill positions (f32 arithmetic, one rounding
 // to bf16), the rotation the reference applies to staged Q / K tiles:
 // prepare_rotary (flywheel_tpu/softmax_attention/rotary.py:27-167) and
-// rotate_tile (rotary.py:170-215).  Eight threads per (row, head): thread i
-// owns dims 8i..8i+7 and 64+8i..64+8i+7, which holds both partners of every
-// pair in either pairing (halves: d with d+64; interleaved: 2j with 2j+1).
+// rotate_tile (rotary.py:170-215), for head_dim D in {64, 128, 256} (tables of
+// D / 2 columns).  D / 16 threads per (row, head): thread i owns dims
+// 8i..8i+7 and D/2+8i..D/2+8i+7, which holds both partners of every pair in
+// either pairing (halves: d with d + D/2; interleaved: 2j with 2j+1).
 #include "fw_common.h"
 
 // Products and sums are rounded separately (no fused multiply-add), as in the
@@ -40,12 +41,12 @@ __device__ __forceinline__ int token_position(const RotaryArgs &a, int t) {
   return local + base;
 }
 
-// Thread i's two 8-dim chunks (dims 8i.. and 64 + 8i..) rotated at table row
-// tb / 64.
-template <bool F32>
+// Thread i's two 8-dim chunks (dims 8i.. and D/2 + 8i..) rotated at table row
+// tb / (D / 2).
+template <bool F32, int D>
 __device__ __forceinline__ void rope_rows(const RotaryArgs &a, size_t tb, int i, const float (&xl)[8],
                                           const float (&xh)[8], float (&yl)[8], float (&yh)[8]) {
-  if (!a.interleaved) {  // pair (d, d + 64) with column d
+  if (!a.interleaved) {  // pair (d, d + D/2) with column d
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       float c[4], s[4];
@@ -62,8 +63,8 @@ __device__ __forceinline__ void rope_rows(const RotaryArgs &a, size_t tb, int i,
     float c0[4], s0[4], c1[4], s1[4];
     rope_load4<F32>(a.cosv, tb + 4 * i, c0);
     rope_load4<F32>(a.sinv, tb + 4 * i, s0);
-    rope_load4<F32>(a.cosv, tb + 32 + 4 * i, c1);
-    rope_load4<F32>(a.sinv, tb + 32 + 4 * i, s1);
+    rope_load4<F32>(a.cosv, tb + D / 4 + 4 * i, c1);
+    rope_load4<F32>(a.sinv, tb + D / 4 + 4 * i, s1);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       yl[2 * e] = xl[2 * e] * c0[e] - xl[2 * e + 1] * s0[e];
@@ -74,10 +75,12 @@ __device__ __forceinline__ void rope_rows(const RotaryArgs &a, size_t tb, int i,
   }
 }
 
+template <int D>
 __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
+  constexpr int TP = D / 16;  // threads per row
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t row = gid >> 3;
-  const int i = gid & 7;
+  const uint32_t row = gid / TP;
+  const int i = gid % TP;
   if (row >= (uint32_t)a.rows_b * a.H * a.T) return;
   const uint32_t bh = row / (uint32_t)a.T;
   const int t = row - bh * a.T;
@@ -86,17 +89,17 @@ __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
   const int pos = min(max(token_position(a, t), 0), a.table_rows - 1);
   const uint16_t *xr = a.x + (size_t)b * a.xsb + (size_t)h * a.xsh + (size_t)t * a.xst;
   uint16_t *yr = a.y + (size_t)b * a.ysb + (size_t)h * a.ysh + (size_t)t * a.yst;
-  const u32x4_t lo = *(const u32x4_t *)(xr + 8 * i), hi = *(const u32x4_t *)(xr + 64 + 8 * i);
+  const u32x4_t lo = *(const u32x4_t *)(xr + 8 * i), hi = *(const u32x4_t *)(xr + D / 2 + 8 * i);
   float xl[8], xh[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     xl[2 * e] = bf16_lo(lo[e]); xl[2 * e + 1] = bf16_hi(lo[e]);
     xh[2 * e] = bf16_lo(hi[e]); xh[2 * e + 1] = bf16_hi(hi[e]);
   }
-  const size_t tb = (size_t)pos * 64;  // table row (head_dim / 2 columns)
+  const size_t tb = (size_t)pos * (D / 2);  // table row (head_dim / 2 columns)
   float yl[8], yh[8];
-  if (a.table_f32) rope_rows<true>(a, tb, i, xl, xh, yl, yh);
-  else rope_rows<false>(a, tb, i, xl, xh, yl, yh);
+  if (a.table_f32) rope_rows<true, D>(a, tb, i, xl, xh, yl, yh);
+  else rope_rows<false, D>(a, tb, i, xl, xh, yl, yh);
   u32x4_t ol, oh;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
     oh[e] = pack_bf16(yh[2 * e], yh[2 * e + 1]);
   }
   *(u32x4_t *)(yr + 8 * i) = ol;
-  *(u32x4_t *)(yr + 64 + 8 * i) = oh;
+  *(u32x4_t *)(yr + D / 2 + 8 * i) = oh;
 }
 
 }  // namespace fw
@@ -112,8 +115,8 @@ __global__ __launch_bounds__(256) void fw_rotary_kernel(RotaryArgs a) {
 using namespace fw;
 
 extern "C" int fw_rotary(const fw_rotary_params *p, fw_stream_t stream) {
-  FW_REQUIRE(p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 rotary kernel takes head_dim 128; got %d", p->head_dim);
+  FW_REQUIRE(p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256, FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 rotary kernel takes head_dim 64, 128 or 256; got %d", p->head_dim);
   FW_REQUIRE(p->x && p->y && p->cos_table && p->sin_table, FW_ERR_VALUE,
              "x, y, cos_table and sin_table are required");
   FW_REQUIRE(p->table_rows > 0 && p->batch_rows >= 0 && p->nheads >= 0 && p->ntokens >= 0,
@@ -138,9 +141,14 @@ extern "C" int fw_rotary(const fw_rotary_params *p, fw_stream_t stream) {
   a.interleaved = p->interleaved ? 1 : 0;
   a.pos_offset = p->pos_offset;
   a.nseq = p->nseq;
-  const long threads = (long)a.rows_b * a.H * a.T * 8;
+  const int tp = p->head_dim / 16;  // threads per row
+  const long threads = (long)a.rows_b * a.H * a.T * tp;
   if (threads == 0) return FW_OK;
-  FW_REQUIRE(threads < (1l << 32), FW_ERR_VALUE, "%ld rows exceed one launch", threads / 8);
-  fw_rotary_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
+  FW_REQUIRE(threads < (1l << 32), FW_ERR_VALUE, "%ld rows exceed one launch", threads / tp);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  if (p->head_dim == 64) fw_rotary_kernel<64><<<grid, 256, 0, st>>>(a);
+  else if (p->head_dim == 128) fw_rotary_kernel<128><<<grid, 256, 0, st>>>(a);
+  else fw_rotary_kernel<256><<<grid, 256, 0, st>>>(a);
   return check_launch("fw_rotary_kernel");
 }

@@ -227,7 +227,7 @@ typedef struct fw_prefill_params {
   /* Head dim of v and out, 0 = head_dim (prefill.py's head_dim_v,
    * inputs.py:193-207).  head_dim / head_dim_v: 64/64, 128/128, 256/256,
    * 128/256 or 256/128; a paged pool has one head dim; the fused RoPE takes
-   * 128/128. */
+   * head_dim_v == head_dim (64, 128 or 256). */
   int32_t head_dim_v;
 } fw_prefill_params;
 
@@ -301,7 +301,7 @@ typedef struct fw_rotary_params {
   int32_t batch_rows;   /* size of the b index (1 for packed layouts) */
   int32_t nheads;
   int32_t ntokens;
-  int32_t head_dim;     /* 128 */
+  int32_t head_dim;     /* 64, 128 or 256 */
   int32_t table_rows;
   int32_t table_f32;
   int32_t interleaved;

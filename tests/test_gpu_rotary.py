@@ -14,14 +14,14 @@ from flywheel_tpu import rotary as R
 from oracle import attention as A
 from oracle import dtypes as T
 from oracle import rotary as RO
-from tests.gpu_util import (DEV, PagedCase, announce, assert_close, assert_lse, codes_of, randn,
-                            to_dev_bf16)
+from tests.gpu_util import (DEV, FP8, PagedCase, announce, assert_close, assert_lse, codes_of,
+                            randn, to_dev_bf16)
 
 pytestmark = pytest.mark.gpu
 
 
-def tables(rng, rows, f32):
-    ang = rng.random((rows, 64)) * 2 * math.pi
+def tables(rng, rows, f32, d=128):
+    ang = rng.random((rows, d // 2)) * 2 * math.pi
     cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
     if not f32:
         cos, sin = T.bf16(cos), T.bf16(sin)
@@ -178,3 +178,85 @@ def test_paged_rotary_q_at_cache_positions(interleaved):
                                     round_scaled_q=True, num_active=num_active)
         assert_close(out.float().cpu().numpy().transpose(1, 0, 2), ro, what=f"active={num_active}")
         assert_lse(lse.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rotate_rows_bitexact_head_dims(d, interleaved):
+    """fw_rotary at head_dim 64 and 256 (tables of d/2 columns): dense rows at
+    t + offset and packed rows with kv bases, bit-exact."""
+    announce(f"fw_rotary d{d} interleaved={interleaved}")
+    rng = np.random.default_rng(45 + d)
+    (cos, sin), tab = tables(rng, 300, f32=interleaved, d=d)  # bf16 and f32 tables both run
+    x = randn(rng, (2, 3, 65, d), scale=3.0)
+    y = R.rotate(to_dev_bf16(x), tab, interleaved, strides=(3 * 65 * d, 65 * d, d),
+                 batch_rows=2, nheads=3, ntokens=65, pos_offset=200)
+    want = RO.rotate(x, cos, sin, np.arange(65) + 200, interleaved)
+    np.testing.assert_array_equal(codes_of(y), T.bf16_round(want))
+    cu_q = np.array([0, 5, 5, 40], np.int32)
+    cu_k = np.array([0, 9, 12, 290], np.int32)
+    total = 43
+    x = randn(rng, (total, 2, d))
+    y = R.rotate(to_dev_bf16(x.reshape(total, 2 * d)), tab, interleaved, strides=(0, d, 2 * d),
+                 batch_rows=1, nheads=2, ntokens=total, cu=torch.tensor(cu_q, device=DEV),
+                 kv_cu=torch.tensor(cu_k, device=DEV))
+    pos = RO.packed_positions(cu_q, total, np.diff(cu_k) - np.diff(cu_q))
+    want = RO.rotate(x.transpose(1, 0, 2), cos, sin, pos, interleaved).transpose(1, 0, 2)
+    np.testing.assert_array_equal(codes_of(y).reshape(total, 2, d), T.bf16_round(want))
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("interleaved,rotary_k,f32", [(False, True, False), (True, True, True),
+                                                      (False, False, True)])
+def test_flash_attn_func_rotary_head_dims(d, interleaved, rotary_k, f32):
+    """Fused Q RoPE in the head_dim-64 (register-staged) and head_dim-256
+    kernels, K through fw_rotary: against rotate-then-attend."""
+    announce(f"dense rotary d{d} il={interleaved} rk={rotary_k} f32={f32}")
+    rng = np.random.default_rng(46 + d)
+    b, h, hk, sq, sk = 1, 8, 2, 190, 333
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, d))
+    (cos, sin), (tc, ts) = tables(rng, sk + 2, f32, d)
+    qpos, kpos = RO.dense_positions(sq, sk)
+    qr = RO.rotate(q.transpose(0, 2, 1, 3), cos, sin, qpos, interleaved).transpose(0, 2, 1, 3)
+    kr = RO.rotate(k.transpose(0, 2, 1, 3), cos, sin, kpos, interleaved).transpose(0, 2, 1, 3)
+    if not rotary_k:
+        kr = k
+    out, lse = flash_attn_func(to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)),
+                               to_dev_bf16(head_major(v)), causal=True, return_softmax_lse=True,
+                               rotary_cos=tc, rotary_sin=ts, rotary_interleaved=interleaved,
+                               rotary_k=rotary_k)
+    torch.cuda.synchronize()
+    ro, rl = A.attention_ref(qr, kr, v, causal=True, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy(), head_major(ro))
+    assert_lse(lse.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("d,dtype", [(64, "bf16"), (256, "bf16"), (256, "e4m3")])
+def test_paged_rotary_head_dims(d, dtype):
+    """Paged prefill with Q RoPE at head_dim 64 and 256 (bf16 and an e4m3
+    pool): Q only, at seqused_k - len_q + t."""
+    announce(f"paged rotary d{d} {dtype}")
+    rng = np.random.default_rng(47 + d)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    kd, vd = (1.0, 1.0) if dtype == "bf16" else (0.75, 1.5)
+    qlens, prefix = [3, 70, 130], [127, 0, 200]
+    totals = np.array(qlens) + np.array(prefix)
+    case = PagedCase(rng, batch=3, nheads=8, nheads_k=2, lengths=totals, new_tokens=[0] * 3,
+                     head_dim=d, dtype=dt, k_descale=kd, v_descale=vd)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = randn(rng, (cu[-1] + 2, 8, d))
+    (cos, sin), (tc, ts) = tables(rng, 400, True, d)
+    kp, vp = case.kv_pages(case.pool_codes)
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
+        torch.tensor(cu, device=DEV), None, max(qlens), 400, causal=True,
+        return_softmax_lse=True, block_table=torch.tensor(case.table, device=DEV),
+        seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), rotary_cos=tc,
+        rotary_sin=ts, rotary_k=False, k_descale=kd, v_descale=vd, nheads_k=2)
+    torch.cuda.synchronize()
+    pos = RO.packed_positions(cu, q.shape[0], np.array(prefix))
+    qr = RO.rotate(q.transpose(1, 0, 2), cos, sin, pos, False).transpose(1, 0, 2)
+    ro, rl = A.ragged_reference(qr, kp, vp, cu, totals, case.table, causal=True,
+                                k_descale=kd, v_descale=vd, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy().transpose(1, 0, 2), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
