@@ -130,10 +130,11 @@ def test_capi_validation_status_codes():
     bw.nheads, bw.nheads_k, bw.seqlen_k = 16, 2, 520  # few key tiles: heads split, partials
     assert lib.fw_attn_bwd_workspace_bytes(bw) > 2 * 2 * 520 * 128 * 4
     r = N.RotaryParams()
-    r.head_dim, r.table_rows = 64, 8
-    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED
-    r.head_dim = 128
-    assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
+    r.head_dim, r.table_rows = 96, 8
+    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED  # head dims 64, 128, 256
+    for d in (64, 128, 256):
+        r.head_dim = d
+        assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
 
 
 def bf(*shape):
