@@ -206,10 +206,11 @@ struct KvAddr {
 template <int MODE, int KV, int D, int DV>
 __global__ __launch_bounds__(256, D > 128 || DV > 128 ? 1 : 2) void fw_prefill_staged_kernel(PrefillArgs a) {
   constexpr int KS = kKS<D>;
-  // 8-element chunks of a K / V row per staging thread (16 threads a row; at
-  // head dim 64 threads 8-15 of a row have none)
-  constexpr int CPR = D >= 128 ? D / 128 : 1;
-  constexpr int CPRV = DV >= 128 ? DV / 128 : 1;
+  // 8-element chunks of a K / V row per staging thread (16 threads a row; a
+  // head dim that is not a multiple of 128 leaves the last threads of a row
+  // without a last chunk)
+  constexpr int CPR = (D + 127) / 128;
+  constexpr int CPRV = (DV + 127) / 128;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kStagedLds<D, DV>];
   uint16_t *Ks = (uint16_t *)smem;
   uint16_t *Vt = (uint16_t *)(smem + kKT * KS * 2);
@@ -1767,8 +1768,9 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 
 // Kernel choice (the host has checked the head dims): 128/128 -> the ping-pong
 // kernel, 256/256 -> the d256 kernel (fp8 pools widened as they land in LDS in
-// both), everything else (head dim 64, head_dim_v != head_dim) -> the
-// register-staged kernel.
+// both), everything else (head dims 64, 96, 192, head_dim_v != head_dim) ->
+// the register-staged kernel.  head_dim_v 512 (with head dim 64) runs as two
+// launches of head_dim_v 256 over the two halves of v and out.
 template <int MODE, int KV, int D, int DV>
 static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
   fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
@@ -1783,11 +1785,15 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
     } else if (d == 256 && dv == 256) {
       if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true><<<grid, 256, 0, s>>>(a);
       else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
-    } else if (d == 64) {
+    } else if (d == 64 && dv == 64) {
       launch_staged<MODE, FW_BF16, 64, 64>(a, grid, s);
-    } else if constexpr (MODE != FW_KV_PAGED) {  // a paged pool has one head dim
+    } else if constexpr (MODE != FW_KV_PAGED) {  // paged pools: 64, 128 and 256 only
       if (d == 128) launch_staged<MODE, FW_BF16, 128, 256>(a, grid, s);
-      else launch_staged<MODE, FW_BF16, 256, 128>(a, grid, s);
+      else if (d == 256) launch_staged<MODE, FW_BF16, 256, 128>(a, grid, s);
+      else if (d == 64) launch_staged<MODE, FW_BF16, 64, 256>(a, grid, s);  // dv 256, or a half of 512
+      else if (d == 96) launch_staged<MODE, FW_BF16, 96, 96>(a, grid, s);
+      else if (dv == 192) launch_staged<MODE, FW_BF16, 192, 192>(a, grid, s);
+      else launch_staged<MODE, FW_BF16, 192, 128>(a, grid, s);
     }
     return;
   }
@@ -1809,15 +1815,31 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
   }
 }
 
+// Half h (0 or 1) of a head_dim_v-512 call: dims 256h .. 256h + 255 of v and
+// out.  Both halves compute the same scores and write the same lse.
+static PrefillArgs v_half(PrefillArgs a, int h) {
+  a.v += (size_t)h * 256 * 2;
+  a.out += (size_t)h * 256;
+  return a;
+}
+
 extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   const int dv = head_dim_v_of(p);
-  const bool dims_ok = (p->head_dim == dv && (dv == 64 || dv == 128 || dv == 256)) ||
-                       (p->head_dim == 128 && dv == 256) || (p->head_dim == 256 && dv == 128);
+  // The reference's compiled prefill head dims (tests/softmax_attention/
+  // test_prefill.py:52,205-208: 64, 96, 128, 192, 256; head_dim_v 256 or 512
+  // at 64, 128 at 192) plus 128/256 and 256/128.
+  const int d = p->head_dim;
+  const bool dims_ok = (d == dv && (dv == 64 || dv == 96 || dv == 128 || dv == 192 || dv == 256)) ||
+                       (d == 128 && dv == 256) || (d == 256 && dv == 128) ||
+                       (d == 192 && dv == 128) || (d == 64 && (dv == 256 || dv == 512));
   FW_REQUIRE(dims_ok, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 prefill kernels take head_dim / head_dim_v 64/64, 128/128, 256/256,"
-             " 128/256 or 256/128; got %d/%d", p->head_dim, dv);
+             "the gfx950 prefill kernels take head_dim / head_dim_v 64/64, 96/96, 128/128,"
+             " 192/192, 256/256, 128/256, 256/128, 192/128, 64/256 or 64/512; got %d/%d",
+             p->head_dim, dv);
   FW_REQUIRE(p->kv_mode != FW_KV_PAGED || dv == p->head_dim, FW_ERR_VALUE,
              "a paged pool has one head dim; got head_dim %d, head_dim_v %d", p->head_dim, dv);
+  FW_REQUIRE(p->kv_mode != FW_KV_PAGED || d == 64 || d == 128 || d == 256, FW_ERR_NOT_IMPLEMENTED,
+             "a paged pool takes head_dim 64, 128 or 256; got %d", d);
   FW_REQUIRE(!p->rotary_cos || p->head_dim == dv, FW_ERR_NOT_IMPLEMENTED,
              "the fused RoPE takes head_dim_v == head_dim; got %d/%d", p->head_dim, dv);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
@@ -1884,8 +1906,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    launch_mode<FW_KV_DENSE>(a, dim3(a.n_qt * p->batch * head_groups), p->kv_dtype, p->head_dim,
-                             dv, s);
+    for (int half = 0; half < (dv == 512 ? 2 : 1); ++half)
+      launch_mode<FW_KV_DENSE>(v_half(a, half), dim3(a.n_qt * p->batch * head_groups), p->kv_dtype,
+                               p->head_dim, min(dv, 256), s);
     return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -1915,7 +1938,11 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (st != FW_OK) return st;
   // one workgroup per (schedule slot, head group); see sched_slot
   dim3 grid(max_tiles * head_groups);
-  if (p->kv_mode == FW_KV_VARLEN) launch_mode<FW_KV_VARLEN>(a, grid, FW_BF16, p->head_dim, dv, s);
-  else launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, dv, s);
+  if (p->kv_mode == FW_KV_VARLEN) {
+    for (int half = 0; half < (dv == 512 ? 2 : 1); ++half)
+      launch_mode<FW_KV_VARLEN>(v_half(a, half), grid, FW_BF16, p->head_dim, min(dv, 256), s);
+  } else {
+    launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, dv, s);
+  }
   return check_launch("fw_prefill");
 }

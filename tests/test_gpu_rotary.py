@@ -180,10 +180,10 @@ def test_paged_rotary_q_at_cache_positions(interleaved):
         assert_lse(lse.cpu().numpy(), rl)
 
 
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [64, 96, 192, 256])
 @pytest.mark.parametrize("interleaved", [False, True])
 def test_rotate_rows_bitexact_head_dims(d, interleaved):
-    """fw_rotary at head_dim 64 and 256 (tables of d/2 columns): dense rows at
+    """fw_rotary at head_dims other than 128 (tables of d/2 columns): dense rows at
     t + offset and packed rows with kv bases, bit-exact."""
     announce(f"fw_rotary d{d} interleaved={interleaved}")
     rng = np.random.default_rng(45 + d)
@@ -205,11 +205,11 @@ def test_rotate_rows_bitexact_head_dims(d, interleaved):
     np.testing.assert_array_equal(codes_of(y).reshape(total, 2, d), T.bf16_round(want))
 
 
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [64, 96, 192, 256])
 @pytest.mark.parametrize("interleaved,rotary_k,f32", [(False, True, False), (True, True, True),
                                                       (False, False, True)])
 def test_flash_attn_func_rotary_head_dims(d, interleaved, rotary_k, f32):
-    """Fused Q RoPE in the head_dim-64 (register-staged) and head_dim-256
+    """Fused Q RoPE in the register-staged (64, 96, 192) and head_dim-256
     kernels, K through fw_rotary: against rotate-then-attend."""
     announce(f"dense rotary d{d} il={interleaved} rk={rotary_k} f32={f32}")
     rng = np.random.default_rng(46 + d)

@@ -108,10 +108,16 @@ def test_capi_validation_status_codes():
     assert lib.fw_paged_decode_workspace_bytes(p) > 0
     assert lib.fw_paged_decode(p, None) == N.FW_ERR_VALUE  # no workspace
     q = N.PrefillParams()
-    q.kv_mode, q.head_dim, q.nheads, q.nheads_k = N.FW_KV_DENSE, 96, 4, 2
+    q.kv_mode, q.head_dim, q.nheads, q.nheads_k = N.FW_KV_DENSE, 160, 4, 2
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
-    q.head_dim, q.head_dim_v = 64, 128  # d64 takes head_dim_v 64 only
+    q.head_dim, q.head_dim_v = 64, 128  # d64 takes head_dim_v 64, 256 or 512
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
+    for d, dv in ((96, 96), (192, 192), (192, 128), (64, 256), (64, 512)):
+        q.head_dim, q.head_dim_v = d, dv
+        assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE  # supported dims; no tensors
+    q.head_dim, q.head_dim_v, q.kv_mode = 96, 0, N.FW_KV_PAGED  # pools: 64, 128, 256
+    assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
+    q.kv_mode = N.FW_KV_DENSE
     q.head_dim, q.head_dim_v, q.kv_mode = 128, 256, N.FW_KV_PAGED  # one head dim in a pool
     assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE
     q.kv_mode, q.head_dim_v = N.FW_KV_DENSE, 0
@@ -130,9 +136,9 @@ def test_capi_validation_status_codes():
     bw.nheads, bw.nheads_k, bw.seqlen_k = 16, 2, 520  # few key tiles: heads split, partials
     assert lib.fw_attn_bwd_workspace_bytes(bw) > 2 * 2 * 520 * 128 * 4
     r = N.RotaryParams()
-    r.head_dim, r.table_rows = 96, 8
-    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED  # head dims 64, 128, 256
-    for d in (64, 128, 256):
+    r.head_dim, r.table_rows = 160, 8
+    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED  # head dims 64, 96, 128, 192, 256
+    for d in (64, 96, 128, 192, 256):
         r.head_dim = d
         assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
 
