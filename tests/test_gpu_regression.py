@@ -1,0 +1,270 @@
+"""GPU counterparts of the reference's regression tests
+(tests/softmax_attention/test_regression.py) that pin behaviour rather than a
+TPU compile detail: scale arguments given as 0-d arrays, sinks far above the
+scores, -inf sinks, padding rows with sinks, a contiguous cache appended step
+after step, block tables that change between calls and rows ending around
+block boundaries of a padded table.  Each compares the HIP path with the
+NumPy oracle (or with the same call without the feature, where the reference
+does)."""
+
+import numpy as np
+import pytest
+import torch
+
+from flywheel_tpu import flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache
+from oracle import attention as A
+from oracle import dtypes as T
+from tests.gpu_util import (DEV, PagedCase, announce, assert_close, assert_lse, codes_of,
+                            dev_from_codes, random_codes, randn, to_dev_bf16)
+
+pytestmark = pytest.mark.gpu
+
+
+def head_major(x):  # (B, S, H, D) <-> (B, H, S, D)
+    return np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+
+
+def packed(rng, seqlens, h, hk, d):
+    cu = np.concatenate([[0], np.cumsum(seqlens)]).astype(np.int32)
+    return cu, randn(rng, (cu[-1], h, d)), randn(rng, (cu[-1], hk, d)), randn(rng, (cu[-1], hk, d))
+
+
+def heads_first(x):  # (T, H, D) -> (H, T, D)
+    return np.ascontiguousarray(x.transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("entry", ["dense", "varlen"])
+@pytest.mark.parametrize("array_type", ["numpy", "torch"])
+def test_array_softmax_scale(entry, array_type):
+    """test_regression.py:235-270: a concrete 0-d array scale gives the result
+    of the float it holds, bit for bit."""
+    announce(f"array softmax_scale {entry} {array_type}")
+    rng = np.random.default_rng(120)
+    d = 128
+    scale = np.asarray(np.float32(1.0) / np.sqrt(np.float32(d)))
+    arr = scale if array_type == "numpy" else torch.tensor(scale)
+    seqlens = [100, 156]
+    cu, q, k, v = packed(rng, seqlens, 2, 2, d)
+
+    def attend(softmax_scale):
+        if entry == "dense":
+            return flash_attn_func(to_dev_bf16(head_major(q[None])), to_dev_bf16(head_major(k[None])),
+                                   to_dev_bf16(head_major(v[None])), causal=True,
+                                   softmax_scale=softmax_scale)
+        c = torch.tensor(cu, device=DEV)
+        return flash_attn_varlen_func(to_dev_bf16(heads_first(q)), to_dev_bf16(heads_first(k)),
+                                      to_dev_bf16(heads_first(v)), c, c, max(seqlens), max(seqlens),
+                                      causal=True, softmax_scale=softmax_scale)
+
+    want = attend(float(scale))
+    got = attend(arr)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def _contig_decode(q, k_cache, v_cache, lens, sinks=None):
+    res = flash_attn_with_kvcache(
+        to_dev_bf16(q), to_dev_bf16(k_cache), to_dev_bf16(v_cache),
+        cache_seqlens=torch.tensor(lens, dtype=torch.int32, device=DEV), return_softmax_lse=True,
+        learnable_sink=None if sinks is None else torch.tensor(sinks, device=DEV))
+    torch.cuda.synchronize()
+    return res[0].float().cpu().numpy(), res[1].cpu().numpy()
+
+
+@pytest.mark.parametrize("entry", ["dense", "varlen", "decode"])
+def test_sinks_far_above_the_scores(entry):
+    """test_regression.py:608-670: q = -2.5 against k = +2.5 scores about
+    -70.7 at d 128, so sinks of 20 and 40 sit far above the anchor; lse must
+    stay finite and out / lse match the oracle."""
+    announce(f"sinks far above the scores: {entry}")
+    rng = np.random.default_rng(121)
+    sinks = np.array([20.0, 40.0, 20.0, 40.0], np.float32)
+    h, hk, d = 4, 2, 128
+    if entry == "decode":
+        cap = 256
+        q = np.full((2, 1, h, d), -2.5, np.float32)
+        kc = np.full((2, cap, hk, d), 2.5, np.float32)
+        vc = T.bf16_to_f32(random_codes(rng, (2, cap, hk, d), torch.bfloat16))
+        lens = np.array([100, 256], np.int32)
+        out, lse = _contig_decode(q, kc, vc, lens, sinks)
+        ro, rl = A.decode_reference(q, kc, vc, lens, cache_batch_idx=np.arange(2), sinks=sinks)
+    else:
+        s = 256
+        q = np.full((1, s, h, d), -2.5, np.float32)
+        k = np.full((1, s, hk, d), 2.5, np.float32)
+        v = randn(rng, (1, s, hk, d))
+        ro, rl = A.attention_ref(q, k, v, causal=True, sinks=sinks, round_scaled_q=True)
+        if entry == "dense":
+            o, l = flash_attn_func(to_dev_bf16(head_major(q)), to_dev_bf16(head_major(k)),
+                                   to_dev_bf16(head_major(v)), causal=True, return_softmax_lse=True,
+                                   learnable_sink=torch.tensor(sinks, device=DEV))
+            torch.cuda.synchronize()
+            out, lse = head_major(o.float().cpu().numpy()), l.cpu().numpy()
+        else:
+            c = torch.tensor([0, s], dtype=torch.int32, device=DEV)
+            o, l = flash_attn_varlen_func(to_dev_bf16(heads_first(q[0])), to_dev_bf16(heads_first(k[0])),
+                                          to_dev_bf16(heads_first(v[0])), c, c, s, s, causal=True,
+                                          return_softmax_lse=True,
+                                          learnable_sink=torch.tensor(sinks, device=DEV))
+            torch.cuda.synchronize()
+            out = o.float().cpu().numpy().transpose(1, 0, 2)[None]
+            lse = l.cpu().numpy()[None]
+    assert np.isfinite(lse).all()
+    assert_close(out, ro)
+    assert_lse(lse, rl)
+
+
+@pytest.mark.parametrize("entry", ["varlen", "decode"])
+def test_minus_inf_sinks_are_no_sink(entry):
+    """test_regression.py:672-735: a -inf sink adds nothing (the head matches
+    the call without sinks); a row with no key returns out 0 and lse -inf
+    under a -inf sink and lse = sink under a finite one, never NaN."""
+    announce(f"-inf sinks: {entry}")
+    rng = np.random.default_rng(122)
+    sinks = np.array([-np.inf, 2.0, -np.inf, 4.0], np.float32)
+    none_heads, sink_heads = np.array([0, 2]), np.array([1, 3])
+    h, hk, d = 4, 2, 128
+    if entry == "decode":
+        cap = 256
+        q = randn(rng, (2, 1, h, d))
+        kc = T.bf16_to_f32(random_codes(rng, (2, cap, hk, d), torch.bfloat16))
+        vc = T.bf16_to_f32(random_codes(rng, (2, cap, hk, d), torch.bfloat16))
+        lens = np.array([0, 200], np.int32)
+        out, lse = _contig_decode(q, kc, vc, lens, sinks)
+        plain_out, plain_lse = _contig_decode(q, kc, vc, lens)
+        # (B, 1, H, D) -> (H, B, D); lse (B, H, 1) -> (H, B)
+        out, plain_out = out[:, 0].swapaxes(0, 1), plain_out[:, 0].swapaxes(0, 1)
+        lse, plain_lse = lse[..., 0].T, plain_lse[..., 0].T
+        empty, keyed = np.array([0]), np.array([1])
+    else:
+        q = randn(rng, (128, h, d))
+        k, v = randn(rng, (80, hk, d)), randn(rng, (80, hk, d))
+        cu_q = torch.tensor([0, 64, 128], dtype=torch.int32, device=DEV)
+        cu_k = torch.tensor([0, 16, 80], dtype=torch.int32, device=DEV)
+        args = (to_dev_bf16(heads_first(q)), to_dev_bf16(heads_first(k)), to_dev_bf16(heads_first(v)),
+                cu_q, cu_k, 64, 64)
+        o, l = flash_attn_varlen_func(*args, causal=True, return_softmax_lse=True,
+                                      learnable_sink=torch.tensor(sinks, device=DEV))
+        po, pl = flash_attn_varlen_func(*args, causal=True, return_softmax_lse=True)
+        torch.cuda.synchronize()
+        out, plain_out = o.float().cpu().numpy(), po.float().cpu().numpy()  # (H, T, D)
+        lse, plain_lse = l.cpu().numpy(), pl.cpu().numpy()
+        # causal rows end on their bottom-right diagonal: the first 48 rows of
+        # the 64-row query against 16 keys see no key
+        empty, keyed = np.arange(48), np.arange(48, 128)
+    assert not np.isnan(out).any() and not np.isnan(lse).any()
+    assert np.all(out[:, empty] == 0)
+    assert np.all(lse[np.ix_(none_heads, empty)] == -np.inf)
+    np.testing.assert_allclose(lse[np.ix_(sink_heads, empty)],
+                               np.broadcast_to(sinks[sink_heads, None], (2, len(empty))))
+    np.testing.assert_allclose(out[np.ix_(none_heads, keyed)], plain_out[np.ix_(none_heads, keyed)],
+                               atol=1e-2)
+    np.testing.assert_allclose(lse[np.ix_(none_heads, keyed)], plain_lse[np.ix_(none_heads, keyed)],
+                               atol=1e-3)
+
+
+def test_varlen_padding_rows_ignore_sinks():
+    """test_regression.py:863-887: padding rows past cu_seqlens[-1] keep out 0
+    and lse -inf with sinks, even when their q is NaN."""
+    announce("varlen padding rows with sinks and NaN q")
+    rng = np.random.default_rng(123)
+    seqlens = [17, 40]
+    cu, q, k, v = packed(rng, seqlens, 4, 2, 128)
+    q = np.concatenate([q, np.full((23, 4, 128), np.nan, np.float32)])
+    k = np.concatenate([k, randn(rng, (23, 2, 128))])
+    v = np.concatenate([v, randn(rng, (23, 2, 128))])
+    c = torch.tensor(cu, device=DEV)
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(heads_first(q)), to_dev_bf16(heads_first(k)), to_dev_bf16(heads_first(v)), c, c,
+        40, 40, causal=True, return_softmax_lse=True,
+        learnable_sink=torch.tensor(rng.standard_normal(4).astype(np.float32), device=DEV))
+    torch.cuda.synchronize()
+    out, lse = out.float().cpu().numpy(), lse.cpu().numpy()
+    assert np.all(out[:, 57:] == 0)
+    assert np.all(lse[:, 57:] == -np.inf)
+    assert np.isfinite(out[:, :57]).all()
+
+
+@pytest.mark.parametrize("nheads,nheads_k,d", [(8, 1, 128), (6, 1, 256), (8, 2, 128)])
+def test_contiguous_cache_appends_step_after_step(nheads, nheads_k, d):
+    """test_regression.py:1185-1230: each step's append lands on the cache the
+    previous step returned; positions cross the cache's first rows and end at
+    its last slot."""
+    announce(f"contiguous append step after step h{nheads}/{nheads_k} d{d}")
+    rng = np.random.default_rng(124)
+    batch, cap = 2, 256
+    positions = [*range(0, 12), *range(cap - 8, cap)]
+    kc = random_codes(rng, (batch, cap, nheads_k, d), torch.bfloat16)
+    vc = random_codes(rng, (batch, cap, nheads_k, d), torch.bfloat16)
+    kc[:, positions] = 0
+    vc[:, positions] = 0
+    q = randn(rng, (batch, 1, nheads, d))
+    k_dev, v_dev = dev_from_codes(kc, torch.bfloat16), dev_from_codes(vc, torch.bfloat16)
+    exp_k, exp_v = kc.copy(), vc.copy()
+    rows = np.arange(batch)
+    for pos in positions:
+        kn = random_codes(rng, (batch, 1, nheads_k, d), torch.bfloat16)
+        vn = random_codes(rng, (batch, 1, nheads_k, d), torch.bfloat16)
+        lens = np.full(batch, pos, np.int32)
+        out, lse, k_dev, v_dev = flash_attn_with_kvcache(
+            to_dev_bf16(q), k_dev, v_dev, dev_from_codes(kn, torch.bfloat16),
+            dev_from_codes(vn, torch.bfloat16), cache_seqlens=torch.tensor(lens, device=DEV),
+            return_softmax_lse=True)
+        torch.cuda.synchronize()
+        exp_k[rows, pos], exp_v[rows, pos] = kn[:, 0], vn[:, 0]
+        np.testing.assert_array_equal(codes_of(k_dev), exp_k)
+        np.testing.assert_array_equal(codes_of(v_dev), exp_v)
+        ro, rl = A.decode_reference(q, T.bf16_to_f32(exp_k), T.bf16_to_f32(exp_v), lens + 1,
+                                    cache_batch_idx=rows)
+        assert_close(out.float().cpu().numpy(), ro, what=f"position {pos}")
+        assert_lse(lse.cpu().numpy(), rl)
+
+
+def test_block_table_changes_between_calls():
+    """test_regression.py:1233-1270: the table and lengths are runtime
+    operands; each append lands where its call's table says, and nothing else
+    in the pool changes."""
+    announce("paged append under two block tables")
+    batch, page, heads, d = 2, 128, 2, 128
+    pool = torch.zeros((4, page, 2 * heads, d), dtype=torch.bfloat16, device=DEV)
+    q = torch.ones((batch, 1, heads, d), dtype=torch.bfloat16, device=DEV)
+    k = torch.ones((batch, 1, heads, d), dtype=torch.bfloat16, device=DEV)
+    v = torch.full_like(k, 2.0)
+    calls = [(np.array([[0, 1], [2, 3]], np.int32), np.array([0, 129], np.int32)),
+             (np.array([[3, 2], [1, 0]], np.int32), np.array([130, 5], np.int32))]
+    for table, lens in calls:
+        _, pool = flash_attn_with_kvcache(q, pool, None, k, v,
+                                          cache_seqlens=torch.tensor(lens, device=DEV),
+                                          block_table=torch.tensor(table, device=DEV))
+        torch.cuda.synchronize()
+        p = pool.float().cpu().numpy()
+        for r in range(batch):
+            slot = p[table[r, lens[r] // page], lens[r] % page]
+            np.testing.assert_array_equal(slot[0::2], 1.0)
+            np.testing.assert_array_equal(slot[1::2], 2.0)
+    assert float(pool.float().abs().sum()) == 4 * heads * d * (1.0 + 2.0)
+
+
+def test_rows_around_block_boundaries_of_a_padded_table():
+    """test_regression.py:1272-1310: 9 pages of 128 tokens per row, rows ending
+    inside the first 1024 keys, on 1024, one past it and on the last real
+    page; append then attend, against the oracle."""
+    announce("paged decode, rows around 1024-key boundaries")
+    rng = np.random.default_rng(125)
+    lens = np.array([129, 1023, 1024, 1151], np.int32)
+    case = PagedCase(rng, batch=4, nheads=4, nheads_k=2, lengths=lens, new_tokens=[1] * 4,
+                     page_size=128, max_pages=9)
+    q = randn(rng, (4, 1, 4, 128))
+    shape = (4, 1, 2, 128)
+    out, lse, pool = flash_attn_with_kvcache(
+        to_dev_bf16(q), case.pool(), None, dev_from_codes(case.k_codes.reshape(shape), torch.bfloat16),
+        dev_from_codes(case.v_codes.reshape(shape), torch.bfloat16),
+        cache_seqlens=torch.tensor(lens, device=DEV), block_table=torch.tensor(case.table, device=DEV),
+        return_softmax_lse=True)
+    torch.cuda.synchronize()
+    after = case.expected_pool()
+    np.testing.assert_array_equal(codes_of(pool), after)
+    krows, vrows = case.rows(after)
+    ro, rl = A.kvcache_reference(q, krows, vrows, lens + 1)
+    assert_close(out.float().cpu().numpy(), ro)
+    assert_lse(lse.cpu().numpy(), rl)
