@@ -1,11 +1,12 @@
 """GPU counterparts of the reference's regression tests
-(tests/softmax_attention/test_regression.py) that pin behaviour rather than a
-TPU compile detail: scale arguments given as 0-d arrays, sinks far above the
-scores, -inf sinks, padding rows with sinks, a contiguous cache appended step
-after step, block tables that change between calls and rows ending around
-block boundaries of a padded table.  Each compares the HIP path with the
-NumPy oracle (or with the same call without the feature, where the reference
-does)."""
+(tests/softmax_attention/test_regression.py, and the packed-cache cases of
+test_paged.py) that pin behaviour rather than a TPU compile detail: scale
+arguments given as 0-d arrays, sinks far above the scores, -inf sinks, padding
+rows with sinks, a contiguous cache appended step after step, block tables that
+change between calls, rows ending around block boundaries of a padded table,
+read-only rows over empty caches, a shared prefix page and an allocation of
+padding rows only.  Each compares the HIP path with the NumPy oracle (or with
+the same call without the feature, where the reference does)."""
 
 import numpy as np
 import pytest
@@ -268,3 +269,80 @@ def test_rows_around_block_boundaries_of_a_padded_table():
     ro, rl = A.kvcache_reference(q, krows, vrows, lens + 1)
     assert_close(out.float().cpu().numpy(), ro)
     assert_lse(lse.cpu().numpy(), rl)
+
+
+def _extend(case, q, cu, prefix, *, causal, append, max_q):
+    """flash_attn_with_kvcache over the case's pool with a packed q: append the
+    case's new rows (k / v padded like q) or read only."""
+    kw = {}
+    if append:
+        pad = q.shape[0] - case.k_codes.shape[0]
+        z = np.zeros((pad,) + case.k_codes.shape[1:], case.k_codes.dtype)
+        kw = dict(k=dev_from_codes(np.concatenate([case.k_codes, z]), case.dtype),
+                  v=dev_from_codes(np.concatenate([case.v_codes, z]), case.dtype))
+    pool = case.pool()
+    out, lse, pool2 = flash_attn_with_kvcache(
+        to_dev_bf16(q), pool, None, cache_seqlens=torch.tensor(prefix, dtype=torch.int32, device=DEV),
+        block_table=torch.tensor(case.table, device=DEV), cu_seqlens_q=torch.tensor(cu, device=DEV),
+        max_seqlen_q=max_q, causal=causal, return_softmax_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert pool2 is pool
+    return out.float().cpu().numpy(), lse.cpu().numpy(), codes_of(pool)
+
+
+def test_read_only_empty_cache_between_cached_requests():
+    """test_paged.py:483-495: read-only packed rows over empty caches (they
+    see no key and are not checked) between requests with cached keys."""
+    announce("read-only packed rows, empty caches between cached requests")
+    rng = np.random.default_rng(126)
+    qlens, prefix = np.array([4, 3, 9, 2]), np.array([0, 130, 0, 5])
+    case = PagedCase(rng, batch=4, nheads=4, nheads_k=2, lengths=prefix, new_tokens=[0] * 4,
+                     page_size=128)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = randn(rng, (cu[-1] + 5, 4, 128))
+    out, lse, pool = _extend(case, q, cu, prefix, causal=False, append=False, max_q=9)
+    np.testing.assert_array_equal(pool, case.pool_codes)
+    kp, vp = case.kv_pages(case.pool_codes)
+    ro, rl = A.ragged_reference(q, kp, vp, cu, prefix, case.table, causal=False,
+                                round_scaled_q=True)
+    for s in (1, 3):
+        rows = slice(cu[s], cu[s + 1])
+        assert_close(out[rows], ro[rows], what=f"request {s}")
+        assert_lse(lse[:, rows], rl[:, rows])
+    assert not np.abs(out[cu[-1]:]).any()
+
+
+def test_shared_read_only_prefix_and_private_append_pages():
+    """test_paged.py:498-510: two requests share their first page (a 128-token
+    prefix) and append to private pages."""
+    announce("shared prefix page, private append pages")
+    rng = np.random.default_rng(127)
+    qlens, prefix = np.array([2, 7]), np.array([128, 128])
+    case = PagedCase(rng, batch=2, nheads=4, nheads_k=2, lengths=prefix, new_tokens=qlens,
+                     page_size=128)
+    case.table[1, 0] = case.table[0, 0]
+    q = randn(rng, (int(qlens.sum()), 4, 128))
+    out, lse, pool = _extend(case, q, case.cu, prefix, causal=True, append=True, max_q=7)
+    after = case.expected_pool()
+    np.testing.assert_array_equal(pool, after)
+    kp, vp = case.kv_pages(after)
+    ro, rl = A.ragged_reference(q, kp, vp, case.cu, prefix + qlens, case.table, causal=True,
+                                round_scaled_q=True)
+    assert_close(out, ro)
+    assert_lse(lse, rl)
+
+
+@pytest.mark.parametrize("append", [False, True])
+def test_empty_packed_allocation(append):
+    """test_paged.py:512-525: every request has zero q rows, so the buffer
+    holds packed padding only: out 0, lse -inf, the pool unchanged."""
+    announce(f"empty packed allocation append={append}")
+    rng = np.random.default_rng(128)
+    case = PagedCase(rng, batch=2, nheads=4, nheads_k=2, lengths=[0, 0], new_tokens=[0, 0],
+                     page_size=128)
+    q = randn(rng, (8, 4, 128))
+    out, lse, pool = _extend(case, q, case.cu, np.array([0, 0]), causal=True, append=append,
+                             max_q=1)
+    np.testing.assert_array_equal(pool, case.pool_codes)
+    assert not np.abs(out).any()
+    assert np.all(lse == -np.inf)
