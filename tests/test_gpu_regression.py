@@ -4,8 +4,9 @@ test_paged.py) that pin behaviour rather than a TPU compile detail: scale
 arguments given as 0-d arrays, sinks far above the scores, -inf sinks, padding
 rows with sinks, a contiguous cache appended step after step, block tables that
 change between calls, rows ending around block boundaries of a padded table,
-read-only rows over empty caches, a shared prefix page and an allocation of
-padding rows only.  Each compares the HIP path with the NumPy oracle (or with
+read-only rows over empty caches, a shared prefix page, an allocation of
+padding rows only, and the static anchor overtaken by a later tile (by ~500
+log2 units, and on the last live tile).  Each compares the HIP path with the NumPy oracle (or with
 the same call without the feature, where the reference does)."""
 
 import numpy as np
@@ -346,3 +347,72 @@ def test_empty_packed_allocation(append):
     np.testing.assert_array_equal(pool, case.pool_codes)
     assert not np.abs(out).any()
     assert np.all(lse == -np.inf)
+
+
+def _merged_pool(kp, vp):
+    """(pages, page, Hk, D) K and V values -> the merged bf16 pool [k0, v0, ...]."""
+    pages, page, hk, d = kp.shape
+    m = np.empty((pages, page, 2 * hk, d), np.float32)
+    m[:, :, 0::2], m[:, :, 1::2] = kp, vp
+    return to_dev_bf16(m)
+
+
+def test_later_block_raises_anchor_paged():
+    """test_paged.py:667-689: cached keys jump from 0 to 32 at position 1024,
+    so later tiles score hundreds of log2 units above the anchor the first
+    ones set; the kernel must rescale instead of overflowing (out ~ 3)."""
+    announce("paged chunk: a later block raises the anchor by ~500 log2 units")
+    rng = np.random.default_rng(129)
+    page, hk, h, d, prefix, qlen = 128, 2, 4, 128, 2048, 64
+    table = rng.permutation(32).astype(np.int32)[None]
+    kp = np.zeros((32, page, hk, d), np.float32)
+    vp = np.ones((32, page, hk, d), np.float32)
+    late = table[0, 1024 // page:]
+    kp[late], vp[late] = 32.0, 3.0
+    q = np.ones((qlen, h, d), np.float32)
+    kn, vn = np.full((qlen, hk, d), 32.0, np.float32), np.full((qlen, hk, d), 3.0, np.float32)
+    out, pool = flash_attn_with_kvcache(
+        to_dev_bf16(q), _merged_pool(kp, vp), None, to_dev_bf16(kn), to_dev_bf16(vn),
+        cache_seqlens=torch.tensor([prefix], dtype=torch.int32, device=DEV),
+        block_table=torch.tensor(table, device=DEV),
+        cu_seqlens_q=torch.tensor([0, qlen], dtype=torch.int32, device=DEV), max_seqlen_q=qlen,
+        causal=True)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert np.isfinite(o).all()
+    np.testing.assert_allclose(o, 3.0, atol=2e-2)
+    ro, _ = A.ragged_reference(q, kp, vp, np.array([0, qlen]), np.array([prefix + qlen]), table,
+                               causal=True, round_scaled_q=True)
+    assert_close(o, ro)
+
+
+def test_overflow_guard_at_the_last_live_kv_tile():
+    """test_paged.py:978-1010: keys [0, 512) score 0 and keys [512, 600) about
+    200 nats; rows past 512 anchor on the first tiles and overflow on the last
+    live one (600 tokens appended to an empty 16-page pool, causal)."""
+    announce("paged chunk: overflow on the last live kv tile")
+    length, hk, h, d, pages, page = 600, 2, 4, 128, 16, 128
+    mag = np.sqrt(200.0 * np.sqrt(d))
+    q = np.zeros((length, h, d), np.float32)
+    q[:, :, 0] = mag
+    k = np.zeros((length, hk, d), np.float32)
+    k[512:, :, 0] = mag
+    v = np.where(np.arange(length)[:, None, None] < 512, 1.0, 3.0) * np.ones((length, hk, d), np.float32)
+    q, k, v = (T.bf16(x) for x in (q, k, v))
+    table = np.arange(pages, dtype=np.int32)[None]
+    zeros = np.zeros((pages, page, hk, d), np.float32)
+    out, lse, pool = flash_attn_with_kvcache(
+        to_dev_bf16(q), _merged_pool(zeros, zeros), None, to_dev_bf16(k), to_dev_bf16(v),
+        cache_seqlens=torch.tensor([0], dtype=torch.int32, device=DEV),
+        block_table=torch.tensor(table, device=DEV),
+        cu_seqlens_q=torch.tensor([0, length], dtype=torch.int32, device=DEV),
+        max_seqlen_q=length, causal=True, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    kp, vp = zeros.copy(), zeros.copy()
+    kp.reshape(-1, hk, d)[:length], vp.reshape(-1, hk, d)[:length] = k, v
+    o = out.float().cpu().numpy()
+    assert np.isfinite(o).all()
+    ro, rl = A.ragged_reference(q, kp, vp, np.array([0, length]), np.array([length]), table,
+                                causal=True, round_scaled_q=True)
+    assert_close(o, ro)
+    assert_lse(lse.cpu().numpy(), rl)
