@@ -4,7 +4,9 @@ Mirrors the reference's differentiation rules (flywheel_tpu/softmax_attention/
 autograd.py:27-109): the dense MHA / GQA / MQA forward with a causal or full
 mask has a backward (flash_attn_bwd, kernels/bwd.py:463); every other
 configuration runs its forward and raises NotImplementedError, naming the
-feature, only when a gradient is requested.  lse carries no gradient of its own.
+feature, only when a gradient is requested.  Head dims 64 and 96 go through the
+head-dim-128 kernels on zero-padded operands (attn_bwd_padded); 192, 256 and
+head_dim_v != head_dim are forward-only.  lse carries no gradient of its own.
 """
 
 import torch
@@ -34,6 +36,27 @@ def attn_bwd(q, k, v, out, dout, lse, *, qs, ks, ls, batch, nheads, nheads_k, se
     return dq, dk, dv
 
 
+def _pad_heads(x, d):
+    """x (contiguous, head dim d innermost) as (rows, 128) with each d-vector
+    zero-padded to 128."""
+    return torch.nn.functional.pad(x.reshape(-1, d), (0, 128 - d))
+
+
+def attn_bwd_padded(q, k, v, out, dout, lse, *, head_dim, qs, ks, **geometry):
+    """The backward at a head dim below 128 (q, k and v share it) through the
+    head-dim-128 kernels: every d-vector of q, k, v, out and dout is
+    zero-padded to 128.  The scores, the softmax (the scale stays the caller's)
+    and rowsum(dout * out) are unchanged by the zero dims, and the padded
+    columns of dq, dk and dv come out zero, so the first d columns are the
+    gradients.  The strides of contiguous d-innermost layouts scale by 128 / d."""
+    d = head_dim
+    padded = [_pad_heads(t, d) for t in (q, k, v, out, dout)]
+    scale = lambda st: tuple(x // d * 128 for x in st)
+    dq, dk, dv = attn_bwd(*padded[:3], padded[3], padded[4], lse, qs=scale(qs), ks=scale(ks),
+                          **geometry)
+    return tuple(g[:, :d].reshape(t.shape) for g, t in ((dq, q), (dk, k), (dv, v)))
+
+
 class FlashAttnFunction(torch.autograd.Function):
     """forward(q, k, v, spec) -> (out, lse); spec holds the launch closure, the
     geometry for the backward and, for forward-only configurations, the
@@ -53,8 +76,12 @@ class FlashAttnFunction(torch.autograd.Function):
         if spec["forward_only"]:
             raise NotImplementedError(spec["forward_only"])
         q, k, v, out, lse = ctx.saved_tensors
-        g = spec["geometry"]
-        dq, dk, dv = attn_bwd(q, k, v, out, dout.contiguous(), lse, **g)
+        g = dict(spec["geometry"])
+        d = g.pop("head_dim", 128)
+        if d == 128:
+            dq, dk, dv = attn_bwd(q, k, v, out, dout.contiguous(), lse, **g)
+        else:
+            dq, dk, dv = attn_bwd_padded(q, k, v, out, dout.contiguous(), lse, head_dim=d, **g)
         return dq, dk, dv, None
 
 

@@ -255,8 +255,8 @@ def flash_attn_func(
         else:
             unsupported = ("window_size" if window_size != (-1, -1) else
                            "softcap" if softcap != 0.0 else
-                           f"head_dim {d}" if d != 128 else
-                           f"head_dim_v {dv}" if dv != 128 else None)
+                           f"head_dim_v {dv}" if dv != d else
+                           f"head_dim {d}" if d not in (64, 96, 128) else None)
             if unsupported:
                 reason = (f"The backward kernel does not support {unsupported}; that"
                           " configuration is forward-only.")
@@ -265,7 +265,8 @@ def flash_attn_func(
             "forward_only": reason,
             "geometry": dict(qs=qs, ks=ks, ls=(nheads * seqlen_q, seqlen_q), batch=batch,
                              nheads=nheads, nheads_k=nheads_k, seqlen_q=seqlen_q,
-                             seqlen_k=seqlen_k, softmax_scale=softmax_scale, causal=causal),
+                             seqlen_k=seqlen_k, softmax_scale=softmax_scale, causal=causal,
+                             head_dim=d),
         }
         out, lse = B.FlashAttnFunction.apply(q, k, v, spec)
     if return_softmax_lse:

@@ -117,3 +117,37 @@ def test_varlen_is_forward_only():
                                  seqused_k=torch.tensor([20, 30], dtype=torch.int32, device=DEV))
     with pytest.raises(NotImplementedError, match="forward-only"):
         out.sum().backward()
+
+
+@pytest.mark.parametrize("d", [64, 96])
+@pytest.mark.parametrize("b,h,hk,sq,sk,causal", [(2, 4, 2, 200, 333, True), (1, 4, 4, 150, 300, False),
+                                                 (1, 4, 1, 333, 200, True)])
+def test_backward_small_head_dims(d, b, h, hk, sq, sk, causal):
+    """Head dims 64 and 96 (the reference's compiled set, test_prefill.py:52,
+    285-333) through the head-dim-128 kernels on zero-padded operands."""
+    what = f"bwd d{d} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+    announce(what)
+    rng = np.random.default_rng(63 + d)
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, d))
+    do = randn(rng, (b, sq, h, d))
+    check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
+
+
+def test_backward_token_major_d64():
+    """The reference's paired token-major d64 form (MHA, even head count)."""
+    announce("bwd token-major d64")
+    rng = np.random.default_rng(65)
+    q, k, v = randn(rng, (2, 140, 4, 64)), randn(rng, (2, 140, 4, 64)), randn(rng, (2, 140, 4, 64))
+    do = randn(rng, (2, 140, 4, 64))
+    check_grads(run(q, k, v, do, True, token_major=True), q, k, v, do, True, "token-major d64")
+
+
+@pytest.mark.parametrize("d,dv,msg", [(256, 256, "head_dim 256"), (192, 128, "head_dim_v 128"),
+                                      (64, 256, "head_dim_v 256")])
+def test_backward_large_head_dims_are_forward_only(d, dv, msg):
+    announce(f"bwd d{d}/{dv} forward-only")
+    rng = np.random.default_rng(66)
+    x = lambda *s: to_dev_bf16(randn(rng, s)).requires_grad_()
+    out = flash_attn_func(x(1, 2, 64, d), x(1, 2, 64, d), x(1, 2, 64, dv), causal=True)
+    with pytest.raises(NotImplementedError, match=msg):
+        out.sum().backward()
