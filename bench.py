@@ -757,8 +757,8 @@ def main():
         "ms_per_step": round(head["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
-        # a published reference number for this exact shape and metric
-        # (the d256 extras), else None
+        # a published reference number for this exact shape and metric (the
+        # d256 extras, docs/v7x.md:60,165 of the reference), else None
         "vs_baseline": head.get("vs_baseline"),
         "dtype": head["dtype"],
         "data": "synthetic (seeded N(0,1) inputs resident in HBM)",
