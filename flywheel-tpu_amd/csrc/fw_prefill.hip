@@ -1768,9 +1768,11 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 
 // Kernel choice (the host has checked the head dims): 128/128 -> the ping-pong
 // kernel, 256/256 -> the d256 kernel (fp8 pools widened as they land in LDS in
-// both), everything else (head dims 64, 96, 192, head_dim_v != head_dim) ->
-// the register-staged kernel.  head_dim_v 512 (with head dim 64) runs as two
-// launches of head_dim_v 256 over the two halves of v and out.
+// both), everything else (head dims 64, 96, 192, 384, 512, head_dim_v !=
+// head_dim) -> the register-staged kernel.  A head_dim_v above 256 runs as
+// launches over chunks of v and out, which keeps O within one wave's
+// registers: 256 dims each at head dim 64, 128 each at head dims 384 and 512
+// (whose Q^T operand alone takes 96-128 registers).
 template <int MODE, int KV, int D, int DV>
 static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
   fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
@@ -1792,8 +1794,10 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
       else if (d == 256) launch_staged<MODE, FW_BF16, 256, 128>(a, grid, s);
       else if (d == 64) launch_staged<MODE, FW_BF16, 64, 256>(a, grid, s);  // dv 256, or a half of 512
       else if (d == 96) launch_staged<MODE, FW_BF16, 96, 96>(a, grid, s);
-      else if (dv == 192) launch_staged<MODE, FW_BF16, 192, 192>(a, grid, s);
-      else launch_staged<MODE, FW_BF16, 192, 128>(a, grid, s);
+      else if (d == 192 && dv == 192) launch_staged<MODE, FW_BF16, 192, 192>(a, grid, s);
+      else if (d == 192) launch_staged<MODE, FW_BF16, 192, 128>(a, grid, s);
+      else if (d == 384) launch_staged<MODE, FW_BF16, 384, 128>(a, grid, s);
+      else launch_staged<MODE, FW_BF16, 512, 128>(a, grid, s);
     }
     return;
   }
@@ -1815,26 +1819,32 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
   }
 }
 
-// Half h (0 or 1) of a head_dim_v-512 call: dims 256h .. 256h + 255 of v and
-// out.  Both halves compute the same scores and write the same lse.
-static PrefillArgs v_half(PrefillArgs a, int h) {
-  a.v += (size_t)h * 256 * 2;
-  a.out += (size_t)h * 256;
+// Chunk c (of width w) of a call whose head_dim_v exceeds 256: dims wc .. wc +
+// w - 1 of v and out.  Every chunk computes the same scores and writes the
+// same lse.
+static PrefillArgs v_chunk(PrefillArgs a, int c, int w) {
+  a.v += (size_t)c * w * 2;
+  a.out += (size_t)c * w;
   return a;
 }
+// Width of those chunks: 256 at head dim 64, else 128 (or dv itself up to 256).
+static int v_chunk_width(int d, int dv) { return dv <= 256 ? dv : d == 64 ? 256 : 128; }
 
 extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   const int dv = head_dim_v_of(p);
   // The reference's compiled prefill head dims (tests/softmax_attention/
   // test_prefill.py:52,205-208: 64, 96, 128, 192, 256; head_dim_v 256 or 512
-  // at 64, 128 at 192) plus 128/256 and 256/128.
+  // at 64, 128 at 192), 384 and 512 (multiples of 128, inputs.py:100-140),
+  // plus 128/256 and 256/128.
   const int d = p->head_dim;
-  const bool dims_ok = (d == dv && (dv == 64 || dv == 96 || dv == 128 || dv == 192 || dv == 256)) ||
+  const bool dims_ok = (d == dv && (dv == 64 || dv == 96 || dv == 128 || dv == 192 || dv == 256 ||
+                                    dv == 384 || dv == 512)) ||
                        (d == 128 && dv == 256) || (d == 256 && dv == 128) ||
                        (d == 192 && dv == 128) || (d == 64 && (dv == 256 || dv == 512));
   FW_REQUIRE(dims_ok, FW_ERR_NOT_IMPLEMENTED,
              "the gfx950 prefill kernels take head_dim / head_dim_v 64/64, 96/96, 128/128,"
-             " 192/192, 256/256, 128/256, 256/128, 192/128, 64/256 or 64/512; got %d/%d",
+             " 192/192, 256/256, 384/384, 512/512, 128/256, 256/128, 192/128, 64/256 or 64/512;"
+             " got %d/%d",
              p->head_dim, dv);
   FW_REQUIRE(p->kv_mode != FW_KV_PAGED || dv == p->head_dim, FW_ERR_VALUE,
              "a paged pool has one head dim; got head_dim %d, head_dim_v %d", p->head_dim, dv);
@@ -1906,9 +1916,10 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
-    for (int half = 0; half < (dv == 512 ? 2 : 1); ++half)
-      launch_mode<FW_KV_DENSE>(v_half(a, half), dim3(a.n_qt * p->batch * head_groups), p->kv_dtype,
-                               p->head_dim, min(dv, 256), s);
+    const int w = v_chunk_width(d, dv);
+    for (int c = 0; c * w < dv; ++c)
+      launch_mode<FW_KV_DENSE>(v_chunk(a, c, w), dim3(a.n_qt * p->batch * head_groups), p->kv_dtype,
+                               p->head_dim, w, s);
     return check_launch("fw_prefill");
   }
   FW_REQUIRE(p->cu_seqlens_q && p->workspace, FW_ERR_VALUE, "cu_seqlens_q and workspace required");
@@ -1939,8 +1950,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   // one workgroup per (schedule slot, head group); see sched_slot
   dim3 grid(max_tiles * head_groups);
   if (p->kv_mode == FW_KV_VARLEN) {
-    for (int half = 0; half < (dv == 512 ? 2 : 1); ++half)
-      launch_mode<FW_KV_VARLEN>(v_half(a, half), grid, FW_BF16, p->head_dim, min(dv, 256), s);
+    const int w = v_chunk_width(d, dv);
+    for (int c = 0; c * w < dv; ++c)
+      launch_mode<FW_KV_VARLEN>(v_chunk(a, c, w), grid, FW_BF16, p->head_dim, w, s);
   } else {
     launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, dv, s);
   }

@@ -1,8 +1,8 @@
 // RoPE of bf16 rows at their prefill positions (f32 arithmetic, one rounding
 // to bf16), the rotation the reference applies to staged Q / K tiles:
 // prepare_rotary (flywheel_tpu/softmax_attention/rotary.py:27-167) and
-// rotate_tile (rotary.py:170-215), for head_dim D in {64, 96, 128, 192, 256}
-// (tables of D / 2 columns).  D / 16 threads per (row, head): thread i owns dims
+// rotate_tile (rotary.py:170-215), for head_dim D in {64, 96, 128, 192, 256,
+// 384, 512} (tables of D / 2 columns).  D / 16 threads per (row, head): thread i owns dims
 // 8i..8i+7 and D/2+8i..D/2+8i+7, which holds both partners of every pair in
 // either pairing (halves: d with d + D/2; interleaved: 2j with 2j+1).
 #include "fw_common.h"
@@ -116,8 +116,9 @@ using namespace fw;
 
 extern "C" int fw_rotary(const fw_rotary_params *p, fw_stream_t stream) {
   const int hd = p->head_dim;
-  FW_REQUIRE(hd == 64 || hd == 96 || hd == 128 || hd == 192 || hd == 256, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 rotary kernel takes head_dim 64, 96, 128, 192 or 256; got %d", hd);
+  FW_REQUIRE(hd == 64 || hd == 96 || hd == 128 || hd == 192 || hd == 256 || hd == 384 || hd == 512,
+             FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 rotary kernel takes head_dim 64, 96, 128, 192, 256, 384 or 512; got %d", hd);
   FW_REQUIRE(p->x && p->y && p->cos_table && p->sin_table, FW_ERR_VALUE,
              "x, y, cos_table and sin_table are required");
   FW_REQUIRE(p->table_rows > 0 && p->batch_rows >= 0 && p->nheads >= 0 && p->ntokens >= 0,
@@ -152,6 +153,8 @@ extern "C" int fw_rotary(const fw_rotary_params *p, fw_stream_t stream) {
   else if (hd == 96) fw_rotary_kernel<96><<<grid, 256, 0, st>>>(a);
   else if (hd == 128) fw_rotary_kernel<128><<<grid, 256, 0, st>>>(a);
   else if (hd == 192) fw_rotary_kernel<192><<<grid, 256, 0, st>>>(a);
-  else fw_rotary_kernel<256><<<grid, 256, 0, st>>>(a);
+  else if (hd == 256) fw_rotary_kernel<256><<<grid, 256, 0, st>>>(a);
+  else if (hd == 384) fw_rotary_kernel<384><<<grid, 256, 0, st>>>(a);
+  else fw_rotary_kernel<512><<<grid, 256, 0, st>>>(a);
   return check_launch("fw_rotary_kernel");
 }

@@ -108,7 +108,8 @@ def flash_attn_func(
     token-major (token_major=True): (batch, seqlen, nheads * head_dim) with
     head_dim given (v's head dim from its width); heads_outer_fold: (nheads,
     batch, seqlen, d).  d / dv: 64/64, 96/96, 128/128, 192/192, 256/256,
-    128/256, 256/128, 192/128, 64/256 or 64/512 (inputs.py:154-207; token-major 64 is the reference's paired form: MHA
+    384/384, 512/512, 128/256, 256/128, 192/128, 64/256 or 64/512
+    (inputs.py:154-207; token-major 64 is the reference's paired form: MHA
     with an even head count, inputs.py:106-147).  causal is bottom-right aligned: query i sees key j iff
     j <= i + seqlen_k - seqlen_q.  Rows with no reachable key return out 0 and
     lse -inf (or the sink).  lse (batch, nheads, seqlen_q) f32.

@@ -226,9 +226,10 @@ typedef struct fw_prefill_params {
   const float *v_descale_ptr;
   /* Head dim of v and out, 0 = head_dim (prefill.py's head_dim_v,
    * inputs.py:193-207).  head_dim / head_dim_v: 64/64, 96/96, 128/128,
-   * 192/192, 256/256, 128/256, 256/128, 192/128, 64/256 or 64/512 (the
-   * reference's compiled set, tests/softmax_attention/test_prefill.py:52,
-   * 205-208, plus 128/256 and 256/128); a paged pool has one head dim of 64,
+   * 192/192, 256/256, 384/384, 512/512, 128/256, 256/128, 192/128, 64/256 or
+   * 64/512 (the reference's compiled set, tests/softmax_attention/
+   * test_prefill.py:52,205-208, multiples of 128 up to 512, plus 128/256 and
+   * 256/128); a paged pool has one head dim of 64,
    * 128 or 256; the fused RoPE takes head_dim_v == head_dim. */
   int32_t head_dim_v;
 } fw_prefill_params;
@@ -303,7 +304,7 @@ typedef struct fw_rotary_params {
   int32_t batch_rows;   /* size of the b index (1 for packed layouts) */
   int32_t nheads;
   int32_t ntokens;
-  int32_t head_dim;     /* 64, 96, 128, 192 or 256 */
+  int32_t head_dim;     /* 64, 96, 128, 192, 256, 384 or 512 */
   int32_t table_rows;
   int32_t table_f32;
   int32_t interleaved;

@@ -246,10 +246,11 @@ def test_prefill_bitwise_repeat():
 
 # Head dims of q/k and v: the d256 kernel, the register-staged kernel at 64, 96
 # and 192 and with head_dim_v != head_dim (inputs.py:193-207); the reference's
-# compiled set (test_prefill.py:52,205-208) plus 128/256 and 256/128.  64/512
-# runs as two launches over the halves of v and out.
+# compiled set (test_prefill.py:52,205-208), 384 and 512 (multiples of 128,
+# inputs.py:100-140) plus 128/256 and 256/128.  A head_dim_v above 256 runs as
+# launches over chunks of v and out.
 HEAD_DIMS = [(256, 256), (64, 64), (128, 256), (256, 128), (96, 96), (192, 192), (192, 128),
-             (64, 256), (64, 512)]
+             (64, 256), (64, 512), (384, 384), (512, 512)]
 
 
 @pytest.mark.parametrize("d,dv", HEAD_DIMS)

@@ -180,7 +180,7 @@ def test_paged_rotary_q_at_cache_positions(interleaved):
         assert_lse(lse.cpu().numpy(), rl)
 
 
-@pytest.mark.parametrize("d", [64, 96, 192, 256])
+@pytest.mark.parametrize("d", [64, 96, 192, 256, 384, 512])
 @pytest.mark.parametrize("interleaved", [False, True])
 def test_rotate_rows_bitexact_head_dims(d, interleaved):
     """fw_rotary at head_dims other than 128 (tables of d/2 columns): dense rows at
@@ -205,7 +205,7 @@ def test_rotate_rows_bitexact_head_dims(d, interleaved):
     np.testing.assert_array_equal(codes_of(y).reshape(total, 2, d), T.bf16_round(want))
 
 
-@pytest.mark.parametrize("d", [64, 96, 192, 256])
+@pytest.mark.parametrize("d", [64, 96, 192, 256, 512])
 @pytest.mark.parametrize("interleaved,rotary_k,f32", [(False, True, False), (True, True, True),
                                                       (False, False, True)])
 def test_flash_attn_func_rotary_head_dims(d, interleaved, rotary_k, f32):

@@ -112,7 +112,7 @@ def test_capi_validation_status_codes():
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
     q.head_dim, q.head_dim_v = 64, 128  # d64 takes head_dim_v 64, 256 or 512
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED
-    for d, dv in ((96, 96), (192, 192), (192, 128), (64, 256), (64, 512)):
+    for d, dv in ((96, 96), (192, 192), (192, 128), (64, 256), (64, 512), (384, 384), (512, 512)):
         q.head_dim, q.head_dim_v = d, dv
         assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE  # supported dims; no tensors
     q.head_dim, q.head_dim_v, q.kv_mode = 96, 0, N.FW_KV_PAGED  # pools: 64, 128, 256
@@ -137,8 +137,8 @@ def test_capi_validation_status_codes():
     assert lib.fw_attn_bwd_workspace_bytes(bw) > 2 * 2 * 520 * 128 * 4
     r = N.RotaryParams()
     r.head_dim, r.table_rows = 160, 8
-    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED  # head dims 64, 96, 128, 192, 256
-    for d in (64, 96, 128, 192, 256):
+    assert lib.fw_rotary(r, None) == N.FW_ERR_NOT_IMPLEMENTED  # head dims 64 .. 512
+    for d in (64, 96, 128, 192, 256, 384, 512):
         r.head_dim = d
         assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
 
