@@ -151,3 +151,28 @@ def test_backward_large_head_dims_are_forward_only(d, dv, msg):
     out = flash_attn_func(x(1, 2, 64, d), x(1, 2, 64, d), x(1, 2, 64, dv), causal=True)
     with pytest.raises(NotImplementedError, match=msg):
         out.sum().backward()
+
+
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 256, 384, 512])
+def test_forward_backward_bitwise_repeat_head_dims(d):
+    """test_prefill.py:827-875's race check at each head dim: repeated calls
+    on the same inputs are bitwise equal (out, and dq / dk / dv where the
+    backward exists)."""
+    announce(f"repeat d{d}")
+    rng = np.random.default_rng(67)
+    grad = d in (64, 96, 128)
+    b, h, s = 2, 4, 384
+    q, k, v, do = (to_dev_bf16(randn(rng, (b, h, s, d))) for _ in range(4))
+
+    def once():
+        ts = [t.detach().clone().requires_grad_(grad) for t in (q, k, v)]
+        out = flash_attn_func(*ts, causal=True)
+        if grad:
+            out.backward(do)
+        torch.cuda.synchronize()
+        return [out.detach()] + ([t.grad for t in ts] if grad else [])
+
+    ref = once()
+    for _ in range(10):
+        for a, b_ in zip(once(), ref):
+            assert torch.equal(a, b_)
