@@ -35,7 +35,7 @@ def one_case(seed, kind, d=128):
     sinks = rng.standard_normal(h).astype(np.float32) if rng.random() < 0.2 else None
     if kind == 0:
         b = int(rng.integers(1, 3)); sq = int(rng.integers(1, 700)); sk = int(rng.integers(1, 700))
-        rope = rng.random() < 0.25 and softcap == 0.0 and d == 128
+        rope = rng.random() < 0.25 and softcap == 0.0
         if rope and sq > sk: sq = sk
         name = f"dense d{d} b{b} h{h}/{hk} sq{sq} sk{sk} c{causal} w{window} sc{softcap} sink{sinks is not None} rope{rope}"
         def f():
@@ -43,7 +43,7 @@ def one_case(seed, kind, d=128):
             kw = {}
             qr, kr = q, k
             if rope:
-                ang = rng.random((sk + 3, 64)) * 6.283
+                ang = rng.random((sk + 3, d // 2)) * 6.283
                 cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
                 kw = dict(rotary_cos=torch.tensor(cos, device=DEV), rotary_sin=torch.tensor(sin, device=DEV))
                 qp, kp = RO.dense_positions(sq, sk)
@@ -158,3 +158,13 @@ def test_random_case_head_dims(d, kind, seed):
     """The same draws at head_dim 64 (register-staged prefill kernel, decode)
     and 256 (the head_dim-256 prefill kernel over bf16 and fp8 pools, decode)."""
     one_case(5000 + 100 * d + 1000 * kind + seed, kind, d)
+
+
+@pytest.mark.parametrize("kind", range(2), ids=KINDS[:2])
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("d", [96, 192, 384, 512])
+def test_random_case_dense_head_dims(d, kind, seed):
+    """Dense and packed-varlen draws (with RoPE, windows, softcap, sinks) at
+    the head dims only those paths take: 96, 192 (register-staged kernel),
+    384 and 512 (head_dim_v in 128-dim launches)."""
+    one_case(9000 + 100 * d + 1000 * kind + seed, kind, d)
