@@ -188,6 +188,27 @@ def test_attention_ref_brute_force(sq, sk, causal, window, softcap, sinks):
     np.testing.assert_allclose(lse[0][fin], bl[fin], atol=2e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("d,dv", [(96, 96), (192, 128), (64, 256), (384, 384), (512, 512)])
+def test_attention_ref_head_dims_match_torch_sdpa(d, dv):
+    """The oracle at the prefill head-dim pairs the kernels take, including
+    head_dim_v != head_dim, against torch's float64 SDPA (bottom-right causal
+    with Sq < Sk)."""
+    rng = np.random.default_rng(9)
+    sq, sk = 24, 40
+    q = randn(rng, (1, sq, 4, d))
+    k = randn(rng, (1, sk, 2, d))
+    v = randn(rng, (1, sk, 2, dv))
+    out, lse = A.attention_ref(q, k, v, causal=True)
+    tq, tk, tv = (torch.from_numpy(x).permute(0, 2, 1, 3).double() for x in (q, k, v))
+    tk, tv = tk.repeat_interleave(2, dim=1), tv.repeat_interleave(2, dim=1)
+    mask = torch.arange(sk)[None, :] <= torch.arange(sq)[:, None] + (sk - sq)
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask)
+    np.testing.assert_allclose(out, ref.permute(0, 2, 1, 3).numpy(), atol=2e-5)
+    scores = (tq @ tk.transpose(-1, -2)) / math.sqrt(d)
+    want = torch.logsumexp(scores.masked_fill(~mask, -math.inf), dim=-1)
+    np.testing.assert_allclose(lse, want.numpy(), atol=2e-5, rtol=1e-5)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_ref_matches_torch_sdpa(causal):
     rng = np.random.default_rng(5)

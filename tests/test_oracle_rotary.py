@@ -25,31 +25,35 @@ def test_zero_angle_is_identity(interleaved):
     np.testing.assert_array_equal(y, x)
 
 
-def test_halves_pairing_is_complex_multiplication():
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 512])
+def test_halves_pairing_is_complex_multiplication(d):
     rng = np.random.default_rng(1)
-    x = _rand(rng, (2, 33, 128))
-    ang = rng.random((40, 64)) * 2 * np.pi
+    hd = d // 2
+    x = _rand(rng, (2, 33, d))
+    ang = rng.random((40, hd)) * 2 * np.pi
     cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
     pos = rng.integers(0, 40, 33)
-    z = (x[..., :64].astype(np.float64) + 1j * x[..., 64:]) * (
+    z = (x[..., :hd].astype(np.float64) + 1j * x[..., hd:]) * (
         cos[pos].astype(np.float64) + 1j * sin[pos])
     y = RO.rotate_f32(x, cos, sin, pos, False)
-    np.testing.assert_allclose(y[..., :64], z.real, atol=2e-6, rtol=1e-5)
-    np.testing.assert_allclose(y[..., 64:], z.imag, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(y[..., :hd], z.real, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(y[..., hd:], z.imag, atol=2e-6, rtol=1e-5)
     # |rotated pair| == |pair| (rotation).
-    np.testing.assert_allclose(np.hypot(y[..., :64], y[..., 64:]),
-                               np.hypot(x[..., :64], x[..., 64:]), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(np.hypot(y[..., :hd], y[..., hd:]),
+                               np.hypot(x[..., :hd], x[..., hd:]), rtol=1e-5, atol=1e-6)
 
 
-def test_interleaved_is_permuted_halves():
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 512])
+def test_interleaved_is_permuted_halves(d):
     rng = np.random.default_rng(2)
-    x = _rand(rng, (4, 17, 128))
-    ang = rng.random((30, 64)) * 2 * np.pi
+    hd = d // 2
+    x = _rand(rng, (4, 17, d))
+    ang = rng.random((30, hd)) * 2 * np.pi
     cos, sin = T.bf16(np.cos(ang)), T.bf16(np.sin(ang))
     pos = rng.integers(0, 30, 17)
-    # dim 2i of the interleaved head is dim i of the halves head, 2i+1 is i+64.
-    perm = np.empty(128, np.int64)
-    perm[0::2], perm[1::2] = np.arange(64), np.arange(64) + 64
+    # dim 2i of the interleaved head is dim i of the halves head, 2i+1 is i+d/2.
+    perm = np.empty(d, np.int64)
+    perm[0::2], perm[1::2] = np.arange(hd), np.arange(hd) + hd
     yi = RO.rotate(x[..., perm], cos, sin, pos, True)
     yh = RO.rotate(x, cos, sin, pos, False)
     np.testing.assert_array_equal(yi, yh[..., perm])
