@@ -14,6 +14,8 @@ before the timed region):
       -> TFLOP/s
   c5  fp8 e4m3 paged decode with a 4-token verify window, B=128,
       ctx U[4096, 65536] -> HBM GB/s
+  c2d256  the reference's published dense shape (docs/v7x.md:60): c2 at head_dim
+      256 -> TFLOP/s, vs_baseline against the published 653 TFLOP/s
 Extras (not in "all"): bwd (c2's shape through the dense backward), rope (c2
 with fused RoPE tables), copy (calibration of the HBM byte counters).
 The printed JSON line's headline is c2; with
@@ -49,6 +51,71 @@ def log(msg):
 
 
 BURN_IN_S = 1.0
+# MI355X's dense bf16 MFMA peak (2.5 PFLOP/s) is quoted at its peak engine
+# clock of 2400 MHz; frac_at_clock rescales the peak to the clock measured.
+PEAK_SCLK_MHZ = 2400.0
+
+
+class ClockSampler:
+    """Samples the GPU's engine (GFX) clock from amdsmi on a thread while the
+    timed step runs: start() before the burn-in's last half, stop() after the
+    timed loop.  The device is matched by PCI address to torch's cuda:0; with
+    amdsmi missing or unreadable every figure is None."""
+
+    def __init__(self, device):
+        self.handle = None
+        self.samples = []
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            props = torch.cuda.get_device_properties(device)
+            bdf = None
+            if hasattr(props, "pci_bus_id"):
+                bdf = (f"{getattr(props, 'pci_domain_id', 0):04x}:{props.pci_bus_id:02x}:"
+                       f"{getattr(props, 'pci_device_id', 0):02x}")
+            for h in handles:
+                if bdf and amdsmi.amdsmi_get_gpu_device_bdf(h).lower().startswith(bdf):
+                    self.handle = h
+            if self.handle is None and len(handles) == 1:
+                self.handle = handles[0]
+            self.amdsmi = amdsmi
+        except Exception as e:  # pragma: no cover - depends on the box
+            log(f"clock sampling unavailable: {e}")
+
+    def read(self):
+        return self.amdsmi.amdsmi_get_clock_info(
+            self.handle, self.amdsmi.AmdSmiClkType.SYS)["clk"]
+
+    def start(self):
+        import threading
+        self.samples, self.stop_flag = [], threading.Event()
+        if self.handle is None:
+            return
+        def run():
+            while not self.stop_flag.is_set():
+                try:
+                    self.samples.append(float(self.read()))
+                except Exception:  # pragma: no cover
+                    return
+                time.sleep(0.002)
+        self.thread = threading.Thread(target=run, daemon=True)
+        self.thread.start()
+
+    def stop(self):
+        if self.handle is None:
+            return None
+        self.stop_flag.set()
+        self.thread.join()
+        if not self.samples:
+            return None
+        v = np.array(self.samples)
+        return {"median": float(np.median(v)), "min": float(v.min()), "max": float(v.max()),
+                "n": int(v.size)}
+
+
+CLOCK = None  # the ClockSampler of the run, set in main()
+LAST_CLOCK = None  # engine clock statistics of the last timed() call
 
 
 def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
@@ -60,11 +127,18 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
     benchmarks/common/timing.py:33-35): the GPU's clocks ramp up over the
     first few hundred milliseconds of load, and timing before that measures
     the ramp, not the kernel."""
+    global LAST_CLOCK
     t0 = time.perf_counter()
+    sampling = False
     while time.perf_counter() - t0 < burn_in_s:
+        if CLOCK is not None and not sampling and time.perf_counter() - t0 > burn_in_s / 2:
+            CLOCK.start()
+            sampling = True
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
+    if CLOCK is not None and not sampling:
+        CLOCK.start()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -75,6 +149,7 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
         fn()
     end.record()
     torch.cuda.synchronize()
+    LAST_CLOCK = CLOCK.stop() if CLOCK is not None else None
     return start.elapsed_time(end) / steps
 
 
@@ -174,15 +249,16 @@ def workload_c2(args, device):
 
     def cpu():
         from oracle import attention as A
-        rng = np.random.default_rng(0)
-        heads = 8  # sample: 8 of the 32 heads (2 KV heads), full 4096 length
-        qc = rng.standard_normal((1, s, heads, d), dtype=np.float32)
-        kc = rng.standard_normal((1, s, 2, d), dtype=np.float32)
-        vc = rng.standard_normal((1, s, 2, d), dtype=np.float32)
+        # sample: the GPU run's own tensors, query heads 0..7 (the group of
+        # KV head 0), full 4096 causal; head-major (1,H,S,D) -> (1,S,H,D)
+        heads = 8
+        host = lambda t: np.ascontiguousarray(t[0].float().cpu().numpy().transpose(1, 0, 2))[None]
+        qc, kc, vc = host(q[:, :heads]), host(k[:, :1]), host(v[:, :1])
         with cpu_limits():
             t = cpu_time(lambda: A.attention_ref(qc, kc, vc, causal=True))
-        return cpu_info("oracle.attention_ref, 8 of 32 heads (2 KV heads) at full 4096 causal,"
-                        " median of 3 after 1 warm-up",
+        return cpu_info("oracle.attention_ref on the GPU run's inputs copied to the host: query"
+                        " heads 0..7 (the group of KV head 0) at full 4096 causal, median of 3"
+                        " after 1 warm-up",
                         round(4.0 * s * s * heads * d / 2 / t / 1e12, 5), "TFLOP/s")
 
     return dict(
@@ -319,9 +395,10 @@ def workload_c4(args, device, fp8=False):
 
     def cpu():
         from oracle import attention as A
-        # sample: the request with the fewest visible pairs, all 32 heads
+        # sample: the request of median cost (the 4th cheapest of 8 by visible
+        # pairs), all 32 heads
         vis = [int(np.minimum(p + np.arange(c) + 1, window).sum()) for p, c in zip(prior, chunks)]
-        s_ = int(np.argmin(vis))
+        s_ = int(np.argsort(vis, kind="stable")[(len(vis) - 1) // 2])
         total = int(prior[s_] + chunks[s_])
         k, v = seq_values(pool, x["table_np"], s_, total, hk)
         c0 = int(np.sum(chunks[:s_]))
@@ -333,7 +410,7 @@ def workload_c4(args, device, fp8=False):
             t = cpu_time(lambda: A.ragged_reference(qs, k[None], v[None],
                                                     np.array([0, chunks[s_]]), np.array([total]),
                                                     np.zeros((1, 1), np.int64), **kw))
-        return cpu_info(f"oracle.ragged_reference on request {s_} (prior {int(prior[s_])}, chunk"
+        return cpu_info(f"oracle.ragged_reference on request {s_}, the median-cost one (prior {int(prior[s_])}, chunk"
                         f" {int(chunks[s_])}, {vis[s_]} visible pairs x 32 heads), median of 3"
                         " after 1 warm-up", round(4.0 * h * d * vis[s_] / t / 1e12, 5), "TFLOP/s")
 
@@ -348,7 +425,7 @@ def workload_c4(args, device, fp8=False):
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                   "traffic": None if fp8 else read_traffic("c4"),
                   "kernel": "fw_append_kernel + fw_prefill_schedule + " + (
-                      "fw_prefill_staged_kernel<PAGED, e4m3>" if fp8
+                      "fw_prefill_pp_kernel<PAGED, softcap, e4m3>" if fp8
                       else "fw_prefill_pp_kernel<PAGED, softcap>") + " (whole step)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=cpu)
@@ -527,6 +604,21 @@ def workload_c2d256(args, device):
     flops = 4.0 * s * s * h * d / 2 * b
     ms = timed(lambda: flash_attn_func(q, k, v, causal=True), args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
+
+    def cpu():
+        from oracle import attention as A
+        # sample: the GPU run's own tensors, query heads 0..3 (of KV head 0's
+        # group), full 4096 causal
+        heads = 4
+        host = lambda t: np.ascontiguousarray(t[0].float().cpu().numpy().transpose(1, 0, 2))[None]
+        qc, kc, vc = host(q[:, :heads]), host(k[:, :1]), host(v[:, :1])
+        with cpu_limits():
+            t = cpu_time(lambda: A.attention_ref(qc, kc, vc, causal=True))
+        return cpu_info("oracle.attention_ref on the GPU run's inputs copied to the host: query"
+                        " heads 0..3 (of KV head 0's group) at full 4096 causal, head_dim 256,"
+                        " median of 3 after 1 warm-up",
+                        round(4.0 * s * s * heads * d / 2 / t / 1e12, 5), "TFLOP/s")
+
     return dict(
         name="c2d256", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
         vs_baseline=round(tflops / 653.0, 3),
@@ -537,7 +629,7 @@ def workload_c2d256(args, device):
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                   "kernel": "fw_prefill_d256_kernel<DENSE, false>",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
-        cpu=None)
+        cpu=cpu)
 
 
 def workload_c2d256mha(args, device):
@@ -641,9 +733,13 @@ def workload_dec256(args, device):
         cpu=None)
 
 
-WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5}
+WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5,
+             "c2d256": workload_c2d256}
+# "all": the four BASELINE workloads, then the reference's published dense
+# prefill shape (docs/v7x.md:60)
+DEFAULT = ["c2", "c3", "c4", "c5", "c2d256"]
 EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "bwd": workload_bwd, "rope": workload_rope,
-         "c2d256": workload_c2d256, "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
+         "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
          "cp256": workload_cp256, "cp256mha": lambda args, device: workload_cp256(args, device, hk=32),
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
 
@@ -732,12 +828,23 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     device = torch.device("cuda:0")
-    names = list(WORKLOADS) if args.workload == "all" else [args.workload]
+    global CLOCK
+    CLOCK = ClockSampler(device)
+    names = DEFAULT if args.workload == "all" else [args.workload]
     results = []
     for name in names:
         log(f"workload {name}")
         r = {**WORKLOADS, **EXTRA}[name](args, device)
-        log(f"{name}: {r['value']:.2f} {r['unit']} ({r['ms']:.4f} ms/step)")
+        clk = LAST_CLOCK
+        r["roofline"]["sclk_mhz"] = None if clk is None else round(clk["median"], 1)
+        if clk is not None:
+            r["roofline"]["sclk_range_mhz"] = [clk["min"], clk["max"]]
+            if r["roofline"]["bound"] == "mfma":
+                p = r["roofline"]["peak"] * clk["median"] / PEAK_SCLK_MHZ
+                r["roofline"]["peak_at_clock"] = round(p, 1)
+                r["roofline"]["frac_at_clock"] = round(r["roofline"]["achieved"] / p, 4)
+        log(f"{name}: {r['value']:.2f} {r['unit']} ({r['ms']:.4f} ms/step)"
+            f" sclk {r['roofline']['sclk_mhz']} MHz")
         if not args.no_cpu and r.get("cpu") is not None:
             log(f"{name}: timing the CPU oracle")
             r["cpu_baseline"] = r["cpu"]()

@@ -1916,6 +1916,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->kv_mode == FW_KV_DENSE) {
     FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
                "batch, seqlen_q and seqlen_k must be positive");
+    FW_REQUIRE(p->v, FW_ERR_VALUE, "dense attention needs v");
     const int w = v_chunk_width(d, dv);
     for (int c = 0; c * w < dv; ++c)
       launch_mode<FW_KV_DENSE>(v_chunk(a, c, w), dim3(a.n_qt * p->batch * head_groups), p->kv_dtype,
@@ -1931,6 +1932,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   } else {
     FW_REQUIRE(p->seqused_k && p->block_table && p->page_size > 0 && p->num_pages > 0,
                FW_ERR_VALUE, "paged needs seqused_k, block_table and page geometry");
+    // the kernels read keys in 8- and 16-row groups that never straddle a page
+    FW_REQUIRE(p->page_size % 16 == 0, FW_ERR_VALUE,
+               "page_size must be a multiple of 16; got %d", p->page_size);
   }
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);

@@ -8,9 +8,9 @@ Each test runs the HIP path once at full size, then checks
   * the whole KV pool bit-exact against oracle.paged.append_to_pages applied to
     a host copy of the pool taken before the call (every appended row, and
     every other byte unchanged);
-  * out (and lse) against the NumPy oracle on sampled rows / requests, always
-    including the longest, with the north_star tolerance: bf16 max-abs 2e-2
-    and mean-abs 2e-3, fp8 caches 5e-2.
+  * out (and lse) against the NumPy oracle on every row / request (about a
+    minute of host time in all), with the north_star tolerance: bf16 max-abs
+    2e-2 and mean-abs 2e-3, fp8 caches 5e-2.
 """
 
 import numpy as np
@@ -62,7 +62,7 @@ def test_c3_full_size():
     del before
     np.testing.assert_array_equal(after, expected)
     del expected
-    rows = sorted({int(np.argmax(lengths)), int(np.argmin(lengths)), 0, b - 1, 17})
+    rows = range(b)  # every row: stream-K cuts each at different range boundaries
     q = x["q"].float().cpu().numpy()
     o = out.float().cpu().numpy()
     ls = lse.cpu().numpy()
@@ -98,8 +98,7 @@ def test_c4_full_size():
     q = x["q"].float().cpu().numpy()
     o = out.float().cpu().numpy()
     ls = lse.cpu().numpy()
-    # the request with the longest prior, and the one with the longest chunk
-    for s in sorted({int(np.argmax(prior)), int(np.argmax(chunks))}):
+    for s in range(x["n"]):  # every request
         total = int(prior[s] + chunks[s])
         k, v = seq_rows(after, x["table_np"][s], total, hk, torch.bfloat16)
         rows = slice(int(cu[s]), int(cu[s + 1]))
@@ -136,7 +135,7 @@ def test_c4_fp8_full_size():
     q = x["q"].float().cpu().numpy()
     o = out.float().cpu().numpy()
     ls = lse.cpu().numpy()
-    for s in sorted({int(np.argmax(prior)), int(np.argmax(chunks))}):
+    for s in range(x["n"]):  # every request
         total = int(prior[s] + chunks[s])
         k, v = seq_rows(after, x["table_np"][s], total, hk, torch.float8_e4m3fn)
         rows = slice(int(cu[s]), int(cu[s + 1]))
@@ -169,7 +168,7 @@ def test_c5_full_size():
     del before
     np.testing.assert_array_equal(after, expected)
     del expected
-    rows = sorted({int(np.argmax(lengths)), int(np.argmin(lengths)), 0, b - 1})
+    rows = range(b)  # every row
     q = x["q"].float().cpu().numpy()
     o = out.float().cpu().numpy()
     ls = lse.cpu().numpy()

@@ -123,6 +123,19 @@ def test_capi_validation_status_codes():
     q.kv_mode, q.head_dim_v = N.FW_KV_DENSE, 0
     q.head_dim, q.kv_dtype = 128, N.FW_FP8_E4M3
     assert lib.fw_prefill(q, None) == N.FW_ERR_NOT_IMPLEMENTED  # fp8 only for a paged pool
+    # the checks run before any launch, so these stand-in addresses are never read
+    fake = ctypes.c_void_p(0x1000)
+    q.head_dim, q.kv_dtype, q.batch, q.seqlen_q, q.seqlen_k = 128, N.FW_BF16, 1, 8, 8
+    q.q = q.out = q.k = fake
+    assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE  # dense without v
+    assert b"needs v" in lib.fw_last_error()
+    q.kv_mode, q.cu_seqlens_q, q.workspace, q.workspace_bytes = N.FW_KV_PAGED, fake, fake, 1 << 40
+    q.seqused_k, q.block_table, q.num_pages, q.max_pages = fake, fake, 4, 4
+    for page in (12, 20, 24):  # key groups of 8 and 16 rows would straddle pages
+        q.page_size = page
+        assert lib.fw_prefill(q, None) == N.FW_ERR_VALUE
+        assert b"multiple of 16" in lib.fw_last_error()
+    q.kv_mode = N.FW_KV_DENSE
     assert lib.fw_append_ragged(None, None, None, None, None, None, None, 1, 0, 2, 128, 16, 1, 1,
                                 7, None) == N.FW_ERR_NOT_IMPLEMENTED
     bw = N.AttnBwdParams()

@@ -2,7 +2,8 @@
 through the C-ABI, against fw_paged_decode with a workspace on the same
 inputs: two calls in a row, the second with a smaller input, each within the
 bf16 tolerance (max-abs 2e-2, mean-abs 2e-3) of the workspace entry point
-(the same kernels, so in practice bit-equal), the KV pool bit-exact."""
+(the same kernels, so in practice bit-equal), the KV pool bit-exact, and out
+and lse against the NumPy oracle (kvcache_reference) themselves."""
 
 import numpy as np
 import pytest
@@ -10,8 +11,9 @@ import torch
 
 from flywheel_tpu import _native as N
 from flywheel_tpu.decode import decode_params, paged_decode
-from tests.gpu_util import (DEV, PagedCase, announce, assert_close, codes_of, dev_from_codes,
-                            randn, to_dev_bf16)
+from oracle import attention as A
+from tests.gpu_util import (DEV, PagedCase, announce, assert_close, assert_lse, codes_of,
+                            dev_from_codes, randn, to_dev_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -21,7 +23,9 @@ def _case(seed, batch, max_len):
     lengths = rng.integers(1, max_len, batch)
     case = PagedCase(rng, batch=batch, nheads=32, nheads_k=8, lengths=lengths,
                      new_tokens=[1] * batch)
-    q = to_dev_bf16(randn(rng, (batch, 1, 32, 128)))
+    qh = randn(rng, (batch, 1, 32, 128))
+    q = to_dev_bf16(qh)
+    case.q_host = qh
     kn = dev_from_codes(case.k_codes.reshape(batch, 8, 128), torch.bfloat16)
     vn = dev_from_codes(case.v_codes.reshape(batch, 8, 128), torch.bfloat16)
     return case, q, kn, vn
@@ -68,6 +72,10 @@ def test_noalloc_decode_matches_workspace_decode_twice():
         assert_close(out_n.float().cpu().numpy(), out_w.float().cpu().numpy(),
                      what=f"{name} out")
         np.testing.assert_allclose(lse_n.cpu().numpy(), lse_w.cpu().numpy(), rtol=2e-3, atol=4e-3)
+        krows, vrows = case.rows(case.expected_pool())
+        ro, rl = A.kvcache_reference(case.q_host, krows, vrows, case.lengths + 1)
+        assert_close(out_n.float().cpu().numpy(), ro, what=f"{name} out vs oracle")
+        assert_lse(lse_n.cpu().numpy(), rl)
 
 
 def test_noalloc_rejects_a_call_beyond_its_scratch():
