@@ -55,6 +55,9 @@ struct PrefillArgs {
   // log2 of the query heads one workgroup serves (the ping-pong kernel: heads
   // of one GQA group over the same q rows; 0 for the other kernels)
   int hpw_shift;
+  // paged: first V dim this launch reads (a launch over a chunk of a head_dim_v
+  // above 256 starts at that chunk's dims of the merged row's V head)
+  int vdim0;
 };
 
 // Varlen/paged workgroup -> (schedule slot, head group of 2^hpw_shift
@@ -188,7 +191,7 @@ struct KvAddr {
   __device__ __forceinline__ const uint8_t *v_row(int key) const {
     if constexpr (MODE == FW_KV_PAGED) {
       constexpr int EB = KV == FW_BF16 ? 2 : 1;
-      return k_row(key) + D * EB;
+      return k_row(key) + (D + a.vdim0) * EB;
     } else {
       return a.v + 2 * ((size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)(kbase + key) * a.vst);
     }
@@ -1789,7 +1792,10 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
       else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
     } else if (d == 64 && dv == 64) {
       launch_staged<MODE, FW_BF16, 64, 64>(a, grid, s);
-    } else if constexpr (MODE != FW_KV_PAGED) {  // paged pools: 64, 128 and 256 only
+    } else if constexpr (MODE == FW_KV_PAGED) {  // pools at 384 and 512: 128-dim V chunks
+      if (d == 384) launch_staged<MODE, FW_BF16, 384, 128>(a, grid, s);
+      else launch_staged<MODE, FW_BF16, 512, 128>(a, grid, s);
+    } else {
       if (d == 128) launch_staged<MODE, FW_BF16, 128, 256>(a, grid, s);
       else if (d == 256) launch_staged<MODE, FW_BF16, 256, 128>(a, grid, s);
       else if (d == 64) launch_staged<MODE, FW_BF16, 64, 256>(a, grid, s);  // dv 256, or a half of 512
@@ -1806,6 +1812,10 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
       constexpr int KV = decltype(kv)::value;
       if (d == 64) {
         launch_staged<MODE, KV, 64, 64>(a, grid, s);
+      } else if (d == 384) {
+        launch_staged<MODE, KV, 384, 128>(a, grid, s);
+      } else if (d == 512) {
+        launch_staged<MODE, KV, 512, 128>(a, grid, s);
       } else if (d == 256) {
         if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true, KV><<<grid, 256, 0, s>>>(a);
         else fw_prefill_d256_kernel<MODE, false, KV><<<grid, 256, 0, s>>>(a);
@@ -1823,7 +1833,8 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
 // w - 1 of v and out.  Every chunk computes the same scores and writes the
 // same lse.
 static PrefillArgs v_chunk(PrefillArgs a, int c, int w) {
-  a.v += (size_t)c * w * 2;
+  if (a.v) a.v += (size_t)c * w * 2;  // a paged pool's V is addressed from k
+  a.vdim0 = c * w;
   a.out += (size_t)c * w;
   return a;
 }
@@ -1848,8 +1859,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
              p->head_dim, dv);
   FW_REQUIRE(p->kv_mode != FW_KV_PAGED || dv == p->head_dim, FW_ERR_VALUE,
              "a paged pool has one head dim; got head_dim %d, head_dim_v %d", p->head_dim, dv);
-  FW_REQUIRE(p->kv_mode != FW_KV_PAGED || d == 64 || d == 128 || d == 256, FW_ERR_NOT_IMPLEMENTED,
-             "a paged pool takes head_dim 64, 128 or 256; got %d", d);
+  FW_REQUIRE(p->kv_mode != FW_KV_PAGED || d == 64 || d == 128 || d == 256 || d == 384 || d == 512,
+             FW_ERR_NOT_IMPLEMENTED, "a paged pool takes head_dim 64, 128, 256, 384 or 512; got %d",
+             d);
   FW_REQUIRE(!p->rotary_cos || p->head_dim == dv, FW_ERR_NOT_IMPLEMENTED,
              "the fused RoPE takes head_dim_v == head_dim; got %d/%d", p->head_dim, dv);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
@@ -1887,6 +1899,7 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.Sk = p->seqlen_k;
   const bool pingpong = use_pingpong(p);
   a.hpw_shift = pingpong ? pp_head_shift(p) : 0;
+  a.vdim0 = 0;
   const int qt_rows = prefill_tile_rows(p);
   const int head_groups = p->nheads >> a.hpw_shift;
   a.n_qt = (p->seqlen_q + qt_rows - 1) / qt_rows;
@@ -1958,7 +1971,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
     for (int c = 0; c * w < dv; ++c)
       launch_mode<FW_KV_VARLEN>(v_chunk(a, c, w), grid, FW_BF16, p->head_dim, w, s);
   } else {
-    launch_mode<FW_KV_PAGED>(a, grid, p->kv_dtype, p->head_dim, dv, s);
+    const int w = v_chunk_width(d, dv);
+    for (int c = 0; c * w < dv; ++c)
+      launch_mode<FW_KV_PAGED>(v_chunk(a, c, w), grid, p->kv_dtype, p->head_dim, w, s);
   }
   return check_launch("fw_prefill");
 }

@@ -366,11 +366,13 @@ def test_flash_attn_varlen_head_dims(d, dv):
     assert not outs[:, cu_q[-1]:].any()
 
 
-@pytest.mark.parametrize("hd", [256, 64])
+@pytest.mark.parametrize("hd", [256, 64, 384, 512])
 @pytest.mark.parametrize("dtype", ["bf16", "e4m3"])
 def test_chunked_prefill_kvcache_head_dims(dtype, hd):
     """The chunked-prefill call (append + paged varlen, window, softcap,
-    num_active) at head_dim 256 and 64."""
+    num_active) at head_dim 256, 64, 384 and 512 (the reference's paged
+    prefill takes any multiple of 128 shared by q and the pool,
+    kernels/fwd_paged.py:1186-1190)."""
     announce(f"chunked prefill d{hd} {dtype}")
     rng = np.random.default_rng(72)
     dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
@@ -401,3 +403,39 @@ def test_chunked_prefill_kvcache_head_dims(dtype, hd):
                                 num_active=3)
     assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
     assert_lse(lse.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("hd", [384, 512])
+@pytest.mark.parametrize("dtype", ["bf16", "e4m3", "e5m2"])
+def test_paged_varlen_read_only_wide_heads(dtype, hd):
+    """flash_attn_varlen_func(block_table=...) over a merged pool at head dims
+    384 and 512 (launched as 128-dim chunks of V, each chunk reading its dims
+    of the merged row's V head): random_ragged_case's (3, 0, 5) on prefixes
+    (127, 0, 251), plus a longer request, with an odd KV head count."""
+    announce(f"paged varlen d{hd} {dtype}")
+    rng = np.random.default_rng(91 + hd)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.5, 2.0)
+    h, hk = 6, 3
+    qlens = [3, 0, 5, 300]
+    prefix = [127, 0, 251, 700]
+    totals = np.array(qlens) + np.array(prefix)
+    case = PagedCase(rng, batch=4, nheads=h, nheads_k=hk, lengths=totals, new_tokens=[0] * 4,
+                     dtype=dt, k_descale=ks, v_descale=vs, head_dim=hd)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = randn(rng, (cu[-1] + 7, h, hd))
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
+        torch.tensor(cu, device=DEV), None, max(qlens), int(totals.max()), causal=True,
+        window_size=(200, 0), softcap=20.0,
+        return_softmax_lse=True, block_table=torch.tensor(case.table, device=DEV),
+        seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), k_descale=ks,
+        v_descale=vs, nheads_k=hk)
+    torch.cuda.synchronize()
+    kp, vp = case.kv_pages(case.pool_codes)
+    ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True, window_left=200,
+                                softcap=20.0, k_descale=ks, v_descale=vs, round_scaled_q=True)
+    got = out.float().cpu().numpy().transpose(1, 0, 2)
+    assert_close(got[:cu[-1]], ro[:cu[-1]], fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy()[:, :cu[-1]], rl[:, :cu[-1]])
+    assert not got[cu[-1]:].any()

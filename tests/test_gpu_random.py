@@ -168,3 +168,11 @@ def test_random_case_dense_head_dims(d, kind, seed):
     the head dims only those paths take: 96, 192 (register-staged kernel),
     384 and 512 (head_dim_v in 128-dim launches)."""
     one_case(9000 + 100 * d + 1000 * kind + seed, kind, d)
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("d", [384, 512])
+def test_random_case_paged_wide_heads(d, seed):
+    """Paged varlen draws (bf16 / e4m3 / e5m2 pools, page sizes 16-64,
+    windows, softcap, sinks) at head dims 384 and 512."""
+    one_case(20000 + 100 * d + seed, 2, d)
