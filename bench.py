@@ -542,7 +542,8 @@ def workload_bwd(args, device):
     (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device)
     do = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
     out, lse = flash_attn_func(q, k, v, causal=True, return_softmax_lse=True)
-    kw = dict(qs=(h * s * d, s * d, d), ks=(hk * s * d, s * d, d), ls=(h * s, s), batch=b,
+    kw = dict(qs=(h * s * d, s * d, d), ks=(hk * s * d, s * d, d), vs=(hk * s * d, s * d, d),
+              os_=(h * s * d, s * d, d), ls=(h * s, s), batch=b,
               nheads=h, nheads_k=hk, seqlen_q=s, seqlen_k=s, softmax_scale=d ** -0.5, causal=True)
     flops = 2.5 * 4.0 * s * s * h * d / 2 * b
     ms = timed(lambda: attn_bwd(q, k, v, out, do, lse, **kw), args.steps, args.warmup)

@@ -22,6 +22,8 @@
 // that MFMA is permuted to match, and its LDS operand is read in the same
 // permuted order from a transposed copy).
 #include "fw_common.h"
+#include <algorithm>
+#include <type_traits>
 
 namespace fw {
 
@@ -40,7 +42,9 @@ struct BwdArgs {
   float *lse2, *delta;     // (B, H, Sq) workspace
   float *dk_part, *dv_part;  // (split, B, Hk, Sk, 128) workspace, or null
   int64_t qsb, qsh, qst, ksb, ksh, kst, vsb, vsh, vst, lsb, lsh;
+  int64_t osb, osh, ost;  // out and dout
   int B, H, Hk, G, Sq, Sk, split;
+  int dqw, dvw;  // head dims of q / k and of v / out (multiples of 128)
   float scale, qscale;
 };
 
@@ -60,13 +64,15 @@ __global__ __launch_bounds__(256) void fw_bwd_prep_kernel(BwdArgs a) {
   const int t = row - bh * a.Sq;
   const int b = bh / (uint32_t)a.H;
   const int h = bh - (uint32_t)b * a.H;
-  const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)t * a.qst + 8 * c;
-  const u32x4_t o = ld16(a.o + base), d = ld16(a.dout + base);
+  const size_t base = (size_t)b * a.osb + (size_t)h * a.osh + (size_t)t * a.ost + 8 * c;
   float acc = 0.f;
+  for (int cb = 0; cb < a.dvw; cb += 128) {
+    const u32x4_t o = ld16(a.o + base + cb), d = ld16(a.dout + base + cb);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    acc += bf16_lo(o[e]) * bf16_lo(d[e]);
-    acc += bf16_hi(o[e]) * bf16_hi(d[e]);
+    for (int e = 0; e < 4; ++e) {
+      acc += bf16_lo(o[e]) * bf16_lo(d[e]);
+      acc += bf16_hi(o[e]) * bf16_hi(d[e]);
+    }
   }
 #pragma unroll
   for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
@@ -192,6 +198,7 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
   for (int hi = 0; hi < chunk; ++hi) {
     const int h = hk * a.G + sp * chunk + hi;
     const size_t qbase = (size_t)b * a.qsb + (size_t)h * a.qsh;
+    const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh;
     const size_t sbase = ((size_t)b * a.H + h) * a.Sq;
     auto gload = [&](int t) {
       const int qb = t * kBT;
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
         for (int r = 0; r < 2; ++r) {
           const int q = min(qb + 2 * (sr + 16 * p) + r, a.Sq - 1);
           qx[2 * p + r] = ld16(a.q + qbase + (size_t)q * a.qst + 8 * sc);
-          dx[2 * p + r] = ld16(a.dout + qbase + (size_t)q * a.qst + 8 * sc);
+          dx[2 * p + r] = ld16(a.dout + obase + (size_t)q * a.ost + 8 * sc);
         }
       if (tid < kBT) {
         const int q = qb + tid;
@@ -357,25 +364,30 @@ __global__ __launch_bounds__(256) void fw_bwd_reduce_kernel(BwdArgs a) {
   const int key = row - bh * a.Sk;
   const int b = bh / (uint32_t)a.Hk;
   const int hk = bh - (uint32_t)b * a.Hk;
-  float sk[8] = {}, sv[8] = {};
-  for (int s = 0; s < a.split; ++s) {
-    const size_t base = ((size_t)s * rows + row) * 128 + 8 * c;
-    const f32x4_t k0 = *(const f32x4_t *)(a.dk_part + base), k1 = *(const f32x4_t *)(a.dk_part + base + 4);
-    const f32x4_t v0 = *(const f32x4_t *)(a.dv_part + base), v1 = *(const f32x4_t *)(a.dv_part + base + 4);
+  // dk over dqw dims, then dv over dvw dims, 128 at a time
+  for (int cb = 0; cb < a.dqw + a.dvw; cb += 128) {
+    const bool is_k = cb < a.dqw;
+    const int w = is_k ? a.dqw : a.dvw, col = is_k ? cb : cb - a.dqw;
+    const float *part = is_k ? a.dk_part : a.dv_part;
+    float sum[8] = {};
+    for (int s = 0; s < a.split; ++s) {
+      const size_t base = ((size_t)s * rows + row) * w + col + 8 * c;
+      const f32x4_t x0 = *(const f32x4_t *)(part + base), x1 = *(const f32x4_t *)(part + base + 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      sk[e] += k0[e]; sk[4 + e] += k1[e];
-      sv[e] += v0[e]; sv[4 + e] += v1[e];
+      for (int e = 0; e < 4; ++e) {
+        sum[e] += x0[e];
+        sum[4 + e] += x1[e];
+      }
     }
-  }
-  u32x4_t ko, vo;
+    const float f = is_k ? a.scale : 1.f;
+    u32x4_t o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    ko[e] = pack_bf16(sk[2 * e] * a.scale, sk[2 * e + 1] * a.scale);
-    vo[e] = pack_bf16(sv[2 * e], sv[2 * e + 1]);
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16(sum[2 * e] * f, sum[2 * e + 1] * f);
+    if (is_k)
+      *(u32x4_t *)(a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst + col + 8 * c) = o;
+    else
+      *(u32x4_t *)(a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst + col + 8 * c) = o;
   }
-  *(u32x4_t *)(a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst + 8 * c) = ko;
-  *(u32x4_t *)(a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst + 8 * c) = vo;
 }
 
 // ------------------------------------------------------------------ dq
@@ -402,11 +414,12 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
   float l2 = INFINITY, dl = 0.f;
   {
     const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)(row_ok ? qrow : 0) * a.qst;
+    const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(row_ok ? qrow : 0) * a.ost;
     const float qs = row_ok ? a.qscale : 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
-      const u32x4_t d = ld16(a.dout + base + 16 * j + 8 * g);
+      const u32x4_t d = ld16(a.dout + obase + 16 * j + 8 * g);
       dop[j] = __builtin_bit_cast(bf16x8_t, row_ok ? d : u32x4_t{0, 0, 0, 0});
     }
     if (row_ok) {
@@ -521,11 +534,398 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
     }
 }
 
+
+// ------------------------------------------------------------------ wide head dims
+// The same recurrences at head dims DQ (q, k) and DV (v, out) of 128, 256 or
+// 512 (smaller head dims reach them zero-padded).  Each launch of a kernel
+// below computes one 128-dim chunk (blockIdx.z) of its outputs: the scores S
+// and dP are recomputed per chunk over the full head dims, and only the
+// chunk's accumulators (64 registers each) stay live beside the resident
+// operands.  Tiles are staged row-major only (stride W + 8 bf16, 4 banks
+// apart per row like 136); transposed operands come from transposing reads.
+
+// A 64-row tile's rows 2(sr + 16p) + r (p, r = 0, 1), dims col + 8sc .. + 7,
+// stored row-major with stride S (bf16 elements).
+template <int S>
+__device__ __forceinline__ void store_rows(uint16_t *R, const u32x4_t (&x)[4], int sr, int sc,
+                                           int col) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) *(u32x4_t *)(R + (2 * (sr + 16 * p) + r) * S + col + 8 * sc) = x[2 * p + r];
+}
+
+// tr_operand_rm over a row-major tile of stride S: the A operand of dims col ..
+// col + 31, reduction rows 16u + 4g .. + 3 and 16u + 8 + 4g .. + 3.
+template <int S>
+__device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane) {
+  const int g = lane >> 5, grp = lane >> 4, i = lane & 15;
+  const uint32_t o = Rb + 2u * ((16 * u + 4 * g + (i >> 2)) * S + col + 16 * (grp & 1) + 4 * (i & 3));
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)o);
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(o + 16u * S));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int DQ, int DV>
+constexpr int kWideDkvLds = (64 * (DQ + 8) + 64 * (DV + 8) + 64 * 136) * 2 + 2 * kBT * 4;
+
+// dk / dv chunk cc = blockIdx.z: dk dims 128cc .. + 127 when cc < DQ / 128,
+// dv dims 128cc .. + 127 when cc < DV / 128.  Workgroup = 4 waves = 128 keys
+// of KV head hk, K and V rows resident as operands; per 64-row q tile the LDS
+// holds q_s rows (DQ), dout rows (DV) and the chunk's raw q rows (128).
+template <bool CAUSAL, int DQ, int DV>
+__global__ __launch_bounds__(256, 1) void fw_bwd_dkv_wide_kernel(BwdArgs a) {
+  constexpr int SQ = DQ + 8, SV = DV + 8, SR = 136;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kWideDkvLds<DQ, DV>];
+  uint16_t *Qs = (uint16_t *)smem;
+  uint16_t *Ds = Qs + 64 * SQ;
+  uint16_t *Qr = Ds + 64 * SV;
+  float *Ls = (float *)(Qr + 64 * SR);
+  float *Dl = Ls + kBT;
+  const uint32_t lds_ds = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)Ds;
+  const uint32_t lds_qr = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)Qr;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  const int k0 = blockIdx.x * 128;
+  int z = blockIdx.y;
+  const int sp = z % a.split;
+  z /= a.split;
+  const int hk = z % a.Hk;
+  const int b = z / a.Hk;
+  const int cc = blockIdx.z;
+  const bool do_k = cc < DQ / 128, do_v = cc < DV / 128;
+  const int chunk = a.G / a.split;
+  const int off = a.Sk - a.Sq;
+
+  const int key = k0 + 32 * w + n;
+  const bool key_ok = key < a.Sk;
+  bf16x8_t kop[DQ / 16], vop[DV / 16];
+  {
+    const int kr = key_ok ? key : 0;
+    const uint16_t *kp = a.k + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)kr * a.kst;
+    const uint16_t *vp = a.v + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)kr * a.vst;
+    const u32x4_t z4 = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < DQ / 16; ++j)
+      kop[j] = __builtin_bit_cast(bf16x8_t, key_ok ? ld16(kp + 16 * j + 8 * g) : z4);
+#pragma unroll
+    for (int j = 0; j < DV / 16; ++j)
+      vop[j] = __builtin_bit_cast(bf16x8_t, key_ok ? ld16(vp + 16 * j + 8 * g) : z4);
+  }
+  f32x16_t dkacc[4], dvacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dkacc[c][e] = dvacc[c][e] = 0.f;
+
+  const int q_first = CAUSAL ? max(0, k0 - off) : 0;
+  const int t_begin = q_first / kBT;
+  const int t_end = (a.Sq + kBT - 1) / kBT;
+  const int kw0 = k0 + 32 * w;
+  const int sr = tid & 15, sc = tid >> 4;
+
+  for (int hi = 0; hi < chunk; ++hi) {
+    const int h = hk * a.G + sp * chunk + hi;
+    const size_t qbase = (size_t)b * a.qsb + (size_t)h * a.qsh;
+    const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh;
+    const size_t sbase = ((size_t)b * a.H + h) * a.Sq;
+    for (int t = t_begin; t < t_end; ++t) {
+      const int qb = t * kBT;
+      __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+      for (int cb = 0; cb < DQ / 128; ++cb) {
+        u32x4_t x[4], xs[4];
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int q = min(qb + 2 * (sr + 16 * p) + r, a.Sq - 1);
+            x[2 * p + r] = ld16(a.q + qbase + (size_t)q * a.qst + 128 * cb + 8 * sc);
+          }
+        if (cb == cc) store_rows<SR>(Qr, x, sr, sc, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xs[i] = scale_words(x[i], a.qscale);
+        store_rows<SQ>(Qs, xs, sr, sc, 128 * cb);
+      }
+#pragma unroll
+      for (int cb = 0; cb < DV / 128; ++cb) {
+        u32x4_t x[4];
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int q = min(qb + 2 * (sr + 16 * p) + r, a.Sq - 1);
+            x[2 * p + r] = ld16(a.dout + obase + (size_t)q * a.ost + 128 * cb + 8 * sc);
+          }
+        store_rows<SV>(Ds, x, sr, sc, 128 * cb);
+      }
+      if (tid < kBT) {
+        const int q = qb + tid;
+        Ls[tid] = q < a.Sq ? a.lse2[sbase + q] : INFINITY;
+        Dl[tid] = q < a.Sq ? a.delta[sbase + q] : 0.f;
+      }
+      __syncthreads();
+      const bool full = !CAUSAL || qb + off >= kw0 + 31;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        f32x16_t sacc, dpacc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
+        const uint16_t *qr = Qs + (32 * st + n) * SQ + 8 * g;
+        const uint16_t *dr = Ds + (32 * st + n) * SV + 8 * g;
+#pragma unroll
+        for (int j = 0; j < DQ / 16; ++j)
+          sacc = mfma32(__builtin_bit_cast(bf16x8_t, ld16(qr + 16 * j)), kop[j], sacc);
+#pragma unroll
+        for (int j = 0; j < DV / 16; ++j)
+          dpacc = mfma32(__builtin_bit_cast(bf16x8_t, ld16(dr + 16 * j)), vop[j], dpacc);
+        float pe[16];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          const f32x4_t l4 = *(const f32x4_t *)(Ls + 32 * st + 8 * blk + 4 * g);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pe[4 * blk + i] = fast_exp2(sacc[4 * blk + i] - l4[i]);
+        }
+        if (!full) {
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int r = 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+            pe[e] = qb + r + off >= key ? pe[e] : 0.f;
+          }
+        }
+        bf16x8_t pop[2], dsop[2];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          const int r0 = 32 * st + 8 * blk + 4 * g;
+          const f32x4_t d4 = *(const f32x4_t *)(Dl + r0);
+          float pv[4], dv4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * blk + i;
+            pv[i] = pe[e];
+            dv4[i] = pe[e] * (dpacc[e] - d4[i]);
+          }
+          const int u = blk >> 1, half = blk & 1;
+          u32x4_t pw = __builtin_bit_cast(u32x4_t, pop[u]);
+          u32x4_t dw = __builtin_bit_cast(u32x4_t, dsop[u]);
+          pw[2 * half] = pack_bf16(pv[0], pv[1]);
+          pw[2 * half + 1] = pack_bf16(pv[2], pv[3]);
+          dw[2 * half] = pack_bf16(dv4[0], dv4[1]);
+          dw[2 * half + 1] = pack_bf16(dv4[2], dv4[3]);
+          pop[u] = __builtin_bit_cast(bf16x8_t, pw);
+          dsop[u] = __builtin_bit_cast(bf16x8_t, dw);
+        }
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu) {
+          const int u = 2 * st + uu;
+          if (do_v) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              dvacc[c] = mfma32(tr_rm<SV>(lds_ds, 128 * cc + 32 * c, u, lane), pop[uu], dvacc[c]);
+          }
+          if (do_k) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              dkacc[c] = mfma32(tr_rm<SR>(lds_qr, 32 * c, u, lane), dsop[uu], dkacc[c]);
+          }
+        }
+      }
+    }
+  }
+
+  if (!key_ok) return;
+  if (a.split == 1) {
+    uint16_t *kp = a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst + 128 * cc;
+    uint16_t *vp = a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst + 128 * cc;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d = 32 * c + 8 * rr + 4 * g;
+        const f32x16_t &K = dkacc[c];
+        const f32x16_t &V = dvacc[c];
+        if (do_k)
+          *(u32x2_t *)(kp + d) = u32x2_t{pack_bf16(K[4 * rr] * a.scale, K[4 * rr + 1] * a.scale),
+                                         pack_bf16(K[4 * rr + 2] * a.scale, K[4 * rr + 3] * a.scale)};
+        if (do_v)
+          *(u32x2_t *)(vp + d) = u32x2_t{pack_bf16(V[4 * rr], V[4 * rr + 1]),
+                                         pack_bf16(V[4 * rr + 2], V[4 * rr + 3])};
+      }
+  } else {
+    const size_t row = (((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d = 128 * cc + 32 * c + 8 * rr + 4 * g;
+        if (do_k)
+          *(f32x4_t *)(a.dk_part + row * DQ + d) = f32x4_t{dkacc[c][4 * rr], dkacc[c][4 * rr + 1],
+                                                           dkacc[c][4 * rr + 2], dkacc[c][4 * rr + 3]};
+        if (do_v)
+          *(f32x4_t *)(a.dv_part + row * DV + d) = f32x4_t{dvacc[c][4 * rr], dvacc[c][4 * rr + 1],
+                                                           dvacc[c][4 * rr + 2], dvacc[c][4 * rr + 3]};
+      }
+  }
+}
+
+// dq chunk cc = blockIdx.z (dims 128cc .. + 127 of DQ).  Workgroup = 4 waves
+// = 128 query rows of head h, q_s and dout resident as operands; per 64-key
+// tile the LDS holds K rows (DQ) and V rows (DV); the chunk's K^T operand
+// comes from the K rows by transposing reads.
+template <bool CAUSAL, int DQ, int DV>
+__global__ __launch_bounds__(256, 1) void fw_bwd_dq_wide_kernel(BwdArgs a) {
+  constexpr int SK = DQ + 8, SV = DV + 8;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[(64 * SK + 64 * SV) * 2];
+  uint16_t *Ks = (uint16_t *)smem;
+  uint16_t *Vs = Ks + 64 * SK;
+  const uint32_t lds_ks = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)Ks;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  const int n_qt = (a.Sq + 127) / 128;
+  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
+  const int cc = blockIdx.z;
+  const int q0 = qt * 128;
+  const int off = a.Sk - a.Sq;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < a.Sq;
+
+  bf16x8_t qop[DQ / 16], dop[DV / 16];
+  float l2 = INFINITY, dl = 0.f;
+  {
+    const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)(row_ok ? qrow : 0) * a.qst;
+    const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(row_ok ? qrow : 0) * a.ost;
+    const float qs = row_ok ? a.qscale : 0.f;
+#pragma unroll
+    for (int j = 0; j < DQ / 16; ++j)
+      qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
+#pragma unroll
+    for (int j = 0; j < DV / 16; ++j) {
+      const u32x4_t d = ld16(a.dout + obase + 16 * j + 8 * g);
+      dop[j] = __builtin_bit_cast(bf16x8_t, row_ok ? d : u32x4_t{0, 0, 0, 0});
+    }
+    if (row_ok) {
+      const size_t s = ((size_t)b * a.H + h) * a.Sq + qrow;
+      l2 = a.lse2[s];
+      dl = a.delta[s];
+    }
+  }
+  f32x16_t dqacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqacc[c][e] = 0.f;
+
+  auto row_hi = [&](int r) { return CAUSAL ? min(a.Sk, r + off + 1) : a.Sk; };
+  const int last_row = min(q0 + 127, a.Sq - 1);
+  const int wg_hi = row_hi(last_row);
+  const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
+  const int r_hi = row_hi(qrow);
+  const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
+  const size_t vbase = (size_t)b * a.vsb + (size_t)hk * a.vsh;
+  const int sr = tid & 15, sc = tid >> 4;
+  for (int t = 0; t < t_end; ++t) {
+    const int kb = t * kBT;
+    __syncthreads();
+#pragma unroll
+    for (int cb = 0; cb < DQ / 128; ++cb) {
+      u32x4_t x[4];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int kk = min(kb + 2 * (sr + 16 * p) + r, a.Sk - 1);
+          x[2 * p + r] = ld16(a.k + kbase + (size_t)kk * a.kst + 128 * cb + 8 * sc);
+        }
+      store_rows<SK>(Ks, x, sr, sc, 128 * cb);
+    }
+#pragma unroll
+    for (int cb = 0; cb < DV / 128; ++cb) {
+      u32x4_t x[4];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int kk = min(kb + 2 * (sr + 16 * p) + r, a.Sk - 1);
+          x[2 * p + r] = ld16(a.v + vbase + (size_t)kk * a.vst + 128 * cb + 8 * sc);
+        }
+      store_rows<SV>(Vs, x, sr, sc, 128 * cb);
+    }
+    __syncthreads();
+    const bool full = kb + kBT <= row_hi(q0 + 32 * w);
+    bf16x8_t dsop[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x16_t sacc, dpacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
+      const uint16_t *kr = Ks + (32 * st + n) * SK + 8 * g;
+      const uint16_t *vr = Vs + (32 * st + n) * SV + 8 * g;
+#pragma unroll
+      for (int j = 0; j < DQ / 16; ++j)
+        sacc = mfma32(__builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j)), qop[j], sacc);
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j)
+        dpacc = mfma32(__builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j)), dop[j], dpacc);
+      if (!full) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kk = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[e] = kk < r_hi ? sacc[e] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        u32x4_t dw;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          float dsv[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int e = 8 * u2 + 2 * e2 + i;
+            dsv[i] = fast_exp2(sacc[e] - l2) * (dpacc[e] - dl);
+          }
+          dw[e2] = pack_bf16(dsv[0], dsv[1]);
+        }
+        dsop[2 * st + u2] = __builtin_bit_cast(bf16x8_t, dw);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        dqacc[c] = mfma32(tr_rm<SK>(lds_ks, 128 * cc + 32 * c, u, lane), dsop[u], dqacc[c]);
+  }
+
+  if (!row_ok) return;
+  uint16_t *dp = a.dq + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qrow * a.qst + 128 * cc;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const f32x16_t &Q = dqacc[c];
+      *(u32x2_t *)(dp + 32 * c + 8 * rr + 4 * g) =
+          u32x2_t{pack_bf16(Q[4 * rr] * a.scale, Q[4 * rr + 1] * a.scale),
+                  pack_bf16(Q[4 * rr + 2] * a.scale, Q[4 * rr + 3] * a.scale)};
+    }
+}
+
 // Query heads of one KV head are split over `split` workgroups when the
 // (batch, kv head, key tile) grid alone would leave CUs idle.
+int head_dim_v_of(const fw_attn_bwd_params *p) { return p->head_dim_v > 0 ? p->head_dim_v : p->head_dim; }
+
+// dk / dv chunks of 128 dims one dk/dv launch runs as separate workgroups
+int dkv_chunks(const fw_attn_bwd_params *p) {
+  if (p->head_dim == 128 && head_dim_v_of(p) == 128) return 1;
+  return std::max(p->head_dim, head_dim_v_of(p)) / 128;
+}
+
 int pick_split(const fw_attn_bwd_params *p) {
   const int G = p->nheads / p->nheads_k;
-  const long base = (long)p->batch * p->nheads_k * ceil_div(p->seqlen_k, 128);
+  const long base = (long)p->batch * p->nheads_k * ceil_div(p->seqlen_k, 128) * dkv_chunks(p);
   int split = 1;
   while (split < G && base * split < 512) {
     int nxt = split + 1;
@@ -547,13 +947,36 @@ extern "C" size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p) {
   const size_t rows = (size_t)p->batch * p->nheads * p->seqlen_q;
   size_t bytes = 2 * align256(rows * 4);
   const int split = pick_split(p);
-  if (split > 1) bytes += 2 * align256((size_t)split * p->batch * p->nheads_k * p->seqlen_k * 128 * 4);
+  const size_t keys = (size_t)split * p->batch * p->nheads_k * p->seqlen_k * 4;
+  if (split > 1) bytes += align256(keys * p->head_dim) + align256(keys * head_dim_v_of(p));
   return bytes;
 }
 
+template <bool CAUSAL>
+static void launch_wide(const BwdArgs &a, int dq_w, int dv_w, dim3 gkv, dim3 gq, bool dkv,
+                        hipStream_t s) {
+  auto run = [&](auto dqc, auto dvc) {
+    constexpr int DQ = decltype(dqc)::value, DV = decltype(dvc)::value;
+    if (dkv) fw_bwd_dkv_wide_kernel<CAUSAL, DQ, DV><<<gkv, 256, 0, s>>>(a);
+    else fw_bwd_dq_wide_kernel<CAUSAL, DQ, DV><<<gq, 256, 0, s>>>(a);
+  };
+  using I128 = std::integral_constant<int, 128>;
+  using I256 = std::integral_constant<int, 256>;
+  using I512 = std::integral_constant<int, 512>;
+  if (dq_w == 128 && dv_w == 256) run(I128(), I256());
+  else if (dq_w == 128 && dv_w == 512) run(I128(), I512());
+  else if (dq_w == 256 && dv_w == 128) run(I256(), I128());
+  else run(I256(), I256());
+}
+
 extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
-  FW_REQUIRE(p->head_dim == 128, FW_ERR_NOT_IMPLEMENTED,
-             "the gfx950 backward takes head_dim 128; got %d", p->head_dim);
+  const int dvw = head_dim_v_of(p);
+  FW_REQUIRE((p->head_dim == 128 && (dvw == 128 || dvw == 256 || dvw == 512)) ||
+                 (p->head_dim == 256 && (dvw == 128 || dvw == 256)),
+             FW_ERR_NOT_IMPLEMENTED,
+             "the gfx950 backward takes head_dim / head_dim_v 128/128, 128/256, 128/512, 256/128"
+             " or 256/256 (smaller head dims zero-padded to those); got %d/%d",
+             p->head_dim, dvw);
   FW_REQUIRE(p->nheads_k > 0 && p->nheads % p->nheads_k == 0, FW_ERR_VALUE,
              "nheads (%d) must be a multiple of nheads_k (%d)", p->nheads, p->nheads_k);
   FW_REQUIRE(p->batch > 0 && p->seqlen_q > 0 && p->seqlen_k > 0, FW_ERR_VALUE,
@@ -583,11 +1006,19 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   a.split = pick_split(p);
   a.dk_part = a.dv_part = nullptr;
   if (a.split > 1) {
-    const size_t part = align256((size_t)a.split * p->batch * p->nheads_k * p->seqlen_k * 128 * 4);
+    const size_t keys = (size_t)a.split * p->batch * p->nheads_k * p->seqlen_k * 4;
     a.dk_part = (float *)(ws + 2 * align256(rows * 4));
-    a.dv_part = (float *)(ws + 2 * align256(rows * 4) + part);
+    a.dv_part = (float *)(ws + 2 * align256(rows * 4) + align256(keys * p->head_dim));
   }
   a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qst = p->q_stride_t;
+  const bool o_given = p->o_stride_b || p->o_stride_h || p->o_stride_t;
+  FW_REQUIRE(o_given || dvw == p->head_dim, FW_ERR_VALUE,
+             "head_dim_v %d != head_dim %d needs the out / dout strides", dvw, p->head_dim);
+  a.osb = o_given ? p->o_stride_b : p->q_stride_b;
+  a.osh = o_given ? p->o_stride_h : p->q_stride_h;
+  a.ost = o_given ? p->o_stride_t : p->q_stride_t;
+  a.dqw = p->head_dim;
+  a.dvw = dvw;
   a.ksb = p->k_stride_b; a.ksh = p->k_stride_h; a.kst = p->k_stride_t;
   a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.vst = p->v_stride_t;
   a.lsb = p->lse_stride_b; a.lsh = p->lse_stride_h;
@@ -604,9 +1035,17 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   fw_bwd_prep_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a);  // 16 rows per block
   int st = check_launch("fw_bwd_prep_kernel");
   if (st != FW_OK) return st;
-  const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split);
-  if (p->causal) fw_bwd_dkv_kernel<true><<<gkv, 256, 0, s>>>(a);
-  else fw_bwd_dkv_kernel<false><<<gkv, 256, 0, s>>>(a);
+  const bool wide = dkv_chunks(p) > 1 || dvw != p->head_dim;
+  const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split, dkv_chunks(p));
+  const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);
+  if (wide) {
+    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, true, s);
+    else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, true, s);
+  } else if (p->causal) {
+    fw_bwd_dkv_kernel<true><<<gkv, 256, 0, s>>>(a);
+  } else {
+    fw_bwd_dkv_kernel<false><<<gkv, 256, 0, s>>>(a);
+  }
   st = check_launch("fw_bwd_dkv_kernel");
   if (st != FW_OK) return st;
   if (a.split > 1) {
@@ -615,8 +1054,13 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     st = check_launch("fw_bwd_reduce_kernel");
     if (st != FW_OK) return st;
   }
-  const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads);
-  if (p->causal) fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
-  else fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
+  if (wide) {
+    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, false, s);
+    else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, false, s);
+  } else if (p->causal) {
+    fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
+  } else {
+    fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
+  }
   return check_launch("fw_bwd_dq_kernel");
 }

@@ -84,6 +84,8 @@ class AttnBwdParams(ctypes.Structure):
         ("batch", _i32), ("nheads", _i32), ("nheads_k", _i32), ("head_dim", _i32),
         ("seqlen_q", _i32), ("seqlen_k", _i32),
         ("softmax_scale", _f32), ("causal", _i32),
+        ("head_dim_v", _i32),
+        ("o_stride_b", _i64), ("o_stride_h", _i64), ("o_stride_t", _i64),
     ]
 
 

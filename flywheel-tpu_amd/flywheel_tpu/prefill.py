@@ -256,18 +256,18 @@ def flash_attn_func(
         else:
             unsupported = ("window_size" if window_size != (-1, -1) else
                            "softcap" if softcap != 0.0 else
-                           f"head_dim_v {dv}" if dv != d else
-                           f"head_dim {d}" if d not in (64, 96, 128) else None)
+                           f"head_dim {d} / head_dim_v {dv}" if B.bwd_widths(d, dv) is None
+                           else None)
             if unsupported:
                 reason = (f"The backward kernel does not support {unsupported}; that"
                           " configuration is forward-only.")
         spec = {
             "run": lambda q, k, v: run(q, k, v, True),
             "forward_only": reason,
-            "geometry": dict(qs=qs, ks=ks, ls=(nheads * seqlen_q, seqlen_q), batch=batch,
-                             nheads=nheads, nheads_k=nheads_k, seqlen_q=seqlen_q,
+            "geometry": dict(qs=qs, ks=ks, vs=vs, os_=os_, ls=(nheads * seqlen_q, seqlen_q),
+                             batch=batch, nheads=nheads, nheads_k=nheads_k, seqlen_q=seqlen_q,
                              seqlen_k=seqlen_k, softmax_scale=softmax_scale, causal=causal,
-                             head_dim=d),
+                             head_dim=d, head_dim_v=dv),
         }
         out, lse = B.FlashAttnFunction.apply(q, k, v, spec)
     if return_softmax_lse:

@@ -246,8 +246,9 @@ int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
  * rounded scaled q, ds = p (dp - delta), dk = scale ds^T q, dv = p^T dout,
  * dq = scale ds k).  MHA and GQA / MQA; causal (bottom-right, offset
  * seqlen_k - seqlen_q) or full mask; the backward supports nothing else of the
- * forward (variant.py:365-384).  Element (b, h, t, d) of q, out, dout and dq is
- * at b*q_stride_b + h*q_stride_h + t*q_stride_t + d; k and dk use the k
+ * forward (variant.py:365-384).  Element (b, h, t, d) of q and dq is at
+ * b*q_stride_b + h*q_stride_h + t*q_stride_t + d, of out and dout likewise
+ * with the o strides (the q strides when those are 0); k and dk use the k
  * strides, v and dv the v strides; lse (b, h, t) at b*lse_stride_b +
  * h*lse_stride_h + t.  Deterministic: no atomics.  The workspace (its size
  * from fw_attn_bwd_workspace_bytes) holds f32 row statistics and, when the
@@ -266,6 +267,14 @@ typedef struct fw_attn_bwd_params {
   int32_t batch, nheads, nheads_k, head_dim, seqlen_q, seqlen_k;
   float softmax_scale;
   int32_t causal;
+  /* Head dim of v, out, dout and dv; 0 = head_dim.  head_dim / head_dim_v:
+   * 128/128, 128/256, 128/512, 256/128 or 256/256 (the reference's backward
+   * pairs 64/64, 64/256, 64/512, 96/96, 192/128, 192/192, test_prefill.py:
+   * 205-208,285-333, reach these with zero-padded head vectors). */
+  int32_t head_dim_v;
+  /* Element (b, h, t, d) of out and dout; all 0 = the q strides (allowed
+   * only when head_dim_v == head_dim). */
+  int64_t o_stride_b, o_stride_h, o_stride_t;
 } fw_attn_bwd_params;
 
 size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p);

@@ -36,9 +36,9 @@ def run(q, k, v, do, causal, token_major=False):
     if token_major:
         tens = [to_dev_bf16(x.reshape(x.shape[0], x.shape[1], -1)).requires_grad_() for x in (q, k, v)]
         out = flash_attn_func(*tens, causal=causal, token_major=True, head_dim=d)
-        out.backward(to_dev_bf16(do.reshape(b, sq, h * d)))
+        out.backward(to_dev_bf16(do.reshape(b, sq, -1)))
         torch.cuda.synchronize()
-        return [t.grad.float().cpu().numpy().reshape(t.shape[0], t.shape[1], -1, d) for t in tens]
+        return [t.grad.float().cpu().numpy().reshape(x.shape) for t, x in zip(tens, (q, k, v))]
     tens = [to_dev_bf16(head_major(x)).requires_grad_() for x in (q, k, v)]
     out = flash_attn_func(*tens, causal=causal)
     out.backward(to_dev_bf16(head_major(do)))
@@ -142,8 +142,40 @@ def test_backward_token_major_d64():
     check_grads(run(q, k, v, do, True, token_major=True), q, k, v, do, True, "token-major d64")
 
 
-@pytest.mark.parametrize("d,dv,msg", [(256, 256, "head_dim 256"), (192, 128, "head_dim_v 128"),
-                                      (64, 256, "head_dim_v 256")])
+WIDE_PAIRS = [(192, 192), (192, 128), (256, 256), (64, 256), (64, 512), (128, 256), (256, 128)]
+
+
+@pytest.mark.parametrize("d,dv", WIDE_PAIRS)
+@pytest.mark.parametrize("b,h,hk,sq,sk,causal", [(2, 4, 2, 200, 333, True), (1, 4, 4, 150, 300, False),
+                                                 (1, 4, 1, 333, 200, True),
+                                                 (1, 16, 2, 260, 260, True)])
+def test_backward_wide_head_dims(d, dv, b, h, hk, sq, sk, causal):
+    """The reference's backward pairs above head dim 128 and with head_dim_v
+    != head_dim (test_prefill.py:205-208,285-333: 192/128, 192/192, 256/256,
+    64/256, 64/512), plus 128/256 and 256/128: the wide kernels, one
+    launch per 128-dim chunk of the gradients; the last shape splits a KV
+    head's query heads over workgroups (f32 partials at both widths)."""
+    what = f"bwd d{d}/{dv} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+    announce(what)
+    rng = np.random.default_rng(70 + d + dv)
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, dv))
+    do = randn(rng, (b, sq, h, dv))
+    check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
+
+
+def test_backward_wide_token_major():
+    """Token-major (fused head) layout at 256/128 and 256/256 (token-major
+    head dims are multiples of 128, prefill.py:150)."""
+    for d, dv in ((256, 128), (256, 256)):
+        what = f"bwd token-major d{d}/{dv}"
+        announce(what)
+        rng = np.random.default_rng(80 + d)
+        q, k, v = randn(rng, (2, 150, 4, d)), randn(rng, (2, 150, 2, d)), randn(rng, (2, 150, 2, dv))
+        do = randn(rng, (2, 150, 4, dv))
+        check_grads(run(q, k, v, do, True, token_major=True), q, k, v, do, True, what)
+
+
+@pytest.mark.parametrize("d,dv,msg", [(384, 384, "head_dim 384"), (512, 512, "head_dim 512")])
 def test_backward_large_head_dims_are_forward_only(d, dv, msg):
     announce(f"bwd d{d}/{dv} forward-only")
     rng = np.random.default_rng(66)
@@ -160,7 +192,7 @@ def test_forward_backward_bitwise_repeat_head_dims(d):
     backward exists)."""
     announce(f"repeat d{d}")
     rng = np.random.default_rng(67)
-    grad = d in (64, 96, 128)
+    grad = d <= 256  # a backward exists
     b, h, s = 2, 4, 384
     q, k, v, do = (to_dev_bf16(randn(rng, (b, h, s, d))) for _ in range(4))
 

@@ -141,6 +141,13 @@ def test_capi_validation_status_codes():
     bw = N.AttnBwdParams()
     bw.head_dim, bw.nheads, bw.nheads_k, bw.batch, bw.seqlen_q, bw.seqlen_k = 64, 4, 2, 1, 8, 8
     assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_NOT_IMPLEMENTED
+    for d, dv in ((192, 0), (256, 512), (128, 384)):  # kernels: 128 or 256 / 128, 256 or 512
+        bw.head_dim, bw.head_dim_v = d, dv
+        assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_NOT_IMPLEMENTED
+    bw.head_dim, bw.head_dim_v = 256, 128
+    assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_VALUE  # supported; no tensors
+    assert lib.fw_attn_bwd_workspace_bytes(bw) >= 2 * 4 * 8 * 4
+    bw.head_dim_v = 0
     bw.head_dim, bw.nheads = 128, 3
     assert lib.fw_attn_bwd(bw, None) == N.FW_ERR_VALUE  # heads not a multiple of nheads_k
     bw.nheads = 4

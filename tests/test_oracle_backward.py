@@ -46,6 +46,24 @@ def test_backward_matches_torch_autograd(h, hk, sq, sk, causal):
         np.testing.assert_allclose(a, b_, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("d,dv,h,hk,causal", [(48, 16, 4, 2, True), (16, 64, 2, 1, False),
+                                                (32, 128, 3, 3, True)])
+def test_backward_head_dim_v_matches_torch_autograd(d, dv, h, hk, causal):
+    """head_dim_v != head_dim (the reference's 192/128 and 64/256, 64/512
+    pairs, test_prefill.py:205-208), at small sizes: the scale stays
+    1/sqrt(head_dim)."""
+    rng = np.random.default_rng(7)
+    q = T.bf16(rng.standard_normal((1, 21, h, d), dtype=np.float32))
+    k = T.bf16(rng.standard_normal((1, 26, hk, d), dtype=np.float32))
+    v = T.bf16(rng.standard_normal((1, 26, hk, dv), dtype=np.float32))
+    do = T.bf16(rng.standard_normal((1, 21, h, dv), dtype=np.float32))
+    ours = B.attention_bwd_ref(q, k, v, do, causal=causal)
+    theirs = torch_grads(q, k, v, do, causal)
+    for a, b_ in zip(ours, theirs):
+        assert a.shape == b_.shape
+        np.testing.assert_allclose(a, b_, rtol=1e-5, atol=1e-5)
+
+
 def test_rounding_variants_stay_close():
     """round_scaled_q and bf16_intermediates perturb at bf16 precision only."""
     rng = np.random.default_rng(6)
