@@ -25,6 +25,7 @@ a bounded sample, host cores).
 """
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -56,66 +57,31 @@ BURN_IN_S = 1.0
 PEAK_SCLK_MHZ = 2400.0
 
 
-class ClockSampler:
-    """Samples the GPU's engine (GFX) clock from amdsmi on a thread while the
-    timed step runs: start() before the burn-in's last half, stop() after the
-    timed loop.  The device is matched by PCI address to torch's cuda:0; with
-    amdsmi missing or unreadable every figure is None."""
-
-    def __init__(self, device):
-        self.handle = None
-        self.samples = []
-        try:
-            import amdsmi
-            amdsmi.amdsmi_init()
-            handles = amdsmi.amdsmi_get_processor_handles()
-            props = torch.cuda.get_device_properties(device)
-            bdf = None
-            if hasattr(props, "pci_bus_id"):
-                bdf = (f"{getattr(props, 'pci_domain_id', 0):04x}:{props.pci_bus_id:02x}:"
-                       f"{getattr(props, 'pci_device_id', 0):02x}")
-            for h in handles:
-                if bdf and amdsmi.amdsmi_get_gpu_device_bdf(h).lower().startswith(bdf):
-                    self.handle = h
-            if self.handle is None and len(handles) == 1:
-                self.handle = handles[0]
-            self.amdsmi = amdsmi
-        except Exception as e:  # pragma: no cover - depends on the box
-            log(f"clock sampling unavailable: {e}")
-
-    def read(self):
-        return self.amdsmi.amdsmi_get_clock_info(
-            self.handle, self.amdsmi.AmdSmiClkType.SYS)["clk"]
-
-    def start(self):
-        import threading
-        self.samples, self.stop_flag = [], threading.Event()
-        if self.handle is None:
-            return
-        def run():
-            while not self.stop_flag.is_set():
-                try:
-                    self.samples.append(float(self.read()))
-                except Exception:  # pragma: no cover
-                    return
-                time.sleep(0.002)
-        self.thread = threading.Thread(target=run, daemon=True)
-        self.thread.start()
-
-    def stop(self):
-        if self.handle is None:
-            return None
-        self.stop_flag.set()
-        self.thread.join()
-        if not self.samples:
-            return None
-        v = np.array(self.samples)
-        return {"median": float(np.median(v)), "min": float(v.min()), "max": float(v.max()),
-                "n": int(v.size)}
+def engine_clock(fn, ms):
+    """Engine clock (MHz) while fn runs back to back: about 250 ms of steps on
+    the current stream, and beside them, on a second stream (default
+    priority), the library's clock probe (fw_clock_probe: one wave that waits
+    40 ms, then counts shader-clock cycles against the 100 MHz reference clock
+    over 150 ms).  None if the probe is unavailable."""
+    from flywheel_tpu import _native as N
+    try:
+        lib = N.lib()
+    except Exception as e:  # pragma: no cover - the library is required elsewhere
+        log(f"clock probe unavailable: {e}")
+        return None
+    n = max(3, min(20000, int(250.0 / max(ms, 1e-3))))
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    N.check(lib.fw_clock_probe(N.ptr(out), 40000, 150000, ctypes.c_void_p(side.cuda_stream)))
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    cycles, ticks = out.tolist()
+    return round(100.0 * cycles / ticks, 1) if ticks > 0 else None
 
 
-CLOCK = None  # the ClockSampler of the run, set in main()
-LAST_CLOCK = None  # engine clock statistics of the last timed() call
+LAST_CLOCK = None  # engine clock (MHz) measured after the last timed() call
 
 
 def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
@@ -129,16 +95,10 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
     the ramp, not the kernel."""
     global LAST_CLOCK
     t0 = time.perf_counter()
-    sampling = False
     while time.perf_counter() - t0 < burn_in_s:
-        if CLOCK is not None and not sampling and time.perf_counter() - t0 > burn_in_s / 2:
-            CLOCK.start()
-            sampling = True
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
-    if CLOCK is not None and not sampling:
-        CLOCK.start()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -149,8 +109,9 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
         fn()
     end.record()
     torch.cuda.synchronize()
-    LAST_CLOCK = CLOCK.stop() if CLOCK is not None else None
-    return start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / steps
+    LAST_CLOCK = engine_clock(fn, ms)
+    return ms
 
 
 def cpu_time(fn, min_rounds=3):
@@ -829,19 +790,16 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     device = torch.device("cuda:0")
-    global CLOCK
-    CLOCK = ClockSampler(device)
     names = DEFAULT if args.workload == "all" else [args.workload]
     results = []
     for name in names:
         log(f"workload {name}")
         r = {**WORKLOADS, **EXTRA}[name](args, device)
         clk = LAST_CLOCK
-        r["roofline"]["sclk_mhz"] = None if clk is None else round(clk["median"], 1)
+        r["roofline"]["sclk_mhz"] = clk
         if clk is not None:
-            r["roofline"]["sclk_range_mhz"] = [clk["min"], clk["max"]]
             if r["roofline"]["bound"] == "mfma":
-                p = r["roofline"]["peak"] * clk["median"] / PEAK_SCLK_MHZ
+                p = r["roofline"]["peak"] * clk / PEAK_SCLK_MHZ
                 r["roofline"]["peak_at_clock"] = round(p, 1)
                 r["roofline"]["frac_at_clock"] = round(r["roofline"]["achieved"] / p, 4)
         log(f"{name}: {r['value']:.2f} {r['unit']} ({r['ms']:.4f} ms/step)"

@@ -149,3 +149,29 @@ extern "C" int fw_write_kv_cache_pages(const void *k, const void *v, void *kv_ca
       total_tokens, nheads_k, head_bytes, merged_heads(nheads_k, kv_dtype), num_rows);
   return check_launch("fw_write_pages_kernel");
 }
+
+namespace fw {
+// s_memrealtime ticks at 100 MHz; s_memtime at the shader clock.
+__global__ __launch_bounds__(64) void fw_clock_probe_kernel(unsigned long long *out,
+                                                            unsigned long long delay,
+                                                            unsigned long long window) {
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - r0 < delay) __builtin_amdgcn_s_sleep(8);
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - r1 < window) __builtin_amdgcn_s_sleep(8);
+  const unsigned long long c2 = __builtin_amdgcn_s_memtime(), r2 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[0] = c2 - c1;
+    out[1] = r2 - r1;
+  }
+}
+}  // namespace fw
+
+extern "C" int fw_clock_probe(unsigned long long *out, int delay_us, int window_us,
+                              fw_stream_t stream) {
+  FW_REQUIRE(out && delay_us >= 0 && window_us > 0 && delay_us <= 10000000 && window_us <= 10000000,
+             FW_ERR_VALUE, "fw_clock_probe: out required, delay and window in [0, 10 s]");
+  fw::fw_clock_probe_kernel<<<1, 64, 0, (hipStream_t)stream>>>(out, 100ull * delay_us,
+                                                               100ull * window_us);
+  return check_launch("fw_clock_probe");
+}

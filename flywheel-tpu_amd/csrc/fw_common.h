@@ -22,6 +22,7 @@ int check_launch(const char *what);
 // ---------------------------------------------------------------- vector types
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -185,6 +186,19 @@ __device__ __forceinline__ f32x16_t mfma32(const bf16x8_t &a, const bf16x8_t &b,
 }
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+// Compute units of the current device (cached per device).
+static inline int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
 inline size_t align_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
 inline int dtype_bytes(int kv_dtype) { return kv_dtype == FW_BF16 ? 2 : 1; }

@@ -711,19 +711,6 @@ static int chunk_keys_for(int P) {
   return ((64 * kTblPerLane - 1) * P + gcd) / 32 * 32;
 }
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
 
 struct DecodeLayout {
   int G, Rq, n_qtiles, rows_item, waves, groups, nw, occ;

@@ -58,6 +58,15 @@ struct PrefillArgs {
   // paged: first V dim this launch reads (a launch over a chunk of a head_dim_v
   // above 256 starts at that chunk's dims of the merged row's V head)
   int vdim0;
+  // Varlen / paged ping-pong kernel: key-split slots.  split_code[slot] is -1
+  // (the slot's whole key range) or 2 * pair + part: part 0 takes the first
+  // half of the slot's key tiles, part 1 the rest, and the workgroup of a
+  // (pair, head group) that finishes second merges the two (m, l, O)
+  // partials.  split_max = 0: no split slots (the arrays are unused).
+  const int32_t *split_code;
+  int *split_cnt;      // (split_max, head groups) arrival counters
+  float *split_part;   // (split_max, head groups, 2 parts) partials
+  int split_max;
 };
 
 // Varlen/paged workgroup -> (schedule slot, head group of 2^hpw_shift
@@ -609,6 +618,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 
   // ------------------------------------------------------------ tile decode
   int b = 0, hg, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
+  int split = -1;  // key split of the slot: -1 none, else 2 * pair + part
   if constexpr (MODE == FW_KV_DENSE) {
     const int ng = a.H >> a.hpw_shift;
     const int nbh = a.B * ng;
@@ -633,6 +643,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     if (slot >= a.sched[0]) return;
     seq = a.sched[1 + 2 * slot];
     q0 = a.sched[2 + 2 * slot];
+    if (a.split_max > 0) split = a.split_code[slot];
     if (seq < 0) {  // packed padding rows: out 0, lse -inf
       const int hp = (hg << a.hpw_shift) + (w >> wph_shift);
       const int r0 = q0 + 32 * rb + n;
@@ -681,8 +692,13 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
-  const int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
+  int t_begin = wg_hi > wg_lo ? wg_lo / kKT : 0;
+  int t_end = wg_hi > wg_lo ? (wg_hi + kKT - 1) / kKT : 0;
+  if (split >= 0) {  // key split: part 0 the first half of the tiles, part 1 the rest
+    const int mid = t_begin + (t_end - t_begin) / 2;
+    if (split & 1) t_begin = mid;
+    else t_end = mid;
+  }
   const int T = t_end - t_begin;
 
   // ---- global -> registers -> LDS: wave w moves key rows 8w .. 8w+7 of a
@@ -1146,6 +1162,98 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 
   // ------------------------------------------------------------ epilogue
   l_run += __shfl_xor(l_run, 32, 64);
+  if constexpr (MODE != FW_KV_DENSE) {
+    if (split >= 0) {
+      // Key split: both parts store their (m, l, O) partial; the second to
+      // arrive merges the other's into its own and writes the output.  No
+      // workgroup waits on another.  Partial of (pair, head group, part):
+      // wave w's 32 rows x 128 f32 dims, then (m, l) of its rows.
+      const int pair = split >> 1, part = split & 1;
+      const int ng = a.H >> a.hpw_shift;
+      constexpr size_t kPartO = (size_t)kPPWaves * 32 * 128;   // floats
+      constexpr size_t kPartF = kPartO + (size_t)kPPWaves * 32 * 2;
+      float *base = a.split_part + ((size_t)(pair * ng + hg) * 2) * kPartF;
+      float *mine = base + (size_t)part * kPartF, *other = base + (size_t)(part ^ 1) * kPartF;
+      // Coherence without cache maintenance: the partials go out and come back
+      // with device-scope (sc1) stores and loads, coherent at the device level
+      // one access at a time, so neither workgroup flushes or invalidates its
+      // L2 (which holds the other workgroups' K/V tiles), and every store is
+      // complete (vmcnt 0) before the arrival counter moves.  Rows are staged
+      // through LDS (the loop's buffers are free) so that each instruction
+      // moves 1 KiB of contiguous rows: wave w's 32 rows of 512 B at lds0 +
+      // 16 KiB w, 16-byte chunks XOR-swizzled by row.
+      const uint32_t sb = lds0 + (uint32_t)w * 16384u;
+      auto lds_at = [&](int r, int ch) {  // 16-byte chunk ch of staged row r
+        return sb + (uint32_t)r * 512u + 16u * (uint32_t)(ch ^ r);
+      };
+      // buffer accesses with the device-scope bit (sc1, cache policy 16)
+      constexpr int kSc1 = 16;
+      auto rsrc = [](const float *base) {
+        return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7ffffff0, 0x00020000);
+      };
+      const __amdgpu_buffer_rsrc_t wr = rsrc(mine + (size_t)w * 32 * 128);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          *(FW_LDS f32x4_t *)lds_at(n, 8 * c + 2 * rr + g) =
+              f32x4_t{oacc[c][4 * rr], oacc[c][4 * rr + 1], oacc[c][4 * rr + 2], oacc[c][4 * rr + 3]};
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // lane l moves chunk l % 32 of row 2i + l / 32
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 2 * i + (lane >> 5);
+        const u32x4_t v = *(const FW_LDS u32x4_t *)lds_at(r, lane & 31);
+        __builtin_amdgcn_raw_buffer_store_b128(v, wr, (r * 128 + 4 * (lane & 31)) * 4, 0, kSc1);
+      }
+      const __amdgpu_buffer_rsrc_t mlr = rsrc(mine + kPartO);
+      if (g == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, f32x2_t{m_run, l_run}), mlr,
+                                              (w * 32 + n) * 8, 0, kSc1);
+      __shared__ int arrival;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are done
+      __syncthreads();
+      if (tid == 0)
+        arrival = __hip_atomic_fetch_add(a.split_cnt + pair * ng + hg, 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (arrival == 0) return;  // first to arrive: the other part merges
+      const __amdgpu_buffer_rsrc_t orr = rsrc(other + (size_t)w * 32 * 128);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 2 * i + (lane >> 5);
+        *(FW_LDS u32x4_t *)lds_at(r, lane & 31) =
+            __builtin_amdgcn_raw_buffer_load_b128(orr, (r * 128 + 4 * (lane & 31)) * 4, 0, kSc1);
+      }
+      const f32x2_t ml = __builtin_bit_cast(
+          f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rsrc(other + kPartO), (w * 32 + n) * 8, 0, kSc1));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // The same operations in part order whichever part merges, so repeated
+      // calls give the same bits: x = x0 * f0, then fma(x1, f1, x).
+      const float m0 = part ? ml[0] : m_run, m1 = part ? m_run : ml[0];
+      const float Mx = fmaxf(m0, m1);
+      const float f0 = Mx == -INFINITY || m0 == -INFINITY ? 0.f : fast_exp2(m0 - Mx);
+      const float f1 = Mx == -INFINITY || m1 == -INFINITY ? 0.f : fast_exp2(m1 - Mx);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const f32x4_t o2 = *(const FW_LDS f32x4_t *)lds_at(n, 8 * c + 2 * rr + g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = part ? o2[e] : oacc[c][4 * rr + e];
+            const float x1 = part ? oacc[c][4 * rr + e] : o2[e];
+            oacc[c][4 * rr + e] = __builtin_fmaf(x1, f1, __fmul_rn(x0, f0));
+          }
+        }
+      {
+        const float l0 = part ? ml[1] : l_run, l1 = part ? l_run : ml[1];
+        l_run = __builtin_fmaf(l1, f1, __fmul_rn(l0, f0));
+      }
+      m_run = Mx;
+      __syncthreads();  // the staging below reuses other waves' LDS
+    }
+  }
   float M = m_run, Lsum = l_run, oscale = 1.f;
   if (a.sinks) {
     const float sk = a.sinks[h] * kLog2e;
@@ -1659,10 +1767,19 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
 // fill the tail (a greedy longest-first list schedule); padding tiles go last.
 // The order changes no result: every q tile is computed independently.
 constexpr int kSortTiles = 2048;
+// Key splits (split_max > 0, the ping-pong kernel): with W = tiles x ng
+// workgroups on `cus` compute units, one workgroup per CU at a time, the last
+// round of a heaviest-first list schedule runs W % cus workgroups while the
+// other CUs idle.  Splitting the k heaviest tiles in two along their keys
+// (k = the fewest that make the count a multiple of cus, at most split_max,
+// only tiles of >= kMinSplitCost key tiles, and only when W < 16 cus) evens
+// the rounds: their first halves go first, the unsplit tiles follow in cost
+// order, the second halves last.
+constexpr int kMinSplitCost = 8;
 __global__ __launch_bounds__(1024) void fw_prefill_schedule(
     const int32_t *cu_q, const int32_t *num_active, int B, int total_q, int32_t *sched,
     int max_tiles, int qt, const int32_t *cu_k, const int32_t *seqused_k, int plus_q, int wl,
-    int wr) {
+    int wr, int32_t *split_code, int *split_cnt, int split_max, int ng, int cus) {
   __shared__ int part[1024];
   __shared__ unsigned long long key[kSortTiles];
   __shared__ int eseq[kSortTiles], eq0[kSortTiles];
@@ -1699,10 +1816,28 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
       } else if (idx < max_tiles) {
         sched[1 + 2 * idx] = s;
         sched[2 + 2 * idx] = q0;
+        if (split_max > 0) split_code[idx] = -1;
       }
       ++idx;
     }
   }
+  int nsplit = 0;  // the nsplit heaviest tiles are split (ranks 0 .. nsplit - 1)
+  if (sort && split_max > 0) {
+    __shared__ int nbig;
+    if (tid == 0) nbig = 0;
+    for (int i = tid; i < split_max * ng; i += nt) split_cnt[i] = 0;
+    __syncthreads();
+    int mybig = 0;
+    for (int i = tid; i < real; i += nt) mybig += (int)(key[i] >> 32) >= kMinSplitCost;
+    if (mybig) atomicAdd(&nbig, mybig);
+    __syncthreads();
+    const long wgs = (long)real * ng;
+    if (wgs < 16l * cus) {
+      const int gap = (int)((cus - wgs % cus) % cus);
+      nsplit = min(min(split_max, nbig), (gap + ng - 1) / ng);
+    }
+  }
+  const int cap = max_tiles + split_max;  // schedule slots
   if (sort) {
     // Rank sort, descending: a tile's slot is the number of larger keys (keys
     // are distinct: the low word is the tile's index).  Every thread reads
@@ -1713,21 +1848,32 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
       const unsigned long long x = key[i];
       int rank = 0;
       for (int j = 0; j < real; ++j) rank += key[j] > x;
-      if (rank < max_tiles) {
+      // ranks below nsplit all hold tiles of >= kMinSplitCost key tiles
+      const bool split = rank < nsplit;
+      if (rank < cap) {
         sched[1 + 2 * rank] = eseq[i];
         sched[2 + 2 * rank] = eq0[i];
+        if (split_max > 0) split_code[rank] = split ? 2 * rank : -1;
+      }
+      if (split) {  // the second half's slot
+        const int r2 = real + rank;
+        sched[1 + 2 * r2] = eseq[i];
+        sched[2 + 2 * r2] = eq0[i];
+        split_code[r2] = 2 * rank + 1;
       }
     }
   }
   const int pad0 = nact > 0 ? cu_q[nact] : 0;
   const int npad = total_q > pad0 ? (total_q - pad0 + qt - 1) / qt : 0;
+  const int base = real + nsplit;
   for (int i = tid; i < npad; i += nt) {
-    if (real + i < max_tiles) {
-      sched[1 + 2 * (real + i)] = -1;
-      sched[2 + 2 * (real + i)] = pad0 + i * qt;
+    if (base + i < cap) {
+      sched[1 + 2 * (base + i)] = -1;
+      sched[2 + 2 * (base + i)] = pad0 + i * qt;
+      if (split_max > 0) split_code[base + i] = -1;
     }
   }
-  if (tid == 0) sched[0] = min(real + npad, max_tiles);
+  if (tid == 0) sched[0] = min(base + npad, cap);
 }
 
 static int max_sched_tiles(const fw_prefill_params *p, int qt) {
@@ -1763,10 +1909,35 @@ static int prefill_tile_rows(const fw_prefill_params *p) {
 
 using namespace fw;
 
+// Key-split pairs the schedule may create (the ping-pong kernel's varlen and
+// paged modes): enough to fill one round of the CUs, at most 32.
+static int split_pairs_max(const fw_prefill_params *p) {
+  if (p->kv_mode == FW_KV_DENSE || !use_pingpong(p)) return 0;
+  if (const char *e = getenv("FW_PREFILL_KEY_SPLIT"); e && e[0] == '0') return 0;
+  const int ng = p->nheads >> pp_head_shift(p);
+  return ng > 0 ? std::min(32, std::max(1, 256 / ng)) : 0;
+}
+constexpr size_t kSplitPartBytes = ((size_t)kPPWaves * 32 * 128 + kPPWaves * 32 * 2) * 4;
+
+struct PrefillWorkspace {
+  size_t sched, codes, cnt, part, total;  // byte offsets of each part, and the size
+};
+static PrefillWorkspace workspace_layout(const fw_prefill_params *p) {
+  const int slots = max_sched_tiles(p, prefill_tile_rows(p)) + split_pairs_max(p);
+  const int sm = split_pairs_max(p);
+  const size_t ng = sm ? (size_t)(p->nheads >> pp_head_shift(p)) : 0;
+  PrefillWorkspace w;
+  w.sched = 0;
+  w.codes = align_up((size_t)(1 + 2 * slots) * sizeof(int32_t), 256);
+  w.cnt = w.codes + (sm ? align_up((size_t)slots * sizeof(int32_t), 256) : 0);
+  w.part = w.cnt + align_up((size_t)sm * ng * sizeof(int), 256);
+  w.total = w.part + (size_t)sm * ng * 2 * kSplitPartBytes;
+  return w;
+}
+
 extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
   if (p->kv_mode == FW_KV_DENSE) return 0;
-  return align_up((size_t)(1 + 2 * max_sched_tiles(p, prefill_tile_rows(p))) * sizeof(int32_t),
-                  256);
+  return workspace_layout(p).total;
 }
 
 // Kernel choice (the host has checked the head dims): 128/128 -> the ping-pong
@@ -1900,6 +2071,10 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   const bool pingpong = use_pingpong(p);
   a.hpw_shift = pingpong ? pp_head_shift(p) : 0;
   a.vdim0 = 0;
+  a.split_max = 0;
+  a.split_code = nullptr;
+  a.split_cnt = nullptr;
+  a.split_part = nullptr;
   const int qt_rows = prefill_tile_rows(p);
   const int head_groups = p->nheads >> a.hpw_shift;
   a.n_qt = (p->seqlen_q + qt_rows - 1) / qt_rows;
@@ -1952,6 +2127,12 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);
   const bool varlen = p->kv_mode == FW_KV_VARLEN;
+  const PrefillWorkspace wl = workspace_layout(p);
+  uint8_t *ws = (uint8_t *)p->workspace;
+  a.split_max = split_pairs_max(p);
+  a.split_code = a.split_max ? (const int32_t *)(ws + wl.codes) : nullptr;
+  a.split_cnt = a.split_max ? (int *)(ws + wl.cnt) : nullptr;
+  a.split_part = a.split_max ? (float *)(ws + wl.part) : nullptr;
   // a thread per sequence and per q tile (up to 1024): the rank sort's pass
   int sched_threads = 64;
   while (sched_threads < 1024 &&
@@ -1961,11 +2142,12 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
                                          (int32_t *)p->workspace, max_tiles, qt_rows,
                                          varlen ? p->cu_seqlens_k : nullptr,
                                          varlen ? nullptr : p->seqused_k, a.seqused_plus_q,
-                                         a.wl, a.wr);
+                                         a.wl, a.wr, (int32_t *)a.split_code, a.split_cnt,
+                                         a.split_max, head_groups, device_cus());
   int st = check_launch("fw_prefill_schedule");
   if (st != FW_OK) return st;
   // one workgroup per (schedule slot, head group); see sched_slot
-  dim3 grid(max_tiles * head_groups);
+  dim3 grid((max_tiles + a.split_max) * head_groups);
   if (p->kv_mode == FW_KV_VARLEN) {
     const int w = v_chunk_width(d, dv);
     for (int c = 0; c * w < dv; ++c)

@@ -115,6 +115,7 @@ SIGNATURES = {
     "fw_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(PrefillParams)]),
     "fw_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillParams), _c_p]),
     "fw_rotary": (ctypes.c_int, [ctypes.POINTER(RotaryParams), _c_p]),
+    "fw_clock_probe": (ctypes.c_int, [_c_p, _i32, _i32, _c_p]),
     "fw_attn_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnBwdParams)]),
     "fw_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _c_p]),
 }

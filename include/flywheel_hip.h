@@ -323,6 +323,17 @@ typedef struct fw_rotary_params {
 
 int fw_rotary(const fw_rotary_params *p, fw_stream_t stream);
 
+/*
+ * Measurement helper with no counterpart in the reference: one wave on the
+ * stream waits delay_us, then counts shader-clock cycles (s_memtime) over
+ * window_us of the 100 MHz reference clock (s_memrealtime) and stores
+ * (cycles, reference ticks) in out[0..1] (device memory).  Run beside a
+ * workload on another stream it gives the engine clock of the XCD it landed
+ * on while that workload ran: clock MHz = 100 * out[0] / out[1].  The wait
+ * is bounded by the reference clock, so the wave always exits.
+ */
+int fw_clock_probe(unsigned long long *out, int delay_us, int window_us, fw_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

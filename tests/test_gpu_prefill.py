@@ -439,3 +439,75 @@ def test_paged_varlen_read_only_wide_heads(dtype, hd):
     assert_close(got[:cu[-1]], ro[:cu[-1]], fp8=dtype != "bf16")
     assert_lse(lse.cpu().numpy()[:, :cu[-1]], rl[:, :cu[-1]])
     assert not got[cu[-1]:].any()
+
+
+@pytest.mark.parametrize("dtype,window,softcap,sinks", [
+    ("bf16", -1, 0.0, False), ("bf16", 1000, 30.0, True), ("e4m3", -1, 50.0, False),
+    ("bf16", 300, 0.0, True)])
+def test_key_split_slots(dtype, window, softcap, sinks):
+    """Few heavy q tiles over long prior contexts: the schedule splits the
+    heaviest slots in two along their keys (fewer workgroups than CUs), each
+    half stores an (m, l, O) partial and the second to finish merges them.
+    Windows leave rows with no key in one half; sinks fold in after the
+    merge."""
+    announce(f"key split {dtype} window {window} softcap {softcap} sinks {sinks}")
+    rng = np.random.default_rng(400 + window)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (0.8, 1.25)
+    h, hk = 32, 8
+    qlens = [300, 100, 64]
+    prefix = [4000, 700, 2500]
+    totals = np.array(qlens) + np.array(prefix)
+    case = PagedCase(rng, batch=3, nheads=h, nheads_k=hk, lengths=totals, new_tokens=[0] * 3,
+                     dtype=dt, k_descale=ks, v_descale=vs)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = randn(rng, (cu[-1], h, 128))
+    sk = rng.standard_normal(h).astype(np.float32) if sinks else None
+    w2 = (window, 0) if window >= 0 else (-1, -1)
+    out, lse = flash_attn_varlen_func(
+        to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
+        torch.tensor(cu, device=DEV), None, max(qlens), int(totals.max()), causal=True,
+        window_size=w2, softcap=softcap, return_softmax_lse=True,
+        block_table=torch.tensor(case.table, device=DEV),
+        seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), k_descale=ks,
+        v_descale=vs, nheads_k=hk, learnable_sink=None if sk is None else torch.tensor(sk, device=DEV))
+    torch.cuda.synchronize()
+    kp, vp = case.kv_pages(case.pool_codes)
+    ro, rl = A.ragged_reference(q, kp, vp, cu, totals, case.table, causal=True,
+                                window_left=None if window < 0 else window, softcap=softcap,
+                                sinks=sk, k_descale=ks, v_descale=vs, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy().transpose(1, 0, 2), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
+    # the same call again: the arrival counters start from zero every call
+    out2 = flash_attn_varlen_func(
+        to_dev_bf16(np.ascontiguousarray(q.transpose(1, 0, 2))), case.pool(), None,
+        torch.tensor(cu, device=DEV), None, max(qlens), int(totals.max()), causal=True,
+        window_size=w2, softcap=softcap, block_table=torch.tensor(case.table, device=DEV),
+        seqused_k=torch.tensor(totals, dtype=torch.int32, device=DEV), k_descale=ks,
+        v_descale=vs, nheads_k=hk, learnable_sink=None if sk is None else torch.tensor(sk, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_key_split_packed_varlen():
+    """The packed-varlen (non-paged) mode of the same kernel with split slots."""
+    announce("key split packed varlen")
+    rng = np.random.default_rng(410)
+    h, hk, d = 16, 4, 128
+    ql = np.array([256, 70]); kl = np.array([3000, 1500])
+    cu_q = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(kl)]).astype(np.int32)
+    q, k, v = randn(rng, (h, cu_q[-1], d)), randn(rng, (hk, cu_k[-1], d)), randn(rng, (hk, cu_k[-1], d))
+    out, lse = flash_attn_varlen_func(to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v),
+                                      torch.tensor(cu_q, device=DEV), torch.tensor(cu_k, device=DEV),
+                                      int(ql.max()), int(kl.max()), causal=True,
+                                      return_softmax_lse=True)
+    torch.cuda.synchronize()
+    outs, lses = out.float().cpu().numpy(), lse.cpu().numpy()
+    for s in range(2):
+        qs_ = q[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2)[None]
+        ks_ = k[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        vs_ = v[:, cu_k[s]:cu_k[s + 1]].transpose(1, 0, 2)[None]
+        ro, rl = A.attention_ref(qs_, ks_, vs_, causal=True, round_scaled_q=True)
+        assert_close(outs[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2), ro[0], what=f"seq {s}")
+        assert_lse(lses[:, cu_q[s]:cu_q[s + 1]], rl[0])
