@@ -45,6 +45,7 @@ struct DecodeArgs {
   const int32_t *num_active;
   float *ws_o;   // [segments][items][rows_item][D] unnormalised partial O
   float2 *ws_ml; // [segments][items][rows_item] (running max in log2 units, row sum)
+  int2 *ws_rows; // [B] (first key range, key range count) of a row with keys
   int B, Sq, H, Hk, G, Rq, n_qtiles, P, max_pages, CH;
   // Token-row geometry: a token row holds CH head rows; KV head h's K row is
   // head row kstep*h and its V row head row kstep*h + vhead, vdelta bytes
@@ -259,6 +260,10 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
     int base;
     const int T = row_tiles(a, b, nact, base);
     const int seg_lo = max(g0 - off, 0), seg_hi = min(g1 - off, T);
+    // the range holding the row's first tile records the row's ranges for
+    // fw_decode_combine
+    if (T > 0 && off >= g0 && blockIdx.y == 0 && threadIdx.x == 0)
+      a.ws_rows[b] = make_int2(x, (off + T - 1) / per - x + 1);
     off += T;
     if (seg_hi <= seg_lo) continue;
     const int L0 = a.cache_seqlens[b];
@@ -493,7 +498,8 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       // tile's loads in flight during the compute (a two-stage register ring)
       // was slower (C3 703 against 675 us): the same random page reads with
       // more of them outstanding stream ~6% slower here, in a plain read probe
-      // as in this kernel.
+      // as in this kernel.  Loading two fp8 tiles at a time (the bf16 kernel's
+      // bytes in flight) was slower too (C5 1449 against 1434 us).
       for (int tb = cb; tb < ce; tb += 32) {
         DecodeTile<KV, D> t0;
         load_tile(tb, t0);
@@ -592,24 +598,14 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
   const bool active = b < nact;
   // This row's segments: key ranges x_first .. x_last of the decode launch
   // (a row longer than the tiles counted there has none past them).
+  // This row's segments, as the decode launch recorded them.
   int nsp = 0, x_first = 0;
   if (active) {
     int base;
-    const int T = row_tiles(a, b, nact, base);
-    if (T > 0) {
-      const int total_t = total_tiles(a, nact, lane);
-      const int per = (total_t + a.nw - 1) / a.nw;
-      int off;
-      int acc = 0;
-      // tiles of rows before b
-      for (int c0 = 0; c0 < b; c0 += 64) {
-        int bs;
-        const int t = c0 + lane < b ? row_tiles(a, c0 + lane, nact, bs) : 0;
-        acc += wave_sum(t);
-      }
-      off = acc;
-      x_first = off / per;
-      nsp = (off + T - 1) / per - x_first + 1;
+    if (row_tiles(a, b, nact, base) > 0) {
+      const int2 rs = a.ws_rows[b];
+      x_first = rs.x;
+      nsp = rs.y;
     }
   }
   const int n_items = a.Hk * a.n_qtiles;
@@ -714,7 +710,7 @@ static int chunk_keys_for(int P) {
 
 struct DecodeLayout {
   int G, Rq, n_qtiles, rows_item, waves, groups, nw, occ;
-  size_t o_bytes, ml_bytes;
+  size_t o_bytes, ml_bytes, rows_bytes;
 };
 
 static int decode_layout(const fw_decode_params *p, DecodeLayout *L) {
@@ -748,6 +744,7 @@ static int decode_layout(const fw_decode_params *p, DecodeLayout *L) {
   const size_t segs = (size_t)L->nw + p->batch;
   L->o_bytes = align_up(segs * items * L->rows_item * p->head_dim * sizeof(float), 256);
   L->ml_bytes = align_up(segs * items * L->rows_item * sizeof(float2), 256);
+  L->rows_bytes = align_up((size_t)p->batch * sizeof(int2), 256);
   return FW_OK;
 }
 
@@ -763,7 +760,7 @@ using namespace fw;
 extern "C" size_t fw_paged_decode_workspace_bytes(const fw_decode_params *p) {
   DecodeLayout L;
   if (decode_layout(p, &L) != FW_OK) return 0;
-  return L.o_bytes + L.ml_bytes;
+  return L.o_bytes + L.ml_bytes + L.rows_bytes;
 }
 
 // The launch of both entry points: ws / ws_bytes is the partial buffer (the
@@ -779,9 +776,9 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
              "a fused append takes one query token per row; got seqlen_q=%d", p->seqlen_q);
   FW_REQUIRE((p->k_new == nullptr) == (p->v_new == nullptr), FW_ERR_VALUE,
              "k_new and v_new must be given together");
-  FW_REQUIRE(ws_bytes >= L.o_bytes + L.ml_bytes && ws, FW_ERR_VALUE,
+  FW_REQUIRE(ws_bytes >= L.o_bytes + L.ml_bytes + L.rows_bytes && ws, FW_ERR_VALUE,
              "workspace of %zu bytes is smaller than the %zu needed", ws_bytes,
-             L.o_bytes + L.ml_bytes);
+             L.o_bytes + L.ml_bytes + L.rows_bytes);
   FW_REQUIRE(p->q && p->kv_cache && p->cache_seqlens && p->block_table && p->out, FW_ERR_VALUE,
              "q, kv_cache, cache_seqlens, block_table and out are required");
   FW_REQUIRE(!p->v_cache || (p->kv_dtype == FW_BF16 && p->max_pages == 1), FW_ERR_VALUE,
@@ -797,6 +794,7 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
   a.num_active = p->num_active;
   a.ws_o = (float *)ws;
   a.ws_ml = (float2 *)((char *)ws + L.o_bytes);
+  a.ws_rows = (int2 *)((char *)ws + L.o_bytes + L.ml_bytes);
   a.B = p->batch;
   a.Sq = p->seqlen_q;
   a.H = p->nheads;
@@ -886,7 +884,7 @@ extern "C" int fw_paged_decode_noalloc(const fw_decode_params *p, fw_stream_t st
   DecodeLayout L;
   int st = decode_layout(p, &L);
   if (st != FW_OK) return st;
-  const size_t need = L.o_bytes + L.ml_bytes;
+  const size_t need = L.o_bytes + L.ml_bytes + L.rows_bytes;
   FW_REQUIRE(need <= FW_DECODE_SCRATCH_BYTES, FW_ERR_VALUE,
              "fw_paged_decode_noalloc: this call needs %zu bytes of partials, more than the"
              " library's static %zu (FW_DECODE_SCRATCH_BYTES); use fw_paged_decode with a"
