@@ -87,6 +87,8 @@ LAST_CLOCK = None  # engine clock (MHz) measured after the last timed() call
 def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
     """Mean ms per call of fn over `steps` calls after `warmup`, bracketed by
     events on the current stream (the stream every kernel is launched on).
+    The engine clock of the workload (LAST_CLOCK) is measured between the
+    burn-in and the warm-up.
 
     Before the warm-up calls the same step runs untimed for burn_in_s seconds
     (the reference's protocol runs rounds of at least 0.5 s,
@@ -95,10 +97,16 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
     the ramp, not the kernel."""
     global LAST_CLOCK
     t0 = time.perf_counter()
+    n_burn = 0
     while time.perf_counter() - t0 < burn_in_s:
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
+        n_burn += 10
+    # the engine clock under the same load, measured before the timed steps so
+    # that they stay the last dispatches of the workload (a kernel trace's
+    # final `steps` dispatches are the timed ones)
+    LAST_CLOCK = engine_clock(fn, 1e3 * (time.perf_counter() - t0) / max(n_burn, 1))
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -109,9 +117,7 @@ def timed(fn, steps, warmup, burn_in_s=BURN_IN_S):
         fn()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    LAST_CLOCK = engine_clock(fn, ms)
-    return ms
+    return start.elapsed_time(end) / steps
 
 
 def cpu_time(fn, min_rounds=3):
