@@ -525,3 +525,68 @@ def flash_attn_varlen_func(
     if return_softmax_lse:
         return out, lse
     return out
+
+
+def _flash_attn_func_pcp_causal_offset(
+    q,
+    k,
+    v,
+    causal_offset,
+    *,
+    softmax_scale=None,
+    return_softmax_lse=False,
+    heads_outer_fold=False,
+    interpret=False,
+):
+    """Dense causal forward with a device-side Q-position offset (reference
+    prefill.py:344-434, the context-parallel caller's internal entry): query i
+    sees keys 0 .. causal_offset + i.  q/k/v are head-major (1, nheads, seqlen,
+    headdim), or (nheads, 1, seqlen, headdim) with heads_outer_fold; bf16; the
+    caller guarantees 0 <= offset and offset + q_len <= kv_len.
+
+    Runs the packed-varlen kernel on one sequence whose key count is
+    offset + q_len, computed on the device (no host read of the offset): its
+    bottom-right causal alignment then puts query i at key offset + i, and the
+    keys past offset + q_len, which no query sees, are never read."""
+    del interpret
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("runtime-offset attention requires 4-D head-major Q/K/V.")
+    batch_axis, head_axis = (1, 0) if heads_outer_fold else (0, 1)
+    batch, nheads = q.shape[batch_axis], q.shape[head_axis]
+    q_len, head_dim = q.shape[2], q.shape[3]
+    if batch != 1 or k.shape[batch_axis] != 1 or v.shape[batch_axis] != 1:
+        raise ValueError("runtime-offset attention requires batch_size == 1.")
+    if tuple(k.shape) != tuple(v.shape) or k.shape[3] != head_dim:
+        raise ValueError("K/V must share shape and Q/K head dimensions must match.")
+    nkv, kv_len = k.shape[head_axis], k.shape[2]
+    if nheads % nkv:
+        raise ValueError("Q heads must be divisible by KV heads.")
+    if q_len <= 0 or kv_len < q_len:
+        raise ValueError("runtime-offset attention requires a positive Q length, a positive KV"
+                         " length, and kv_len >= q_len.")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise NotImplementedError("runtime-offset attention supports bf16 only.")
+    off = as_tensor(causal_offset)
+    if off.numel() != 1 or off.is_floating_point() or off.dtype == torch.bool:
+        raise ValueError("causal_offset must be one integer scalar.")
+    N.require_device(q, k, v)
+    device = q.device
+    d = head_dim
+    # (1, H, S, D) and (H, 1, S, D) are both (H, S, D) in memory
+    qp, kp, vp = (t.contiguous().reshape(t.shape[head_axis], t.shape[2], d) for t in (q, k, v))
+    off_dev = off.reshape(1).to(device=device, dtype=torch.int32)
+    cu_q = torch.tensor([0, q_len], dtype=torch.int32, device=device)
+    cu_k = torch.cat([torch.zeros(1, dtype=torch.int32, device=device), off_dev + q_len])
+    out = qp.new_empty((nheads, q_len, d))
+    lse = (torch.empty((nheads, q_len), dtype=torch.float32, device=device)
+           if return_softmax_lse else None)
+    _run_prefill(N.FW_KV_VARLEN, qp, kp, vp, out, lse, qs=(0, q_len * d, d),
+                 ks=(0, kv_len * d, d), vs=(0, kv_len * d, d), os_=(0, q_len * d, d),
+                 ls=(0, q_len), batch=1, nheads=nheads, nheads_k=nkv, head_dim=d,
+                 seqlen_q=q_len, seqlen_k=kv_len, causal=True, window_size=(-1, -1),
+                 softmax_scale=resolve_scale(softmax_scale, d), softcap=0.0, sinks=None,
+                 cu_q=cu_q, cu_k=cu_k, max_seqlen_q=q_len)
+    out = out.reshape(q.shape)
+    if return_softmax_lse:
+        return out, lse.reshape(1, nheads, q_len)  # (batch, nheads, q_len) either way
+    return out

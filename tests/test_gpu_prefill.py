@@ -511,3 +511,31 @@ def test_key_split_packed_varlen():
         ro, rl = A.attention_ref(qs_, ks_, vs_, causal=True, round_scaled_q=True)
         assert_close(outs[:, cu_q[s]:cu_q[s + 1]].transpose(1, 0, 2), ro[0], what=f"seq {s}")
         assert_lse(lses[:, cu_q[s]:cu_q[s + 1]], rl[0])
+
+
+@pytest.mark.parametrize("h,hk,q_len,kv_len,offset,fold", [
+    (8, 2, 300, 1000, 0, False), (8, 2, 300, 1000, 700, False), (4, 4, 129, 700, 333, True),
+    (16, 2, 1024, 4096, 2048, False)])
+def test_runtime_causal_offset(h, hk, q_len, kv_len, offset, fold):
+    """The dense forward with a device-side causal offset (reference
+    prefill.py:344-434): query i sees keys 0 .. offset + i; against the oracle
+    on the first offset + q_len keys with bottom-right causal alignment."""
+    from flywheel_tpu.prefill import _flash_attn_func_pcp_causal_offset
+    announce(f"runtime causal offset h{h}/{hk} q{q_len} kv{kv_len} off{offset} fold{fold}")
+    rng = np.random.default_rng(500 + offset)
+    q, k, v = randn(rng, (1, q_len, h, 128)), randn(rng, (1, kv_len, hk, 128)), randn(rng, (1, kv_len, hk, 128))
+    hm = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+    dev = [to_dev_bf16(hm(x)) for x in (q, k, v)]
+    if fold:
+        dev = [t.transpose(0, 1).contiguous() for t in dev]
+    out, lse = _flash_attn_func_pcp_causal_offset(
+        *dev, torch.tensor(offset, dtype=torch.int32, device=DEV), return_softmax_lse=True,
+        heads_outer_fold=fold)
+    torch.cuda.synchronize()
+    if fold:
+        out = out.transpose(0, 1)
+    assert lse.shape == (1, h, q_len)
+    n = offset + q_len
+    ro, rl = A.attention_ref(q, k[:, :n], v[:, :n], causal=True, round_scaled_q=True)
+    assert_close(out.float().cpu().numpy().transpose(0, 2, 1, 3), ro)
+    assert_lse(lse.cpu().numpy(), rl)

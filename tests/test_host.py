@@ -370,3 +370,22 @@ def test_internal_exports_warn():
     assert mch(8, torch.bfloat16) == 16 and mch(3, torch.float8_e4m3fn) == 8
     with pytest.raises(AttributeError):
         flywheel_tpu.not_an_export
+
+
+def test_runtime_causal_offset_errors():
+    """_flash_attn_func_pcp_causal_offset's checks (reference prefill.py:362-400),
+    raised before anything touches a device."""
+    from flywheel_tpu.prefill import _flash_attn_func_pcp_causal_offset as f
+    q, k = bf(1, 4, 64, 128), bf(1, 2, 128, 128)
+    with pytest.raises(ValueError, match="4-D"):
+        f(bf(4, 64, 128), k, k, 0)
+    with pytest.raises(ValueError, match="batch_size == 1"):
+        f(bf(2, 4, 64, 128), bf(2, 2, 128, 128), bf(2, 2, 128, 128), 0)
+    with pytest.raises(ValueError, match="kv_len >= q_len"):
+        f(bf(1, 4, 256, 128), k, k, 0)
+    with pytest.raises(ValueError, match="divisible"):
+        f(bf(1, 3, 64, 128), k, k, 0)
+    with pytest.raises(ValueError, match="one integer scalar"):
+        f(q, k, k, torch.tensor([1.5]))
+    with pytest.raises(NotImplementedError, match="bf16"):
+        f(q.float(), k.float(), k.float(), 0)
