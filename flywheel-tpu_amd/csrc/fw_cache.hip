@@ -36,53 +36,11 @@ int check_launch(const char *what) {
   return FW_OK;
 }
 
-// One merged row: chunk c (16 bytes) of head row hr = c / chunks_per_head.
-__device__ __forceinline__ u32x4_t merged_chunk(const uint8_t *k_row, const uint8_t *v_row, int c,
-                                                int chunks_per_head, int nheads_k) {
-  const int hr = c / chunks_per_head;
-  const int off = (c % chunks_per_head) * 16;
-  const int kvh = hr >> 1;
-  if (kvh >= nheads_k) return u32x4_t{0u, 0u, 0u, 0u};
-  const uint8_t *src = (hr & 1 ? v_row : k_row) + (size_t)kvh * chunks_per_head * 16 + off;
-  return *(const u32x4_t *)src;
-}
-
-__global__ __launch_bounds__(256) void fw_append_kernel(
-    uint8_t *cache, const uint8_t *k, const uint8_t *v, const int32_t *cu, const int32_t *lens,
-    const int32_t *table, const int32_t *num_active, int B, int T, int Hk, int head_bytes, int CH,
-    int P, int num_pages, int max_pages) {
-  const int i = blockIdx.x;
-  const int nact = num_active ? min(max(*num_active, 0), B) : B;
-  int r, first;
-  if (cu) {
-    if (i >= cu[nact]) return;  // rows past the last active request are padding
-    // request r: the last r with cu[r] <= i
-    int lo = 0, hi = nact;  // cu[lo] <= i < cu[hi]
-    while (hi - lo > 1) {
-      int mid = (lo + hi) >> 1;
-      if (cu[mid] <= i) lo = mid; else hi = mid;
-    }
-    r = lo;
-    first = cu[r];
-    if (i < first) return;
-  } else {  // T / B tokens per request
-    const int per = T / B;
-    r = i / per;
-    first = r * per;
-    if (r >= nact) return;
-  }
-  const int pos = lens[r] + (i - first);
-  if (pos < 0 || pos / P >= max_pages) return;
-  const int page = table[(size_t)r * max_pages + pos / P];
-  if (page < 0 || page >= num_pages) return;
-  const size_t row_bytes = (size_t)CH * head_bytes;
-  uint8_t *dst = cache + ((size_t)page * P + pos % P) * row_bytes;
-  const uint8_t *k_row = k + (size_t)i * Hk * head_bytes;
-  const uint8_t *v_row = v + (size_t)i * Hk * head_bytes;
-  const int cph = head_bytes / 16;
-  const int nchunks = CH * cph;
-  for (int c = threadIdx.x; c < nchunks; c += blockDim.x)
-    *(u32x4_t *)(dst + (size_t)c * 16) = merged_chunk(k_row, v_row, c, cph, Hk);
+// 16 new tokens per workgroup, 16 lanes per token (append_token_rows,
+// fw_common.h): the per-token metadata walk (request, position, page) runs for
+// 16 tokens at once instead of one per workgroup.
+__global__ __launch_bounds__(256) void fw_append_kernel(AppendArgs a) {
+  append_token_rows(a, blockIdx.x);
 }
 
 __global__ __launch_bounds__(256) void fw_write_pages_kernel(
@@ -126,10 +84,11 @@ extern "C" int fw_append_ragged(void *kv_cache, const void *k, const void *v,
   FW_REQUIRE(head_bytes % 16 == 0, FW_ERR_VALUE, "head_dim %d is not a multiple of 16 bytes",
              head_dim);
   if (total_tokens <= 0) return FW_OK;
-  fw_append_kernel<<<total_tokens, 256, 0, (hipStream_t)stream>>>(
-      (uint8_t *)kv_cache, (const uint8_t *)k, (const uint8_t *)v, cu_seqlens, cache_seqlens,
-      block_table, num_active, batch, total_tokens, nheads_k, head_bytes,
-      merged_heads(nheads_k, kv_dtype), page_size, num_pages, max_pages);
+  const AppendArgs a{(uint8_t *)kv_cache, (const uint8_t *)k, (const uint8_t *)v, cu_seqlens,
+                     cache_seqlens, block_table, num_active, batch, total_tokens, nheads_k,
+                     head_bytes, merged_heads(nheads_k, kv_dtype), page_size, num_pages,
+                     max_pages};
+  fw_append_kernel<<<append_blocks(total_tokens), 256, 0, (hipStream_t)stream>>>(a);
   return check_launch("fw_append_kernel");
 }
 

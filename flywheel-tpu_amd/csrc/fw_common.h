@@ -186,6 +186,84 @@ __device__ __forceinline__ f32x16_t mfma32(const bf16x8_t &a, const bf16x8_t &b,
 }
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+// ---- ragged append of new K/V token rows into the merged paged pool
+// (fw_append_ragged; also fused into fw_prefill's launch).  Token i belongs
+// to the request r with cu[r] <= i < cu[r + 1] (or T / B tokens per request
+// without cu) and lands at position lens[r] + (i - cu[r]) of that request.
+struct AppendArgs {
+  uint8_t *cache;
+  const uint8_t *k, *v;  // (T, Hk, head_bytes) rows
+  const int32_t *cu, *lens, *table, *num_active;
+  int B, T, Hk, head_bytes, CH, P, num_pages, max_pages;
+};
+constexpr int kAppendTokensPerBlock = 16;  // 256 threads: 16 lanes a token
+inline int append_blocks(int T) { return (T + kAppendTokensPerBlock - 1) / kAppendTokensPerBlock; }
+
+// Chunk c (16 bytes) of a merged token row: head row hr = c / chunks_per_head
+// is K (even) or V (odd) of KV head hr / 2; head rows past 2 * Hk (an fp8
+// pool's pad head) are zero.
+__device__ __forceinline__ u32x4_t merged_chunk(const uint8_t *k_row, const uint8_t *v_row, int c,
+                                                int chunks_per_head, int nheads_k) {
+  const int hr = c / chunks_per_head;
+  const int off = (c % chunks_per_head) * 16;
+  const int kvh = hr >> 1;
+  if (kvh >= nheads_k) return u32x4_t{0u, 0u, 0u, 0u};
+  const uint8_t *src = (hr & 1 ? v_row : k_row) + (size_t)kvh * chunks_per_head * 16 + off;
+  return *(const u32x4_t *)src;
+}
+
+// Workgroup `blk` (256 threads) writes tokens 16 blk .. 16 blk + 15.  Rows past
+// the last active request, positions past the table and page ids outside
+// [0, num_pages) write nothing.
+__device__ __forceinline__ void append_token_rows(const AppendArgs &a, int blk) {
+  const int i = blk * kAppendTokensPerBlock + (int)(threadIdx.x >> 4);
+  const int lane = threadIdx.x & 15;
+  if (i >= a.T) return;
+  const int nact = a.num_active ? min(max(*a.num_active, 0), a.B) : a.B;
+  int r, first;
+  if (a.cu) {
+    if (i >= a.cu[nact]) return;  // rows past the last active request are padding
+    int lo = 0, hi = nact;  // cu[lo] <= i < cu[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.cu[mid] <= i) lo = mid; else hi = mid;
+    }
+    r = lo;
+    first = a.cu[r];
+    if (i < first) return;
+  } else {  // T / B tokens per request
+    const int per = a.T / a.B;
+    r = i / per;
+    first = r * per;
+    if (r >= nact) return;
+  }
+  const int pos = a.lens[r] + (i - first);
+  if (pos < 0 || pos / a.P >= a.max_pages) return;
+  const int page = a.table[(size_t)r * a.max_pages + pos / a.P];
+  if (page < 0 || page >= a.num_pages) return;
+  const size_t row_bytes = (size_t)a.CH * a.head_bytes;
+  uint8_t *dst = a.cache + ((size_t)page * a.P + pos % a.P) * row_bytes;
+  const uint8_t *k_row = a.k + (size_t)i * a.Hk * a.head_bytes;
+  const uint8_t *v_row = a.v + (size_t)i * a.Hk * a.head_bytes;
+  const int cph = a.head_bytes / 16;
+  const int nchunks = a.CH * cph;
+  // eight loads in flight before their stores (the compiler cannot reorder a
+  // load past a store that may alias it)
+  for (int c0 = lane; c0 < nchunks; c0 += 8 * 16) {
+    u32x4_t x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 16 * j;
+      x[j] = c < nchunks ? merged_chunk(k_row, v_row, c, cph, a.Hk) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + 16 * j;
+      if (c < nchunks) *(u32x4_t *)(dst + (size_t)c * 16) = x[j];
+    }
+  }
+}
+
 // Compute units of the current device (cached per device).
 static inline int device_cus() {
   static int cus[64];

@@ -1776,14 +1776,39 @@ constexpr int kSortTiles = 2048;
 // the rounds: their first halves go first, the unsplit tiles follow in cost
 // order, the second halves last.
 constexpr int kMinSplitCost = 8;
-__global__ __launch_bounds__(1024) void fw_prefill_schedule(
-    const int32_t *cu_q, const int32_t *num_active, int B, int total_q, int32_t *sched,
-    int max_tiles, int qt, const int32_t *cu_k, const int32_t *seqused_k, int plus_q, int wl,
-    int wr, int32_t *split_code, int *split_cnt, int split_max, int ng, int cus) {
+struct SchedArgs {
+  const int32_t *cu_q, *num_active;
+  int B, total_q;
+  int32_t *sched;
+  int max_tiles, qt;
+  const int32_t *cu_k, *seqused_k;
+  int plus_q, wl, wr;
+  int32_t *split_code;
+  int *split_cnt;
+  int split_max, ng, cus;
+};
+// The schedule, run by one workgroup of blockDim.x threads (a power of two,
+// 64 .. 1024).
+__device__ __forceinline__ void schedule_body(const SchedArgs &sa) {
+  const int32_t *cu_q = sa.cu_q, *num_active = sa.num_active, *cu_k = sa.cu_k,
+                *seqused_k = sa.seqused_k;
+  const int B = sa.B, total_q = sa.total_q, max_tiles = sa.max_tiles, qt = sa.qt;
+  const int plus_q = sa.plus_q, wl = sa.wl, wr = sa.wr, split_max = sa.split_max, ng = sa.ng,
+            cus = sa.cus;
+  int32_t *sched = sa.sched, *split_code = sa.split_code;
+  int *split_cnt = sa.split_cnt;
   __shared__ int part[1024];
   __shared__ unsigned long long key[kSortTiles];
   __shared__ int eseq[kSortTiles], eq0[kSortTiles];
   const int tid = threadIdx.x, nt = blockDim.x;  // nt: a power of two, 64 .. 1024
+  {
+    // one round trip brings every input of a batch up to nt sequences into
+    // the caches (the loops below read them in dependent steps)
+    const int w0 = num_active ? *num_active : 0;
+    const int w1 = tid <= B ? cu_q[tid] : 0;
+    const int w2 = tid < B ? (cu_k ? cu_k[tid + 1] : seqused_k[tid]) : 0;
+    asm volatile("" ::"v"(w0 + w1 + w2));
+  }
   const int nact = num_active ? min(max(*num_active, 0), B) : B;
   const int per = (nact + nt - 1) / nt;
   const int s0 = tid * per, s1 = min(nact, s0 + per);
@@ -1874,6 +1899,16 @@ __global__ __launch_bounds__(1024) void fw_prefill_schedule(
     }
   }
   if (tid == 0) sched[0] = min(base + npad, cap);
+}
+
+__global__ __launch_bounds__(1024) void fw_prefill_schedule(SchedArgs sa) { schedule_body(sa); }
+
+// The ragged append of the new K/V rows and the schedule in one launch:
+// workgroup 0 builds the schedule (it is dispatched first and needs no
+// appended row), workgroups 1 .. append the rows (append_token_rows).
+__global__ __launch_bounds__(256) void fw_append_schedule_kernel(AppendArgs ap, SchedArgs sa) {
+  if (blockIdx.x == 0) schedule_body(sa);
+  else append_token_rows(ap, blockIdx.x - 1);
 }
 
 static int max_sched_tiles(const fw_prefill_params *p, int qt) {
@@ -2124,6 +2159,9 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
     FW_REQUIRE(p->page_size % 16 == 0, FW_ERR_VALUE,
                "page_size must be a multiple of 16; got %d", p->page_size);
   }
+  FW_REQUIRE(!p->k_new || (p->kv_mode == FW_KV_PAGED && p->v_new && p->seqused_k_excludes_q),
+             FW_ERR_VALUE,
+             "k_new / v_new append to a paged pool, together, with seqused_k_excludes_q set");
   if (p->seqlen_q <= 0) return FW_OK;
   const int max_tiles = max_sched_tiles(p, qt_rows);
   const bool varlen = p->kv_mode == FW_KV_VARLEN;
@@ -2133,18 +2171,31 @@ extern "C" int fw_prefill(const fw_prefill_params *p, fw_stream_t stream) {
   a.split_code = a.split_max ? (const int32_t *)(ws + wl.codes) : nullptr;
   a.split_cnt = a.split_max ? (int *)(ws + wl.cnt) : nullptr;
   a.split_part = a.split_max ? (float *)(ws + wl.part) : nullptr;
-  // a thread per sequence and per q tile (up to 1024): the rank sort's pass
-  int sched_threads = 64;
-  while (sched_threads < 1024 &&
-         (sched_threads < p->batch || sched_threads < std::min(max_tiles, kSortTiles)))
-    sched_threads <<= 1;
-  fw_prefill_schedule<<<1, sched_threads, 0, s>>>(p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
-                                         (int32_t *)p->workspace, max_tiles, qt_rows,
-                                         varlen ? p->cu_seqlens_k : nullptr,
-                                         varlen ? nullptr : p->seqused_k, a.seqused_plus_q,
-                                         a.wl, a.wr, (int32_t *)a.split_code, a.split_cnt,
-                                         a.split_max, head_groups, device_cus());
-  int st = check_launch("fw_prefill_schedule");
+  const SchedArgs sa{p->cu_seqlens_q, p->num_active, p->batch, p->seqlen_q,
+                     (int32_t *)p->workspace, max_tiles, qt_rows,
+                     varlen ? p->cu_seqlens_k : nullptr, varlen ? nullptr : p->seqused_k,
+                     a.seqused_plus_q, a.wl, a.wr, (int32_t *)a.split_code, a.split_cnt,
+                     a.split_max, head_groups, device_cus()};
+  int st;
+  if (p->k_new) {
+    // the new rows land after seqused_k of each active request (the rows
+    // fw_append_ragged writes for cu_seqlens_q), in the same launch as the
+    // schedule
+    const AppendArgs ap{(uint8_t *)p->k, (const uint8_t *)p->k_new, (const uint8_t *)p->v_new,
+                        p->cu_seqlens_q, p->seqused_k, p->block_table, p->num_active, p->batch,
+                        p->seqlen_q, p->nheads_k, d * dtype_bytes(p->kv_dtype), a.CH,
+                        p->page_size, p->num_pages, p->max_pages};
+    fw_append_schedule_kernel<<<1 + append_blocks(p->seqlen_q), 256, 0, s>>>(ap, sa);
+    st = check_launch("fw_append_schedule_kernel");
+  } else {
+    // a thread per sequence and per q tile (up to 1024): the rank sort's pass
+    int sched_threads = 64;
+    while (sched_threads < 1024 &&
+           (sched_threads < p->batch || sched_threads < std::min(max_tiles, kSortTiles)))
+      sched_threads <<= 1;
+    fw_prefill_schedule<<<1, sched_threads, 0, s>>>(sa);
+    st = check_launch("fw_prefill_schedule");
+  }
   if (st != FW_OK) return st;
   // one workgroup per (schedule slot, head group); see sched_slot
   dim3 grid((max_tiles + a.split_max) * head_groups);

@@ -69,6 +69,7 @@ class PrefillParams(ctypes.Structure):
         ("seqused_k_excludes_q", _i32),
         ("k_descale_ptr", _c_p), ("v_descale_ptr", _c_p),
         ("head_dim_v", _i32),
+        ("k_new", _c_p), ("v_new", _c_p),
     ]
 
 

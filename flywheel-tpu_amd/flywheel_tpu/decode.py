@@ -116,14 +116,16 @@ def paged_decode(q, kv_cache, k_new, v_new, cache_seqlens, block_table, num_acti
 def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active, sinks, *,
                   nheads_k, softmax_scale, softcap, causal, window_size, k_descale, v_descale,
                   max_seqlen_q, return_lse, token_major_q, q_rotary=None,
-                  seqused_excludes_q=False):
+                  seqused_excludes_q=False, k_new=None, v_new=None):
     """The paged varlen forward (kernels/fwd_paged.py:1351-1491).
 
     q is (total_q, nheads, D) when token_major_q, else head-major
     (nheads, total_q, D); out has q's layout; lse is (nheads, total_q).
     q_rotary: None or (tables, interleaved) for the fused Q RoPE.
     seqused_excludes_q: seqused_k holds the lengths before the q rows were
-    appended (the kernel adds each sequence's q length)."""
+    appended (the kernel adds each sequence's q length).  k_new / v_new
+    (total_q, nheads_k, D) in the pool's dtype: rows appended after seqused_k
+    first, in the launch that builds the schedule (needs seqused_excludes_q)."""
     if token_major_q:
         total_q, nheads, head_dim = q.shape
         qs_h, qs_t = head_dim, nheads * head_dim
@@ -150,6 +152,7 @@ def paged_prefill(q, kv_cache, cu_seqlens_q, seqused_k, block_table, num_active,
     p.causal, p.window_left, p.window_right = int(causal), left, right
     keep_d = set_descales(p, k_descale, v_descale)
     p.seqused_k_excludes_q = int(seqused_excludes_q)
+    p.k_new, p.v_new = N.ptr(k_new), N.ptr(v_new)
     keep = None if q_rotary is None else R.set_q_rotary(p, *q_rotary, q.device)
     lib = N.lib()
     nbytes = lib.fw_prefill_workspace_bytes(p)
@@ -364,17 +367,17 @@ def flash_attn_with_kvcache(
             cu = torch.arange(batch + 1, dtype=torch.int32, device=device) * seqlen_q
             packed_max = seqlen_q
         packed_q = q.reshape(-1, nheads, head_dim)
-        if has_new:
-            append_ragged(k_cache, k.reshape(-1, nheads_k, head_dim), v.reshape(-1, nheads_k, head_dim),
-                          cu, row_cache_seqlens, table, num_active_t, nheads_k)
         # with new tokens the kv length of a row is its cache length plus its
-        # q rows; the kernel adds them (no extra launch)
+        # q rows (the kernel adds them), and the rows are appended in the
+        # launch that builds the schedule (fw_append_ragged's rule)
         out, lse = paged_prefill(
             packed_q, k_cache, cu, row_cache_seqlens, table, num_active_t, sinks,
             nheads_k=nheads_k, softmax_scale=softmax_scale, softcap=float(softcap),
             causal=causal, window_size=window_size, k_descale=k_descale, v_descale=v_descale,
             max_seqlen_q=packed_max, return_lse=return_softmax_lse, token_major_q=True,
-            seqused_excludes_q=has_new)
+            seqused_excludes_q=has_new,
+            k_new=k.reshape(-1, nheads_k, head_dim) if has_new else None,
+            v_new=v.reshape(-1, nheads_k, head_dim) if has_new else None)
         out = out.reshape(q.shape)
         if return_softmax_lse:
             if not is_ragged:

@@ -232,6 +232,15 @@ typedef struct fw_prefill_params {
    * 256/128); a paged pool has one head dim of 64,
    * 128 or 256; the fused RoPE takes head_dim_v == head_dim. */
   int32_t head_dim_v;
+  /* Paged only, optional: new K and V rows (seqlen_q, nheads_k, head_dim) in
+   * the pool's dtype, appended before the attention in the same launch as the
+   * schedule: row i of request r (cu_seqlens_q[r] <= i < cu_seqlens_q[r + 1],
+   * r < num_active) lands at position seqused_k[r] + i - cu_seqlens_q[r]
+   * (fw_append_ragged's rule; requires seqused_k_excludes_q = 1).  Replaces
+   * the append half of flash_attn_with_kvcache's chunked-prefill route
+   * (decode.py:469-478, kernels/kv_append.py:116-184). */
+  const void *k_new;
+  const void *v_new;
 } fw_prefill_params;
 
 size_t fw_prefill_workspace_bytes(const fw_prefill_params *p);
