@@ -335,27 +335,28 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
     }
     auto edge = [&](int tb) { return tb < all_lo || tb + 32 > all_hi; };
 
-    auto compute_tile = [&](int tb, DecodeTile<KV, D> &tl, int lo, int hi, bool is_edge) {
+    // mid() runs between the two sub-tiles' QK products (the main loop issues
+    // the second sub-tile's loads there).
+    auto compute_tile = [&](int tb, DecodeTile<KV, D> &tl, int lo, int hi, bool is_edge,
+                            auto &&mid) {
       // The keys of an invalid page id read as zero K and V rows (the loads
       // used page 0, which may hold anything).
-      if (tl.bad[0] || tl.bad[1]) {
+      auto zero_sub = [&](int sub) {
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-          if (tl.bad[sub]) {
+        for (int j = 0; j < (KV == FW_BF16 ? D / 32 : D / 64); ++j)
+          tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
 #pragma unroll
-            for (int j = 0; j < (KV == FW_BF16 ? D / 32 : D / 64); ++j)
-              tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int vh = 0; vh < VH; ++vh)
-                tl.vraw[4 * sub + i][vh] = std::remove_reference_t<decltype(tl.vraw[0][0])>{};
-          }
-      }
+          for (int vh = 0; vh < VH; ++vh)
+            tl.vraw[4 * sub + i][vh] = std::remove_reference_t<decltype(tl.vraw[0][0])>{};
+      };
       // -------- S^T = K Q^T
       f32x4_t sacc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
+        if (sub == 1) mid();
+        if (tl.bad[sub]) zero_sub(sub);
         sacc[sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < D / 32; ++j)
@@ -461,9 +462,8 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       // Loads are branch-free.  A page id
       // outside [0, num_pages) is never dereferenced: the loads read page 0
       // and the compute stage replaces the sub-tile by zero K and V rows.
-      auto load_tile = [&](int tb, DecodeTile<KV, D> &tl) {
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
+      auto load_sub = [&](int tb, DecodeTile<KV, D> &tl, int sub) {
+        {
           const int sbc = min(tb + 16 * sub, last_key) & ~15;
           const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
           int page = __builtin_amdgcn_readlane(tbl_lane[0], pi & 63);
@@ -500,10 +500,19 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       // more of them outstanding stream ~6% slower here, in a plain read probe
       // as in this kernel.  Loading two fp8 tiles at a time (the bf16 kernel's
       // bytes in flight) was slower too (C5 1449 against 1434 us).
+      // bf16: the second sub-tile's loads go out after the first sub-tile's
+      // QK, so a wave has about one page (16 keys, 8 KiB) of loads in flight
+      // at a time (C3 678 -> 673.5 us); fp8 sub-tiles are half that size and
+      // both go out together (split, C5 ran 1,436 -> 1,459 us).
       for (int tb = cb; tb < ce; tb += 32) {
         DecodeTile<KV, D> t0;
-        load_tile(tb, t0);
-        compute_tile(tb, t0, key_lo, row_hi, edge(tb));
+        load_sub(tb, t0, 0);
+        if constexpr (KV == FW_BF16) {
+          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [&] { load_sub(tb, t0, 1); });
+        } else {
+          load_sub(tb, t0, 1);
+          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [] {});
+        }
       }
     }
     // The appended token's K/V, from k_new / v_new into every key slot (only
@@ -525,7 +534,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
           else
             tn.vraw[k8][vh] = 8 * n < D ? *(const u32x2_t *)(vp + 128 * EB * vh) : u32x2_t{0, 0};
         }
-      compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true);
+      compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true, [] {});
     }
 
     // ---- write the partial of segment (x, b): rows n < Rq of this q tile.
