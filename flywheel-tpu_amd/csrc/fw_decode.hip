@@ -338,7 +338,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
     // mid() runs between the two sub-tiles' QK products (the main loop issues
     // the second sub-tile's loads there).
     auto compute_tile = [&](int tb, DecodeTile<KV, D> &tl, int lo, int hi, bool is_edge,
-                            auto &&mid) {
+                            auto &&mid, auto &&after) {
       // The keys of an invalid page id read as zero K and V rows (the loads
       // used page 0, which may hold anything).
       auto zero_sub = [&](int sub) {
@@ -362,6 +362,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
         for (int j = 0; j < D / 32; ++j)
           sacc[sub] = mfma16(k_operand<KV, D>(tl.krow[sub], j), qop[j], sacc[sub]);
       }
+      after();
       // -------- online softmax on this lane's 8 (row n, key) scores
       if (a.softcap_log2 != 0.f) softcap_scores<2, 4>(sacc, a.softcap_log2);
       float sc[8];
@@ -462,7 +463,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       // Loads are branch-free.  A page id
       // outside [0, num_pages) is never dereferenced: the loads read page 0
       // and the compute stage replaces the sub-tile by zero K and V rows.
-      auto load_sub = [&](int tb, DecodeTile<KV, D> &tl, int sub) {
+      auto load_sub = [&](int tb, DecodeTile<KV, D> &tl, int sub, int what = 3) {
         {
           const int sbc = min(tb + 16 * sub, last_key) & ~15;
           const int pi = sbc / a.P - first_page;  // wave-uniform, < 64 * kTblPerLane
@@ -476,9 +477,10 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
           const uint8_t *prow = a.cache + ((size_t)page * a.P + (sbc % a.P)) * row_bytes;
           const uint8_t *vrow = prow + a.vdelta;
           const uint32_t lim = (uint32_t)(last_key - sbc);  // rows 0..lim hold cache keys
-          load_k_row<KV, D>(prow + (min((uint32_t)n, lim) * rb + kh_lane), g, tl.krow[sub]);
+          if (what & 1)
+            load_k_row<KV, D>(prow + (min((uint32_t)n, lim) * rb + kh_lane), g, tl.krow[sub]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < 4 && (what & 2); ++i) {
             const uint32_t vo = min((uint32_t)(4 * g + i), lim) * rb + vh_lane;
 #pragma unroll
             for (int vh = 0; vh < VH; ++vh) {
@@ -500,18 +502,21 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
       // more of them outstanding stream ~6% slower here, in a plain read probe
       // as in this kernel.  Loading two fp8 tiles at a time (the bf16 kernel's
       // bytes in flight) was slower too (C5 1449 against 1434 us).
-      // bf16: the second sub-tile's loads go out after the first sub-tile's
-      // QK, so a wave has about one page (16 keys, 8 KiB) of loads in flight
-      // at a time (C3 678 -> 673.5 us); fp8 sub-tiles are half that size and
-      // both go out together (split, C5 ran 1,436 -> 1,459 us).
+      // bf16: the first sub-tile's K and V (one page, 8 KiB a wave) go out
+      // first, the second sub-tile's K after the first QK and its V after the
+      // second, so a wave has at most about one page of loads in flight (C3
+      // 678 -> 664 us; the second page's K and V together after the first QK:
+      // 673 us).  fp8 sub-tiles are half that size and both go out together
+      // (split the same way, C5 ran 1,437 -> 1,641 us).
       for (int tb = cb; tb < ce; tb += 32) {
         DecodeTile<KV, D> t0;
         load_sub(tb, t0, 0);
         if constexpr (KV == FW_BF16) {
-          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [&] { load_sub(tb, t0, 1); });
+          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [&] { load_sub(tb, t0, 1, 1); },
+                       [&] { load_sub(tb, t0, 1, 2); });
         } else {
           load_sub(tb, t0, 1);
-          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [] {});
+          compute_tile(tb, t0, key_lo, row_hi, edge(tb), [] {}, [] {});
         }
       }
     }
@@ -534,7 +539,7 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
           else
             tn.vraw[k8][vh] = 8 * n < D ? *(const u32x2_t *)(vp + 128 * EB * vh) : u32x2_t{0, 0};
         }
-      compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true, [] {});
+      compute_tile(L0, tn, max(key_lo, L0), min(key_hi, L0 + 1), true, [] {}, [] {});
     }
 
     // ---- write the partial of segment (x, b): rows n < Rq of this q tile.
