@@ -341,10 +341,13 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
                             auto &&mid, auto &&after) {
       // The keys of an invalid page id read as zero K and V rows (the loads
       // used page 0, which may hold anything).
-      auto zero_sub = [&](int sub) {
+      // K is zeroed before its QK, V after after() (which may load it).
+      auto zero_k = [&](int sub) {
 #pragma unroll
         for (int j = 0; j < (KV == FW_BF16 ? D / 32 : D / 64); ++j)
           tl.krow[sub].w[j] = std::remove_reference_t<decltype(tl.krow[sub].w[j])>{};
+      };
+      auto zero_v = [&](int sub) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -356,13 +359,16 @@ __global__ __launch_bounds__(64 * kWgWaves<D>, (kDecodeOcc<KV, D>)) void fw_deco
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         if (sub == 1) mid();
-        if (tl.bad[sub]) zero_sub(sub);
+        if (tl.bad[sub]) zero_k(sub);
         sacc[sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < D / 32; ++j)
           sacc[sub] = mfma16(k_operand<KV, D>(tl.krow[sub], j), qop[j], sacc[sub]);
       }
       after();
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+        if (tl.bad[sub]) zero_v(sub);
       // -------- online softmax on this lane's 8 (row n, key) scores
       if (a.softcap_log2 != 0.f) softcap_scores<2, 4>(sacc, a.softcap_log2);
       float sc[8];
