@@ -890,6 +890,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     for (int st = 0; st < kPipe; ++st) rd(st, 0, bp * kTileB);
   };
   constexpr bool kCapInM = SOFTCAP;
+  constexpr int kSlotFull = 0, kSlotQK = 1;
   // Issue order of the slot's steps (0-15 PV, 16-31 QK).  With the softcap in
   // the MFMA slot: three PV steps (operands read before the slot), the 16 QK
   // steps, then the other 13 PV steps with the tanh of this tile's scores
@@ -898,7 +899,13 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     if constexpr (!kCapInM) return pos;
     return pos < 3 ? pos : pos < 19 ? pos + 13 : pos - 16;
   };
-  auto mslot = [&](const int bq, const int bp, const bf16x8_t (&pop)[4]) __attribute__((always_inline)) {
+  // kind: kSlotFull (PV of tile j-1, then QK of tile j) or kSlotQK (the first
+  // slot: QK only, no product with P = 0; C2 -1.2%, C4 -1%).  The last slot's
+  // QK (of a tile past the end, never used) stays: peeling that slot too made
+  // the compiler spill 300-500 registers.
+  auto mslot = [&](const int bq, const int bp, const bf16x8_t (&pop)[4], const auto kind)
+      __attribute__((always_inline)) {
+    constexpr int KIND = decltype(kind)::value;
     const uint32_t bufq = bq * kTileB, bufp = bp * kTileB;
     // the QK accumulates onto -anchor (with softcap onto 0: the anchor is
     // subtracted after the tanh)
@@ -925,6 +932,35 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       if (pos + kPipe < 32) rd(slot_step(pos + kPipe), bufq, bufp);
     };
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KIND == kSlotQK) {
+      // QK steps 16-31 in order, their first operands read here
+#pragma unroll
+      for (int st = 16; st < 16 + kPipe; ++st) rd(st, bufq, bufp);
+#pragma unroll
+      for (int pos = 16; pos < 32; ++pos) {
+        const int st = pos;
+        if (st < 18) {
+          if (st == 16) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sacc[1][e] = m_init;
+            sacc[0] = mfma32(opr[st], qr[0], sacc[1]);
+          } else {
+            sacc[1] = mfma32(opr[st], qr[0], sacc[1]);
+          }
+        } else {
+          const int j = (st - 16) >> 1, hh = (st - 16) & 1;
+          sacc[hh] = mfma32(opr[st], qr[j], sacc[hh]);
+        }
+        if (pos + kPipe < 32) rd(pos + kPipe, bufq, bufp);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (kCapInM) {
+        // the tanh of the scores after the MFMAs (no PV steps to spread it over)
+        const float m_qk = m_run == -INFINITY ? 0.f : m_run;
+        softcap_scores<2, 16, true>(sacc, a.softcap_log2, m_qk);
+      }
+      return;
+    }
     if constexpr (kCapInM) {
 #pragma unroll
       for (int pos = 0; pos < 19; ++pos) {
@@ -1084,9 +1120,9 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     }
     slot_barrier();  // tile 0 complete
     if (grp == 1) slot_barrier();
-    mslot_pre(3);  // the first PV multiplies P = 0 into zeroed buffer 3
-    // Unrolled by four so every buffer index is a compile-time constant.
-    auto body = [&](const int j, const auto bi) __attribute__((always_inline)) {
+    // Unrolled by four so every buffer index is a compile-time constant; the
+    // first body (QK only) is peeled.
+    auto body = [&](const int j, const auto bi, const auto kind) __attribute__((always_inline)) {
       // The address registers are opaque to the optimiser here, so the
       // per-buffer constants stay in the LDS instructions' offset fields
       // instead of being hoisted into one register per buffer and step.
@@ -1095,11 +1131,10 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(vofs[c][0]), "+v"(vofs[c][1]));
       constexpr int B = decltype(bi)::value;
-      // One code path for every slot (a branchy variant made the compiler
-      // copy all 64 O registers at each join): the PV of slot 0 multiplies
-      // P = 0 into a zeroed buffer, the QK of slot T reads a stale but finite
-      // tile and is never used, and tiles outside a wave's rows are fully
-      // masked by the softmax, so their P is 0.
+      // One code path for every slot of the loop (a branch inside it made the
+      // compiler copy all 64 O registers at each join): the QK of slot T reads
+      // a stale but finite tile and is never used, and tiles outside a wave's
+      // rows are fully masked by the softmax, so their P is 0.
       // MFMA slot at raised priority: the other wave of this SIMD is in its
       // softmax slot and would otherwise win issue whenever it is the older.
       // Four buffers: tile t+2 lands where tile t-2 was, free from slot 2t;
@@ -1109,7 +1144,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
       // M(t+1)), one slot before the first QK that reads it.  No MFMA slot
       // issues copies.
       __builtin_amdgcn_s_setprio(2);
-      mslot(B, (B + 3) % 4, pops);
+      mslot(B, (B + 3) % 4, pops, kind);
       // V of tile j for the first PV steps of the next MFMA slot, read while
       // this wave would otherwise wait at the barrier (the buffer has been
       // complete since before this slot and is not rewritten until tile j+4)
@@ -1148,14 +1183,17 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    for (int j = 0; j <= T; j += 4) {
-      body(j, I0());
+    using KF = std::integral_constant<int, kSlotFull>;
+    using KQ = std::integral_constant<int, kSlotQK>;
+    body(0, I0(), KQ());
+    for (int j = 1; j <= T; j += 4) {
+      body(j, I1(), KF());
       if (j + 1 > T) break;
-      body(j + 1, I1());
+      body(j + 1, I2(), KF());
       if (j + 2 > T) break;
-      body(j + 2, I2());
+      body(j + 2, I3(), KF());
       if (j + 3 > T) break;
-      body(j + 3, I3());
+      body(j + 3, I0(), KF());
     }
     if (grp == 0) slot_barrier();
   }
