@@ -719,7 +719,7 @@ def short_kernel_name(name):
     if name.startswith("void "):
         name = name[5:]
     if name.startswith("fw::"):
-        name = name[4:]
+        name = name[4:].replace("(anonymous namespace)::", "")
         depth, out = 0, []
         for ch in name:
             if ch == "(" and depth == 0:

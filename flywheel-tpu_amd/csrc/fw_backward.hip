@@ -6,15 +6,21 @@
 //                                    forward's rounded scaled q
 //   dp = dout v^T,  ds = p (dp - delta),  delta = rowsum(dout * out)
 //   dv += p^T dout,  dk += scale ds^T q,  dq += scale ds k
-// Here that work is split into three launches, all deterministic:
-//   fw_bwd_prep_kernel   lse_log2 and delta per query row (bwd.py:685-720)
-//   fw_bwd_dkv_kernel    one workgroup per 128 keys of one KV head (and one
-//                        chunk of its query heads); K and V live in registers,
-//                        q tiles stream through LDS; dk, dv in registers
-//   fw_bwd_dq_kernel     one workgroup per 128 query rows of one head; q and
-//                        dout live in registers, kv tiles stream through LDS
-//   fw_bwd_reduce_kernel sums the per-chunk dk / dv partials when a KV head's
-//                        query heads were split over workgroups
+// Here that work is split into launches, all deterministic (no atomics).
+// At head dims 128/128, while two bf16 (B, H, Sq, Sk) planes fit in 8 GiB of
+// workspace (the stored path):
+//   fw_bwd_prep_kernel        lse_log2 and delta per query row (bwd.py:685-720)
+//   fw_bwd_dq_kernel<., true> one workgroup per 128 query rows of one head; q
+//                             and dout live in registers, kv tiles stream
+//                             through LDS; it also writes P and dS
+//   fw_bwd_dkv_stored_kernel  dk = scale dS^T q and dv = P^T dout from the
+//                             stored planes: two products, no recomputation
+//   fw_bwd_reduce_kernel      sums the per-chunk dk / dv partials when a KV
+//                             head's query heads were split over workgroups
+// Otherwise (and at the wide head dims) fw_bwd_dkv_kernel recomputes the
+// scores: one workgroup per 128 keys of one KV head (and one chunk of its
+// query heads); K and V live in registers, q tiles stream through LDS, dk, dv
+// in registers; then fw_bwd_dq_kernel<., false>.
 // Every product is a 32x32x16 bf16 MFMA whose lane index is the row that owns
 // the accumulator (keys in the dk/dv kernel, query rows in the dq kernel), so
 // the softmax statistics of a lane are per-lane values and P / dS feed the
@@ -46,9 +52,32 @@ struct BwdArgs {
   int B, H, Hk, G, Sq, Sk, split;
   int dqw, dvw;  // head dims of q / k and of v / out (multiples of 128)
   float scale, qscale;
+  // P and dS stored by the dq kernel for the dk / dv products (stored path),
+  // or null: bf16 planes of B * H * sq_pad * sk_pad values in 4 KiB blocks,
+  // each the dq kernel's register image of a 32-row x 64-key tile, at
+  // stored_block(b * H + h, q / 32, key / 64)
+  uint16_t *ws_p, *ws_ds;
+  int sq_pad, sk_pad;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *(const u32x4_t *)p; }
+
+// A wave-uniform pointer in scalar registers (the copies take their base
+// there; a value computed through VALU division would sit in VGPRs).
+__device__ __forceinline__ const uint8_t *sgpr_ptr(const uint8_t *p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t *)(((uint64_t)hi << 32) | lo);
+}
+
+// Index of the stored 4 KiB block of (head row bh, 32-row query tile qt,
+// 64-key tile kt): the four key tiles of a 256-key block lie together, and a
+// 256-key block's query tiles follow each other, so the dk / dv workgroup of
+// that key block streams one contiguous run per head.
+__device__ __forceinline__ size_t stored_block(const BwdArgs &a, int bh, int qt, int kt) {
+  return (((size_t)bh * (a.sk_pad / 256) + (kt >> 2)) * (a.sq_pad / 32) + qt) * 4 + (kt & 3);
+}
 
 // ------------------------------------------------------------------ prep
 // 16 lanes per query row, 8 dims each: delta = sum(out * dout) in f32 and
@@ -107,6 +136,7 @@ __device__ __forceinline__ bf16x8_t tr_operand(const uint16_t *T, int r, int u, 
 // K0 .. K0 + 3 (K0 = 16u + 4g, then 16u + 8 + 4g; D0 = r - lane % 16).
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define FW_LDS __attribute__((address_space(3)))
+#define FW_GLOBAL __attribute__((address_space(1)))
 __device__ __forceinline__ bf16x8_t tr_operand_rm(uint32_t Rb, int c, int u, int lane) {
   const int g = lane >> 5, grp = lane >> 4, i = lane & 15;
   const uint32_t o = Rb + 2u * ((16 * u + 4 * g + (i >> 2)) * kBS + 32 * c + 16 * (grp & 1) + 4 * (i & 3));
@@ -393,7 +423,7 @@ __global__ __launch_bounds__(256) void fw_bwd_reduce_kernel(BwdArgs a) {
 // ------------------------------------------------------------------ dq
 // Workgroup = 4 waves = 128 query rows of head h (wave w: rows q0 + 32w + n);
 // kv tiles of 64 keys stream through LDS as K rows, V rows and K^T.
-template <bool CAUSAL>
+template <bool CAUSAL, bool STORE>
 __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kRowTileB + kTrTileB];
   uint16_t *Ks = (uint16_t *)smem;
@@ -443,6 +473,15 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 
   const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
   const size_t vbase = (size_t)b * a.vsb + (size_t)hk * a.vsh;
+  // the wave's first stored P and dS blocks (key tile 0), and this lane's
+  // byte offset in a block's 1 KiB chunks
+  const uint8_t *pst = nullptr, *dst_ = nullptr;
+  const uint32_t lane_st = 16u * (2 * n + g);
+  if constexpr (STORE) {
+    const size_t blk = stored_block(a, bh, (q0 >> 5) + __builtin_amdgcn_readfirstlane(w), 0) * 4096;
+    pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
+    dst_ = sgpr_ptr((const uint8_t *)a.ws_ds + blk);
+  }
   const int sr = tid & 15, sc = tid >> 4;  // rows vary fastest: conflict-free transposed stores
   u32x4_t kx[4], vx[4];
   auto gload = [&](int t) {
@@ -474,18 +513,38 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
       {
-        bf16x8_t ka[8], va[8];
         const uint16_t *kr = Ks + (32 * st + n) * kBS + 8 * g;
         const uint16_t *vr = Vs + (32 * st + n) * kBS + 8 * g;
+        if constexpr (STORE) {
+          // operands read three steps ahead of their MFMAs (the stores' words
+          // leave no room for all sixteen)
+          bf16x8_t ka[4], va[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
-          va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
-        }
+          for (int j = 0; j < 3; ++j) {
+            ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
+            va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
+          }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          sacc = mfma32(ka[j], qop[j], sacc);    // S^T[key][q]
-          dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
+          for (int j = 0; j < 8; ++j) {
+            if (j + 3 < 8) {
+              ka[(j + 3) % 4] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * (j + 3)));
+              va[(j + 3) % 4] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * (j + 3)));
+            }
+            sacc = mfma32(ka[j % 4], qop[j], sacc);    // S^T[key][q]
+            dpacc = mfma32(va[j % 4], dop[j], dpacc);  // dP^T[key][q]
+          }
+        } else {
+          bf16x8_t ka[8], va[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
+            va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            sacc = mfma32(ka[j], qop[j], sacc);    // S^T[key][q]
+            dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
+          }
         }
       }
       // the causal mask only on tiles that cross the diagonal (a real
@@ -500,18 +559,30 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
       }
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) {
-        u32x4_t dw;
+        u32x4_t dw, pw;
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-          float dsv[2];
+          float dsv[2], pv[2];
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int e = 8 * u2 + 2 * e2 + i;
-            dsv[i] = fast_exp2(sacc[e] - l2) * (dpacc[e] - dl);
+            pv[i] = fast_exp2(sacc[e] - l2);
+            dsv[i] = pv[i] * (dpacc[e] - dl);
           }
           dw[e2] = pack_bf16(dsv[0], dsv[1]);
+          if constexpr (STORE) pw[e2] = pack_bf16(pv[0], pv[1]);
         }
         dsop[2 * st + u2] = __builtin_bit_cast(bf16x8_t, dw);
+        if constexpr (STORE) {
+          // one 1 KiB chunk per (st, u2): whole 16-byte lane words, lane
+          // (n, g) in slot 2n + g (rows of one transposing read then fall on
+          // distinct banks)
+          const uint32_t o = ((uint32_t)(t >> 2) * (uint32_t)(a.sq_pad / 32) * 4u + (t & 3)) * 4096u +
+                             1024u * (2 * st + u2) + lane_st;
+          // written once, read once by the dk / dv kernel: non-temporal
+          __builtin_nontemporal_store(pw, (FW_GLOBAL u32x4_t *)(pst + o));
+          __builtin_nontemporal_store(dw, (FW_GLOBAL u32x4_t *)(dst_ + o));
+        }
       }
     }
     // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
@@ -535,6 +606,206 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 }
 
 
+// tr_operand_rm over a row-major tile of stride S: the A operand of dims col ..
+// col + 31, reduction rows 16u + 4g .. + 3 and 16u + 8 + 4g .. + 3.
+template <int S>
+__device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane) {
+  const int g = lane >> 5, grp = lane >> 4, i = lane & 15;
+  const uint32_t o = Rb + 2u * ((16 * u + 4 * g + (i >> 2)) * S + col + 16 * (grp & 1) + 4 * (i & 3));
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)o);
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(o + 16u * S));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// ------------------------------------------------------------------ dk, dv from stored P, dS
+// The stored path: fw_bwd_dq_kernel<CAUSAL, true> wrote P and dS (bf16, the
+// values its own dq product used), so dk and dv are two plain products over
+// the query rows, with no score recomputed:
+//   dV^T[d][key] += dout^T[d][q] P[q][key],  dK^T[d][key] += q^T[d][q] dS[q][key]
+// Workgroup = 8 waves = 256 keys of KV head hk (and one chunk of its query
+// heads); wave w < 4 accumulates dV of keys k0 + 64w .. + 63, wave w >= 4 dK
+// of keys k0 + 64(w - 4) .. + 63 (2 x 4 32x32 accumulators each).  The work
+// is a flat sequence of items (query head, 32-row query tile); each item's
+// P and dS blocks (32 rows x 256 keys) and dout and q rows (32 x 128) are
+// copied from global memory straight into one of three LDS buffers
+// (global_load_lds_dwordx4), two items ahead of the one computed, so that
+// about 96 KiB per CU are in flight.  Both MFMA operands come from
+// transposing LDS reads (the query row is the reduction index).  Entries of
+// P and dS that a tile's rows do not see (the dq kernel did not write them)
+// are zeroed in the operand registers, on tiles that need a mask only.
+constexpr int kSQ = 32;                    // query rows per item
+constexpr int kStKeys = 256;               // keys per workgroup
+constexpr int kStPB = kSQ * kStKeys * 2;   // 16 KiB: P (or dS) of an item
+constexpr int kStRB = kSQ * 128 * 2;       // 8 KiB: dout (or q) rows of an item
+constexpr int kStBuf = 2 * kStPB + 2 * kStRB;  // 48 KiB
+constexpr int kStRing = 3;
+
+// LDS byte offset of (row r, dims d .. d + 3) of a staged 32 x 128 row tile:
+// 256-byte rows whose 16-byte chunks are permuted by 2(r & 7), so that the
+// four rows one transposing read covers fall on distinct banks.
+__device__ __forceinline__ uint32_t st_row_off(int r, int d) {
+  return (uint32_t)(r * 256 + 16 * ((d >> 3) ^ (2 * (r & 7))) + 2 * (d & 7));
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStRing * kStBuf];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  // blockIdx.y = key block, so that the heaviest (causal: first) key blocks
+  // of every head are dispatched first
+  const int k0 = blockIdx.y * kStKeys;
+  int z = blockIdx.x;
+  const int sp = z % a.split;
+  z /= a.split;
+  const int hk = z % a.Hk;
+  const int b = z / a.Hk;
+  const int chunk = a.G / a.split;
+  const int off = a.Sk - a.Sq;
+  const bool is_k = w >= 4;
+  const int kq = 64 * (w & 3);  // wave's first key within the block
+
+  const int q_first = CAUSAL ? max(0, k0 - off) : 0;
+  const int t_begin = q_first / kSQ;
+  const int nt = max(0, (a.Sq + kSQ - 1) / kSQ - t_begin);
+  const int n_items = chunk * nt;
+
+  // ---- copies: per item, wave w moves P chunks w, w + 8 and dS chunks w,
+  // w + 8 (1 KiB each: 16 chunks per 256 keys), and dout / q rows 4w .. 4w + 3
+  const uint32_t wu = __builtin_amdgcn_readfirstlane(w);  // w, in a scalar register
+  const int rr = 4 * w + (lane >> 4);     // this lane's dout / q row within the item
+  const int rc = (lane & 15) ^ (2 * (rr & 7));  // the global chunk its LDS slot holds
+  auto issue = [&](int it) __attribute__((always_inline)) {
+    const int hi = it / nt, t = t_begin + it % nt;
+    const int h = hk * a.G + sp * chunk + hi;
+    const uint32_t buf = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(it % kStRing) * kStBuf);
+    const uint8_t *pb = sgpr_ptr((const uint8_t *)(a.ws_p + stored_block(a, b * a.H + h, t, k0 / 64) * 2048));
+    const uint8_t *sb = sgpr_ptr(pb + ((const uint8_t *)a.ws_ds - (const uint8_t *)a.ws_p));
+    const uint32_t pv = 1024u * w + 16u * lane;
+    lds_dma16_nt(pb, pv, buf + 1024u * wu);
+    lds_dma16_nt(pb, pv + 8192u, buf + 1024u * (wu + 8));
+    lds_dma16_nt(sb, pv, buf + kStPB + 1024u * wu);
+    lds_dma16_nt(sb, pv + 8192u, buf + kStPB + 1024u * (wu + 8));
+    const int q = min(t * kSQ + rr, a.Sq - 1);
+    const uint8_t *ob = sgpr_ptr((const uint8_t *)(a.dout + (size_t)b * a.osb + (size_t)h * a.osh));
+    const uint8_t *qb = sgpr_ptr((const uint8_t *)(a.q + (size_t)b * a.qsb + (size_t)h * a.qsh));
+    lds_dma16(ob, (uint32_t)(2 * (size_t)q * a.ost) + 16u * rc, buf + 2 * kStPB + 1024u * wu);
+    lds_dma16(qb, (uint32_t)(2 * (size_t)q * a.qst) + 16u * rc, buf + 2 * kStPB + kStRB + 1024u * wu);
+  };
+  constexpr int kCopies = 6;  // copies per wave per item
+
+  // ---- operand addresses (bytes within a buffer)
+  // B (col = key, k = query row) from the P / dS blocks: lane 4a + b of each
+  // 16-lane group reads row K0 + a, keys D0 + 4b .. + 3, which the dq kernel
+  // stored in slot 2(K0 + a) + (b & 1), bytes 8(b >> 1), of chunk
+  // (key tile, st, u2) = (.., kb, grp & 1); K0 = 16u + 4g (+ 8 for the hi half)
+  const int grp = lane >> 4, ia = (lane & 15) >> 2, ib = lane & 3;
+  const uint32_t b_base = (uint32_t)(is_k ? kStPB : 0) + 4096u * (kq >> 6) + 1024u * (grp & 1) +
+                          16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
+  // A (row = dim, k = query row) from the dout / q rows: row K0 + a, dims
+  // 32c + 16(grp & 1) + 4b .. + 3
+  const uint32_t a_base = 2 * kStPB + (is_k ? kStRB : 0);
+  auto b_off = [&](int kb, int u) { return b_base + 2048u * kb + 512u * u; };  // +16 rows = 32 slots
+  auto a_off = [&](int c, int u) { return a_base + st_row_off(16 * u + 4 * g + ia, 32 * c + 16 * (grp & 1) + 4 * ib); };
+  auto tr_pair = [&](uint32_t addr, uint32_t hi_delta) {
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)addr);
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(addr + hi_delta));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[kb][c][e] = 0.f;
+
+  for (int it = 0; it < min(kStRing - 1, n_items); ++it) issue(it);
+  for (int it = 0; it < n_items; ++it) {
+    // this wave's copies of item it are done (the next item's may be
+    // outstanding); the barrier publishes every wave's, and frees the buffer
+    // of item it - 1 for item it + 2
+    if (it + 1 < n_items) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    static_assert(kCopies == 6 && kStRing == 3, "the wait counts above assume 6 copies, 3 buffers");
+    __syncthreads();
+    if (it + kStRing - 1 < n_items) issue(it + kStRing - 1);
+    const int t = t_begin + it % nt;
+    const uint32_t buf = lds0 + (uint32_t)(it % kStRing) * kStBuf;
+    const int qb = t * kSQ;
+    const bool full = qb + kSQ <= a.Sq && k0 + kStKeys <= a.Sk && (!CAUSAL || qb + off >= k0 + kStKeys - 1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bf16x8_t bop[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) bop[kb] = tr_pair(buf + b_off(kb, u), 256u);
+      if (!full) {
+        asm volatile("" ::: "memory");
+        // element e: query row qb + 16u + 4g + (e & 3) (+ 8 for e >= 4), key
+        // k0 + kq + 32kb + n
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int key = k0 + kq + 32 * kb + n;
+          u32x4_t x = __builtin_bit_cast(u32x4_t, bop[kb]);
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int q = qb + 16 * u + 4 * g + ((e + h2) & 3) + ((e + h2) >= 4 ? 8 : 0);
+              const int vis = q >= a.Sq ? 0 : CAUSAL ? min(a.Sk, q + off + 1) : a.Sk;
+              m |= (key < vis ? 0xffffu : 0u) << (16 * h2);
+            }
+            x[e >> 1] &= m;
+          }
+          bop[kb] = __builtin_bit_cast(bf16x8_t, x);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bf16x8_t aop = tr_pair(buf + a_off(c, u), 2048u);  // + 8 rows
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) acc[kb][c] = mfma32(aop, bop[kb], acc[kb][c]);
+      }
+    }
+  }
+
+  // ---------------------------------------------------------------- store
+  // acc[kb][c] value e: dim 32c + 8(e >> 2) + 4g + (e & 3), key k0 + kq + 32kb + n
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int key = k0 + kq + 32 * kb + n;
+    if (key >= a.Sk) continue;
+    if (a.split == 1) {
+      uint16_t *dst = is_k ? a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst
+                           : a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst;
+      const float f = is_k ? a.scale : 1.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int rr2 = 0; rr2 < 4; ++rr2) {
+          const f32x16_t &X = acc[kb][c];
+          *(u32x2_t *)(dst + 32 * c + 8 * rr2 + 4 * g) =
+              u32x2_t{pack_bf16(X[4 * rr2] * f, X[4 * rr2 + 1] * f),
+                      pack_bf16(X[4 * rr2 + 2] * f, X[4 * rr2 + 3] * f)};
+        }
+    } else {
+      float *part = is_k ? a.dk_part : a.dv_part;
+      const size_t row = ((((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key) * 128;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int rr2 = 0; rr2 < 4; ++rr2) {
+          const f32x16_t &X = acc[kb][c];
+          *(f32x4_t *)(part + row + 32 * c + 8 * rr2 + 4 * g) =
+              f32x4_t{X[4 * rr2], X[4 * rr2 + 1], X[4 * rr2 + 2], X[4 * rr2 + 3]};
+        }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ wide head dims
 // The same recurrences at head dims DQ (q, k) and DV (v, out) of 128, 256 or
 // 512 (smaller head dims reach them zero-padded).  Each launch of a kernel
@@ -553,17 +824,6 @@ __device__ __forceinline__ void store_rows(uint16_t *R, const u32x4_t (&x)[4], i
   for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int r = 0; r < 2; ++r) *(u32x4_t *)(R + (2 * (sr + 16 * p) + r) * S + col + 8 * sc) = x[2 * p + r];
-}
-
-// tr_operand_rm over a row-major tile of stride S: the A operand of dims col ..
-// col + 31, reduction rows 16u + 4g .. + 3 and 16u + 8 + 4g .. + 3.
-template <int S>
-__device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane) {
-  const int g = lane >> 5, grp = lane >> 4, i = lane & 15;
-  const uint32_t o = Rb + 2u * ((16 * u + 4 * g + (i >> 2)) * S + col + 16 * (grp & 1) + 4 * (i & 3));
-  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)o);
-  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(o + 16u * S));
-  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 template <int DQ, int DV>
@@ -923,11 +1183,13 @@ int dkv_chunks(const fw_attn_bwd_params *p) {
   return std::max(p->head_dim, head_dim_v_of(p)) / 128;
 }
 
-int pick_split(const fw_attn_bwd_params *p) {
+// Query-head chunks per KV head for the dk / dv launch: the smallest divisor
+// of G giving at least `target` workgroups (or G).
+int pick_split(const fw_attn_bwd_params *p, long target) {
   const int G = p->nheads / p->nheads_k;
   const long base = (long)p->batch * p->nheads_k * ceil_div(p->seqlen_k, 128) * dkv_chunks(p);
   int split = 1;
-  while (split < G && base * split < 512) {
+  while (split < G && base * split < target) {
     int nxt = split + 1;
     while (G % nxt) ++nxt;
     split = nxt;
@@ -936,6 +1198,30 @@ int pick_split(const fw_attn_bwd_params *p) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The stored path (128/128 head dims): the dq kernel writes P and dS once and
+// the dk / dv kernel reads them instead of recomputing the scores.  It needs
+// two bf16 (B, H, Sq rounded up to 128, Sk rounded up to 128) planes of
+// workspace; above kStoredMaxBytes the recomputing kernels run instead.
+// FW_BWD_STORED=0 selects the recomputing kernels at any size.
+constexpr size_t kStoredMaxBytes = (size_t)8 << 30;
+
+// Rows rounded up to the dq workgroup's 128, keys to the dk / dv one's 256.
+size_t stored_plane_bytes(const fw_attn_bwd_params *p) {
+  return align256((size_t)p->batch * p->nheads * (size_t)ceil_div(p->seqlen_q, 128) * 128 *
+                  (size_t)ceil_div(p->seqlen_k, 256) * 256 * 2);
+}
+
+bool use_stored(const fw_attn_bwd_params *p) {
+  if (p->head_dim != 128 || head_dim_v_of(p) != 128) return false;
+  const char *e = getenv("FW_BWD_STORED");
+  if (e && e[0] == '0') return false;
+  return 2 * stored_plane_bytes(p) <= kStoredMaxBytes;
+}
+
+// The stored dk / dv kernel runs two workgroups per CU and wants about four
+// per CU so that the causal imbalance evens out; the recomputing one runs one.
+int bwd_split(const fw_attn_bwd_params *p) { return pick_split(p, use_stored(p) ? 1024 : 512); }
 
 }  // namespace
 }  // namespace fw
@@ -946,9 +1232,10 @@ extern "C" size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p) {
   if (p->nheads_k <= 0 || p->nheads % p->nheads_k) return 0;
   const size_t rows = (size_t)p->batch * p->nheads * p->seqlen_q;
   size_t bytes = 2 * align256(rows * 4);
-  const int split = pick_split(p);
+  const int split = bwd_split(p);
   const size_t keys = (size_t)split * p->batch * p->nheads_k * p->seqlen_k * 4;
   if (split > 1) bytes += align256(keys * p->head_dim) + align256(keys * head_dim_v_of(p));
+  if (use_stored(p)) bytes += 2 * stored_plane_bytes(p);
   return bytes;
 }
 
@@ -986,6 +1273,9 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   const size_t need = fw_attn_bwd_workspace_bytes(p);
   FW_REQUIRE(p->workspace && p->workspace_bytes >= need, FW_ERR_VALUE,
              "workspace of %zu bytes is smaller than the %zu needed", p->workspace_bytes, need);
+  // the stored path's copies address dout / q rows by 32-bit byte offsets
+  FW_REQUIRE(!use_stored(p) || 2 * (long)p->seqlen_q * std::max(std::max(p->q_stride_t, p->o_stride_t), (int64_t)128) < (1l << 32),
+             FW_ERR_VALUE, "q / dout rows span more than 4 GiB");
   FW_REQUIRE((long)p->batch * p->nheads * p->seqlen_q * 16 < (1l << 32) &&
                  (long)p->batch * p->nheads_k * p->seqlen_k * 16 < (1l << 32),
              FW_ERR_VALUE, "too many rows for one launch");
@@ -1003,12 +1293,25 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   uint8_t *ws = (uint8_t *)p->workspace;
   a.lse2 = (float *)ws;
   a.delta = (float *)(ws + align256(rows * 4));
-  a.split = pick_split(p);
+  a.split = bwd_split(p);
   a.dk_part = a.dv_part = nullptr;
   if (a.split > 1) {
     const size_t keys = (size_t)a.split * p->batch * p->nheads_k * p->seqlen_k * 4;
     a.dk_part = (float *)(ws + 2 * align256(rows * 4));
     a.dv_part = (float *)(ws + 2 * align256(rows * 4) + align256(keys * p->head_dim));
+  }
+  const bool stored = use_stored(p);
+  a.ws_p = a.ws_ds = nullptr;
+  a.sq_pad = ceil_div(p->seqlen_q, 128) * 128;
+  a.sk_pad = ceil_div(p->seqlen_k, 256) * 256;
+  if (stored) {
+    size_t o = 2 * align256(rows * 4);
+    if (a.split > 1) {
+      const size_t keys = (size_t)a.split * p->batch * p->nheads_k * p->seqlen_k * 4;
+      o += align256(keys * p->head_dim) + align256(keys * dvw);
+    }
+    a.ws_p = (uint16_t *)(ws + o);
+    a.ws_ds = (uint16_t *)(ws + o + stored_plane_bytes(p));
   }
   a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qst = p->q_stride_t;
   const bool o_given = p->o_stride_b || p->o_stride_h || p->o_stride_t;
@@ -1038,6 +1341,21 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   const bool wide = dkv_chunks(p) > 1 || dvw != p->head_dim;
   const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split, dkv_chunks(p));
   const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);
+  if (stored) {
+    // dq first (it writes P and dS), then dk / dv from them
+    if (p->causal) fw_bwd_dq_kernel<true, true><<<gq, 256, 0, s>>>(a);
+    else fw_bwd_dq_kernel<false, true><<<gq, 256, 0, s>>>(a);
+    st = check_launch("fw_bwd_dq_kernel");
+    if (st != FW_OK) return st;
+    const dim3 gst(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kStKeys));
+    if (p->causal) fw_bwd_dkv_stored_kernel<true><<<gst, 512, 0, s>>>(a);
+    else fw_bwd_dkv_stored_kernel<false><<<gst, 512, 0, s>>>(a);
+    st = check_launch("fw_bwd_dkv_stored_kernel");
+    if (st != FW_OK || a.split == 1) return st;
+    const long thr = (long)p->batch * p->nheads_k * p->seqlen_k * 16;
+    fw_bwd_reduce_kernel<<<(unsigned)((thr + 255) / 256), 256, 0, s>>>(a);
+    return check_launch("fw_bwd_reduce_kernel");
+  }
   if (wide) {
     if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, true, s);
     else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, true, s);
@@ -1058,9 +1376,9 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, false, s);
     else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, false, s);
   } else if (p->causal) {
-    fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<true, false><<<gq, 256, 0, s>>>(a);
   } else {
-    fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<false, false><<<gq, 256, 0, s>>>(a);
   }
   return check_launch("fw_bwd_dq_kernel");
 }

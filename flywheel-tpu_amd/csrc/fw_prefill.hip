@@ -572,26 +572,6 @@ __device__ __attribute__((aligned(256))) uint8_t kZeroKV[1024];
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
 
-// 64 lanes x 16 bytes from base + voff[lane] into LDS at lds_addr + 16 * lane
-// (global_load_lds_dwordx4).  Issued from asm so the compiler does not add a
-// wait for it before every later LDS read: the kernel waits for its own
-// copies (s_waitcnt vmcnt) before the barrier that publishes the buffer.
-__device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
-}
-// Two copies into LDS at lds_addr and lds_addr + 1024 under one M0 value: the
-// second instruction's immediate offset (1024) moves both its LDS and its
-// global address, so its base is passed 1024 lower (the sum is the address
-// voff2 names; nothing is read below base).
-__device__ __forceinline__ void lds_dma16x2(const uint8_t *base, uint32_t voff1, uint32_t voff2,
-                                            uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
-               "global_load_lds_dwordx4 %2, %4 offset:1024"
-               :: "s"(lds_addr), "v"(voff1), "v"(voff2), "s"(base), "s"(base - 1024)
-               : "memory", "m0");
-}
-
 template <int MODE, bool SOFTCAP, int KV = FW_BF16>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile j+2 into

@@ -260,8 +260,13 @@ int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
  * with the o strides (the q strides when those are 0); k and dk use the k
  * strides, v and dv the v strides; lse (b, h, t) at b*lse_stride_b +
  * h*lse_stride_h + t.  Deterministic: no atomics.  The workspace (its size
- * from fw_attn_bwd_workspace_bytes) holds f32 row statistics and, when the
- * query heads of one KV head are split over workgroups, f32 dk / dv partials.
+ * from fw_attn_bwd_workspace_bytes) holds f32 row statistics, f32 dk / dv
+ * partials when the query heads of one KV head are split over workgroups,
+ * and, at head dims 128/128, the bf16 P and dS planes (2 * 2 * batch *
+ * nheads * seqlen_q * seqlen_k bytes, rounded up) through which dk and dv are
+ * computed without recomputing the scores, as long as they fit in 8 GiB
+ * (beyond that, or with the environment variable FW_BWD_STORED=0, the scores
+ * are recomputed and the workspace holds no planes).
  */
 typedef struct fw_attn_bwd_params {
   const void *q, *k, *v, *out, *dout;

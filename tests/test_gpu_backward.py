@@ -66,6 +66,20 @@ def test_flash_attn_func_backward(b, h, hk, sq, sk, causal):
     check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
 
 
+@pytest.mark.parametrize("b,h,hk,sq,sk,causal", [(2, 4, 2, 200, 333, True), (1, 4, 1, 333, 200, True),
+                                                (1, 8, 2, 300, 300, False), (1, 16, 2, 520, 520, True)])
+def test_backward_recompute_path(b, h, hk, sq, sk, causal, monkeypatch):
+    """The recomputing dk / dv kernel (the path above the stored planes'
+    size limit), selected with FW_BWD_STORED=0."""
+    monkeypatch.setenv("FW_BWD_STORED", "0")
+    what = f"bwd recompute b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+    announce(what)
+    rng = np.random.default_rng(61)
+    q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
+    do = randn(rng, (b, sq, h, 128))
+    check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
+
+
 def test_backward_token_major_and_repeat():
     announce("bwd token-major, bitwise repeat")
     rng = np.random.default_rng(61)
