@@ -10,7 +10,7 @@
 // At head dims 128/128, while two bf16 (B, H, Sq, Sk) planes fit in 8 GiB of
 // workspace (the stored path):
 //   fw_bwd_prep_kernel        lse_log2 and delta per query row (bwd.py:685-720)
-//   fw_bwd_dq_kernel<., true> one workgroup per 128 query rows of one head; q
+//   fw_bwd_dq_store_kernel    one workgroup per 128 query rows of one head; q
 //                             and dout live in registers, kv tiles stream
 //                             through LDS; it also writes P and dS
 //   fw_bwd_dkv_stored_kernel  dk = scale dS^T q and dv = P^T dout from the
@@ -20,7 +20,8 @@
 // Otherwise (and at the wide head dims) fw_bwd_dkv_kernel recomputes the
 // scores: one workgroup per 128 keys of one KV head (and one chunk of its
 // query heads); K and V live in registers, q tiles stream through LDS, dk, dv
-// in registers; then fw_bwd_dq_kernel<., false>.
+// in registers; then fw_bwd_dq_kernel (the same dq recurrence without the
+// stores).
 // Every product is a 32x32x16 bf16 MFMA whose lane index is the row that owns
 // the accumulator (keys in the dk/dv kernel, query rows in the dq kernel), so
 // the softmax statistics of a lane are per-lane values and P / dS feed the
@@ -423,7 +424,7 @@ __global__ __launch_bounds__(256) void fw_bwd_reduce_kernel(BwdArgs a) {
 // ------------------------------------------------------------------ dq
 // Workgroup = 4 waves = 128 query rows of head h (wave w: rows q0 + 32w + n);
 // kv tiles of 64 keys stream through LDS as K rows, V rows and K^T.
-template <bool CAUSAL, bool STORE>
+template <bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kRowTileB + kTrTileB];
   uint16_t *Ks = (uint16_t *)smem;
@@ -473,15 +474,6 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 
   const size_t kbase = (size_t)b * a.ksb + (size_t)hk * a.ksh;
   const size_t vbase = (size_t)b * a.vsb + (size_t)hk * a.vsh;
-  // the wave's first stored P and dS blocks (key tile 0), and this lane's
-  // byte offset in a block's 1 KiB chunks
-  const uint8_t *pst = nullptr, *dst_ = nullptr;
-  const uint32_t lane_st = 16u * (2 * n + g);
-  if constexpr (STORE) {
-    const size_t blk = stored_block(a, bh, (q0 >> 5) + __builtin_amdgcn_readfirstlane(w), 0) * 4096;
-    pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
-    dst_ = sgpr_ptr((const uint8_t *)a.ws_ds + blk);
-  }
   const int sr = tid & 15, sc = tid >> 4;  // rows vary fastest: conflict-free transposed stores
   u32x4_t kx[4], vx[4];
   auto gload = [&](int t) {
@@ -513,38 +505,18 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
       {
+        bf16x8_t ka[8], va[8];
         const uint16_t *kr = Ks + (32 * st + n) * kBS + 8 * g;
         const uint16_t *vr = Vs + (32 * st + n) * kBS + 8 * g;
-        if constexpr (STORE) {
-          // operands read three steps ahead of their MFMAs (the stores' words
-          // leave no room for all sixteen)
-          bf16x8_t ka[4], va[4];
 #pragma unroll
-          for (int j = 0; j < 3; ++j) {
-            ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
-            va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
-          }
+        for (int j = 0; j < 8; ++j) {
+          ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
+          va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
+        }
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            if (j + 3 < 8) {
-              ka[(j + 3) % 4] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * (j + 3)));
-              va[(j + 3) % 4] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * (j + 3)));
-            }
-            sacc = mfma32(ka[j % 4], qop[j], sacc);    // S^T[key][q]
-            dpacc = mfma32(va[j % 4], dop[j], dpacc);  // dP^T[key][q]
-          }
-        } else {
-          bf16x8_t ka[8], va[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            ka[j] = __builtin_bit_cast(bf16x8_t, ld16(kr + 16 * j));
-            va[j] = __builtin_bit_cast(bf16x8_t, ld16(vr + 16 * j));
-          }
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            sacc = mfma32(ka[j], qop[j], sacc);    // S^T[key][q]
-            dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
-          }
+        for (int j = 0; j < 8; ++j) {
+          sacc = mfma32(ka[j], qop[j], sacc);    // S^T[key][q]
+          dpacc = mfma32(va[j], dop[j], dpacc);  // dP^T[key][q]
         }
       }
       // the causal mask only on tiles that cross the diagonal (a real
@@ -559,30 +531,18 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
       }
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) {
-        u32x4_t dw, pw;
+        u32x4_t dw;
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-          float dsv[2], pv[2];
+          float dsv[2];
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int e = 8 * u2 + 2 * e2 + i;
-            pv[i] = fast_exp2(sacc[e] - l2);
-            dsv[i] = pv[i] * (dpacc[e] - dl);
+            dsv[i] = fast_exp2(sacc[e] - l2) * (dpacc[e] - dl);
           }
           dw[e2] = pack_bf16(dsv[0], dsv[1]);
-          if constexpr (STORE) pw[e2] = pack_bf16(pv[0], pv[1]);
         }
         dsop[2 * st + u2] = __builtin_bit_cast(bf16x8_t, dw);
-        if constexpr (STORE) {
-          // one 1 KiB chunk per (st, u2): whole 16-byte lane words, lane
-          // (n, g) in slot 2n + g (rows of one transposing read then fall on
-          // distinct banks)
-          const uint32_t o = ((uint32_t)(t >> 2) * (uint32_t)(a.sq_pad / 32) * 4u + (t & 3)) * 4096u +
-                             1024u * (2 * st + u2) + lane_st;
-          // written once, read once by the dk / dv kernel: non-temporal
-          __builtin_nontemporal_store(pw, (FW_GLOBAL u32x4_t *)(pst + o));
-          __builtin_nontemporal_store(dw, (FW_GLOBAL u32x4_t *)(dst_ + o));
-        }
       }
     }
     // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
@@ -606,6 +566,208 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 }
 
 
+// ------------------------------------------------------------------ dq (stored path)
+// fw_bwd_dq_kernel's recurrence for the stored path, with its data movement
+// reshaped around the P and dS stores.  vmcnt counts loads and stores
+// together and the compiler waits for all of them when both are pending, so
+// a tile's wait for its K / V rows would also wait for the previous tile's
+// stores.  Here the K and V rows of tile t + 1 are copied straight into LDS
+// (global_load_lds_dwordx4, double-buffered) at the start of tile t, and
+// tile t - 1's P and dS words (kept in registers) are stored right beside
+// them: both have the whole tile's compute before the wait at the top of
+// tile t + 1.  K^T comes from the K rows by transposing reads, so no
+// transposed copy is staged.
+// LDS rows are 256 bytes (one key) whose 16-byte chunks are permuted by
+// kv_swz(row): the 16 rows of a plain 16-byte read and the 4 rows of a
+// transposing read each fall on distinct banks.
+__device__ __forceinline__ int kv_swz(int r) { return 2 * (r & 7) + ((r >> 3) & 1); }
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
+  constexpr int kTile = 64 * 256;  // bytes of 64 key rows
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];  // [K | V] x 2
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  const int n_qt = (a.Sq + 127) / 128;
+  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
+  const int q0 = qt * 128;
+  const int off = a.Sk - a.Sq;
+  const int qrow = q0 + 32 * w + n;
+  const bool row_ok = qrow < a.Sq;
+
+  bf16x8_t qop[8], dop[8];
+  float l2 = INFINITY, dl = 0.f;
+  {
+    const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)(row_ok ? qrow : 0) * a.qst;
+    const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(row_ok ? qrow : 0) * a.ost;
+    const float qs = row_ok ? a.qscale : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
+      const u32x4_t d = ld16(a.dout + obase + 16 * j + 8 * g);
+      dop[j] = __builtin_bit_cast(bf16x8_t, row_ok ? d : u32x4_t{0, 0, 0, 0});
+    }
+    if (row_ok) {
+      const size_t s = ((size_t)b * a.H + h) * a.Sq + qrow;
+      l2 = a.lse2[s];
+      dl = a.delta[s];
+    }
+  }
+  f32x16_t dqacc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqacc[c][e] = 0.f;
+
+  // visible keys of a row: [0, hi)
+  auto row_hi = [&](int r) { return CAUSAL ? min(a.Sk, r + off + 1) : a.Sk; };
+  const int last_row = min(q0 + 127, a.Sq - 1);
+  const int wg_hi = row_hi(last_row);
+  const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
+  const int r_hi = row_hi(qrow);
+
+  // ---- copies: wave w moves key rows 16w .. 16w + 15 of K and of V (4 rows
+  // of 256 bytes per instruction; lane: row 4i + lane / 16, LDS slot lane % 16
+  // holding global chunk slot ^ kv_swz(row))
+  const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
+  const uint8_t *kg = sgpr_ptr((const uint8_t *)(a.k + (size_t)b * a.ksb + (size_t)hk * a.ksh));
+  const uint8_t *vg = sgpr_ptr((const uint8_t *)(a.v + (size_t)b * a.vsb + (size_t)hk * a.vsh));
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    const uint32_t buf = lds0 + (uint32_t)(t & 1) * (2 * kTile);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * w + 4 * i + (lane >> 4);
+      const int key = min(t * kBT + r, a.Sk - 1);
+      const uint32_t ch = 16u * (uint32_t)((lane & 15) ^ kv_swz(r));
+      const uint32_t dst = buf + 256u * (16 * wu + 4 * i);
+      lds_dma16(kg, (uint32_t)(2 * (size_t)key * a.kst) + ch, dst);
+      lds_dma16(vg, (uint32_t)(2 * (size_t)key * a.vst) + ch, dst + kTile);
+    }
+  };
+  // byte offset of (row r, 16-byte chunk c) in a K or V tile
+  auto kv_at = [](int r, int c) { return (uint32_t)(256 * r + 16 * (c ^ kv_swz(r))); };
+
+  // ---- stored P / dS: the wave's first blocks (key tile 0) and this lane's
+  // byte offset in a block's 1 KiB chunks
+  const size_t blk = stored_block(a, bh, (q0 >> 5) + __builtin_amdgcn_readfirstlane(w), 0) * 4096;
+  const uint8_t *pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
+  const uint8_t *dst_ = sgpr_ptr((const uint8_t *)a.ws_ds + blk);
+  const uint32_t lane_st = 16u * (2 * n + g);
+  u32x4_t pw_prev[4], dw_prev[4];  // the previous tile's words, chunk 2st + u2
+  auto store_prev = [&](int t) __attribute__((always_inline)) {
+    const uint32_t o = ((uint32_t)(t >> 2) * (uint32_t)(a.sq_pad / 32) * 4u + (t & 3)) * 4096u + lane_st;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // written once, read once by the dk / dv kernel: non-temporal
+      __builtin_nontemporal_store(pw_prev[j], (FW_GLOBAL u32x4_t *)(pst + o + 1024u * j));
+      __builtin_nontemporal_store(dw_prev[j], (FW_GLOBAL u32x4_t *)(dst_ + o + 1024u * j));
+    }
+  };
+
+  if (t_end > 0) issue(0);
+  for (int t = 0; t < t_end; ++t) {
+    // tile t's rows are in (every wave's copies, and the previous tile's
+    // stores, are complete); the barrier publishes them and frees the other
+    // buffer (tile t - 1) for tile t + 1
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 < t_end) issue(t + 1);
+    if (t > 0) store_prev(t - 1);
+    const uint32_t kb_l = lds0 + (uint32_t)(t & 1) * (2 * kTile), vb_l = kb_l + kTile;
+    const int kb = t * kBT;
+    // keys no row of the wave sees are masked to p = 0 (one code path)
+    const bool full = kb + kBT <= row_hi(q0 + 32 * w);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x16_t sacc, dpacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = dpacc[e] = 0.f;
+      {
+        // K and V rows 32st + n, dims 16j + 8g: chunk 2j + g
+        const int r = 32 * st + n;
+        bf16x8_t ka[4], va[4];
+        auto ld = [&](uint32_t base, int j) {
+          return __builtin_bit_cast(bf16x8_t, *(const FW_LDS u32x4_t *)(uintptr_t)(base + kv_at(r, 2 * j + g)));
+        };
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          ka[j] = ld(kb_l, j);
+          va[j] = ld(vb_l, j);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j + 3 < 8) {
+            ka[(j + 3) % 4] = ld(kb_l, j + 3);
+            va[(j + 3) % 4] = ld(vb_l, j + 3);
+          }
+          sacc = mfma32(ka[j % 4], qop[j], sacc);    // S^T[key][q]
+          dpacc = mfma32(va[j % 4], dop[j], dpacc);  // dP^T[key][q]
+        }
+      }
+      if (!full) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kk = kb + 32 * st + 8 * (e >> 2) + 4 * g + (e & 3);
+          sacc[e] = kk < r_hi ? sacc[e] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        u32x4_t dw, pw;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          float dsv[2], pv[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int e = 8 * u2 + 2 * e2 + i;
+            pv[i] = fast_exp2(sacc[e] - l2);
+            dsv[i] = pv[i] * (dpacc[e] - dl);
+          }
+          dw[e2] = pack_bf16(dsv[0], dsv[1]);
+          pw[e2] = pack_bf16(pv[0], pv[1]);
+        }
+        pw_prev[2 * st + u2] = pw;
+        dw_prev[2 * st + u2] = dw;
+      }
+    }
+    // dQ^T[d][q] += K^T[d][key] dS^T[key][q]; the K^T operand of dims
+    // 32c + lane % 32, keys 16u + 4g + 0..3 and + 8 .. + 11, read transposed
+    // from the K rows (lane 4a + b of each 16-lane group: key row K0 + a,
+    // dims D0 + 4b .. + 3)
+    const int grp = lane >> 4, ia = (lane & 15) >> 2, ib = lane & 3;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int r = 16 * u + 4 * g + ia;
+        const int d = 32 * c + 16 * (grp & 1) + 4 * ib;
+        const uint32_t ad = kb_l + kv_at(r, d >> 3) + 2u * (d & 7);
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)ad);
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (FW_LDS v4i16_t *)(kb_l + kv_at(r + 8, d >> 3) + 2u * (d & 7)));
+        const bf16x8_t kt = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        dqacc[c] = mfma32(kt, __builtin_bit_cast(bf16x8_t, dw_prev[u]), dqacc[c]);
+      }
+  }
+  if (t_end > 0) store_prev(t_end - 1);
+
+  if (!row_ok) return;
+  uint16_t *dp = a.dq + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qrow * a.qst;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const f32x16_t &Q = dqacc[c];
+      *(u32x2_t *)(dp + 32 * c + 8 * rr + 4 * g) =
+          u32x2_t{pack_bf16(Q[4 * rr] * a.scale, Q[4 * rr + 1] * a.scale),
+                  pack_bf16(Q[4 * rr + 2] * a.scale, Q[4 * rr + 3] * a.scale)};
+    }
+}
+
 // tr_operand_rm over a row-major tile of stride S: the A operand of dims col ..
 // col + 31, reduction rows 16u + 4g .. + 3 and 16u + 8 + 4g .. + 3.
 template <int S>
@@ -618,7 +780,7 @@ __device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane)
 }
 
 // ------------------------------------------------------------------ dk, dv from stored P, dS
-// The stored path: fw_bwd_dq_kernel<CAUSAL, true> wrote P and dS (bf16, the
+// The stored path: fw_bwd_dq_store_kernel wrote P and dS (bf16, the
 // values its own dq product used), so dk and dv are two plain products over
 // the query rows, with no score recomputed:
 //   dV^T[d][key] += dout^T[d][q] P[q][key],  dK^T[d][key] += q^T[d][q] dS[q][key]
@@ -1274,8 +1436,10 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   FW_REQUIRE(p->workspace && p->workspace_bytes >= need, FW_ERR_VALUE,
              "workspace of %zu bytes is smaller than the %zu needed", p->workspace_bytes, need);
   // the stored path's copies address dout / q rows by 32-bit byte offsets
-  FW_REQUIRE(!use_stored(p) || 2 * (long)p->seqlen_q * std::max(std::max(p->q_stride_t, p->o_stride_t), (int64_t)128) < (1l << 32),
-             FW_ERR_VALUE, "q / dout rows span more than 4 GiB");
+  FW_REQUIRE(!use_stored(p) ||
+                 (2 * (long)p->seqlen_q * std::max(std::max(p->q_stride_t, p->o_stride_t), (int64_t)128) < (1l << 32) &&
+                  2 * (long)p->seqlen_k * std::max(std::max(p->k_stride_t, p->v_stride_t), (int64_t)128) < (1l << 32)),
+             FW_ERR_VALUE, "q / dout or k / v rows of one head span more than 4 GiB");
   FW_REQUIRE((long)p->batch * p->nheads * p->seqlen_q * 16 < (1l << 32) &&
                  (long)p->batch * p->nheads_k * p->seqlen_k * 16 < (1l << 32),
              FW_ERR_VALUE, "too many rows for one launch");
@@ -1343,8 +1507,8 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);
   if (stored) {
     // dq first (it writes P and dS), then dk / dv from them
-    if (p->causal) fw_bwd_dq_kernel<true, true><<<gq, 256, 0, s>>>(a);
-    else fw_bwd_dq_kernel<false, true><<<gq, 256, 0, s>>>(a);
+    if (p->causal) fw_bwd_dq_store_kernel<true><<<gq, 256, 0, s>>>(a);
+    else fw_bwd_dq_store_kernel<false><<<gq, 256, 0, s>>>(a);
     st = check_launch("fw_bwd_dq_kernel");
     if (st != FW_OK) return st;
     const dim3 gst(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kStKeys));
@@ -1376,9 +1540,9 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, false, s);
     else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, false, s);
   } else if (p->causal) {
-    fw_bwd_dq_kernel<true, false><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
   } else {
-    fw_bwd_dq_kernel<false, false><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
   }
   return check_launch("fw_bwd_dq_kernel");
 }
