@@ -7,17 +7,20 @@
 //   dp = dout v^T,  ds = p (dp - delta),  delta = rowsum(dout * out)
 //   dv += p^T dout,  dk += scale ds^T q,  dq += scale ds k
 // Here that work is split into launches, all deterministic (no atomics).
-// At head dims 128/128, while two bf16 (B, H, Sq, Sk) planes fit in 8 GiB of
+// At head dims 128/128, while a bf16 (B, H, Sq, Sk) plane fits in 8 GiB of
 // workspace (the stored path):
-//   fw_bwd_prep_kernel        lse_log2 and delta per query row (bwd.py:685-720)
 //   fw_bwd_dq_store_kernel    one workgroup per 128 query rows of one head; q
 //                             and dout live in registers, kv tiles stream
-//                             through LDS; it also writes P and dS
-//   fw_bwd_dkv_stored_kernel  dk = scale dS^T q and dv = P^T dout from the
-//                             stored planes: two products, no recomputation
+//                             through LDS; it also forms the row statistics
+//                             (delta, lse_log2; bwd.py:685-720) and writes P
+//                             and delta
+//   fw_bwd_dkv_stored_kernel  dv = P^T dout from the stored P, dk = scale
+//                             dS^T q with dS = P (dout v^T - delta): three
+//                             products, no score recomputed
 //   fw_bwd_reduce_kernel      sums the per-chunk dk / dv partials when a KV
 //                             head's query heads were split over workgroups
-// Otherwise (and at the wide head dims) fw_bwd_dkv_kernel recomputes the
+// Otherwise (and at the wide head dims) fw_bwd_prep_kernel forms lse_log2 and
+// delta per query row, and fw_bwd_dkv_kernel recomputes the
 // scores: one workgroup per 128 keys of one KV head (and one chunk of its
 // query heads); K and V live in registers, q tiles stream through LDS, dk, dv
 // in registers; then fw_bwd_dq_kernel (the same dq recurrence without the
@@ -53,11 +56,11 @@ struct BwdArgs {
   int B, H, Hk, G, Sq, Sk, split;
   int dqw, dvw;  // head dims of q / k and of v / out (multiples of 128)
   float scale, qscale;
-  // P and dS stored by the dq kernel for the dk / dv products (stored path),
-  // or null: bf16 planes of B * H * sq_pad * sk_pad values in 4 KiB blocks,
-  // each the dq kernel's register image of a 32-row x 64-key tile, at
+  // P stored by the dq kernel for the dk / dv kernel (stored path), or null:
+  // a bf16 plane of B * H * sq_pad * sk_pad values in 4 KiB blocks, each the
+  // dq kernel's register image of a 32-row x 64-key tile, at
   // stored_block(b * H + h, q / 32, key / 64)
-  uint16_t *ws_p, *ws_ds;
+  uint16_t *ws_p;
   int sq_pad, sk_pad;
 };
 
@@ -568,12 +571,12 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 
 // ------------------------------------------------------------------ dq (stored path)
 // fw_bwd_dq_kernel's recurrence for the stored path, with its data movement
-// reshaped around the P and dS stores.  vmcnt counts loads and stores
+// reshaped around the P stores.  vmcnt counts loads and stores
 // together and the compiler waits for all of them when both are pending, so
 // a tile's wait for its K / V rows would also wait for the previous tile's
 // stores.  Here the K and V rows of tile t + 1 are copied straight into LDS
 // (global_load_lds_dwordx4, double-buffered) at the start of tile t, and
-// tile t - 1's P and dS words (kept in registers) are stored right beside
+// tile t - 1's P words (kept in registers) are stored right beside
 // them: both have the whole tile's compute before the wait at the top of
 // tile t + 1.  K^T comes from the K rows by transposing reads, so no
 // transposed copy is staged.
@@ -598,6 +601,10 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   const int qrow = q0 + 32 * w + n;
   const bool row_ok = qrow < a.Sq;
 
+  // The row's statistics are formed here (the recomputing path's prep
+  // kernel does this): delta = rowsum(dout * out) from the dout operand and
+  // the out row, lse_log2 = lse * log2 e (+inf for a row with no key); delta
+  // goes to the workspace for the dk / dv kernel.
   bf16x8_t qop[8], dop[8];
   float l2 = INFINITY, dl = 0.f;
   {
@@ -608,12 +615,21 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
     for (int j = 0; j < 8; ++j) {
       qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
       const u32x4_t d = ld16(a.dout + obase + 16 * j + 8 * g);
+      const u32x4_t o = ld16(a.o + obase + 16 * j + 8 * g);
       dop[j] = __builtin_bit_cast(bf16x8_t, row_ok ? d : u32x4_t{0, 0, 0, 0});
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dl += bf16_lo(o[e]) * bf16_lo(d[e]);
+        dl += bf16_hi(o[e]) * bf16_hi(d[e]);
+      }
     }
+    dl += __shfl_xor(dl, 32, 64);  // the row's other 64 dims
     if (row_ok) {
-      const size_t s = ((size_t)b * a.H + h) * a.Sq + qrow;
-      l2 = a.lse2[s];
-      dl = a.delta[s];
+      const float l = a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qrow];
+      l2 = l == -INFINITY ? INFINITY : l * kLog2e;
+      if (g == 0) a.delta[((size_t)b * a.H + h) * a.Sq + qrow] = dl;
+    } else {
+      dl = 0.f;
     }
   }
   f32x16_t dqacc[4];
@@ -650,21 +666,18 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   // byte offset of (row r, 16-byte chunk c) in a K or V tile
   auto kv_at = [](int r, int c) { return (uint32_t)(256 * r + 16 * (c ^ kv_swz(r))); };
 
-  // ---- stored P / dS: the wave's first blocks (key tile 0) and this lane's
-  // byte offset in a block's 1 KiB chunks
+  // ---- stored P: the wave's first block (key tile 0) and this lane's byte
+  // offset in a block's 1 KiB chunks
   const size_t blk = stored_block(a, bh, (q0 >> 5) + __builtin_amdgcn_readfirstlane(w), 0) * 4096;
   const uint8_t *pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
-  const uint8_t *dst_ = sgpr_ptr((const uint8_t *)a.ws_ds + blk);
   const uint32_t lane_st = 16u * (2 * n + g);
-  u32x4_t pw_prev[4], dw_prev[4];  // the previous tile's words, chunk 2st + u2
+  u32x4_t pw_prev[4];   // the previous tile's P words, chunk 2st + u2
+  bf16x8_t dsop[4];     // this tile's dS, the B operand of dQ
   auto store_prev = [&](int t) __attribute__((always_inline)) {
     const uint32_t o = ((uint32_t)(t >> 2) * (uint32_t)(a.sq_pad / 32) * 4u + (t & 3)) * 4096u + lane_st;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // written once, read once by the dk / dv kernel: non-temporal
+    for (int j = 0; j < 4; ++j)  // written once, read once by the dk / dv kernel: non-temporal
       __builtin_nontemporal_store(pw_prev[j], (FW_GLOBAL u32x4_t *)(pst + o + 1024u * j));
-      __builtin_nontemporal_store(dw_prev[j], (FW_GLOBAL u32x4_t *)(dst_ + o + 1024u * j));
-    }
   };
 
   if (t_end > 0) issue(0);
@@ -731,7 +744,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
           pw[e2] = pack_bf16(pv[0], pv[1]);
         }
         pw_prev[2 * st + u2] = pw;
-        dw_prev[2 * st + u2] = dw;
+        dsop[2 * st + u2] = __builtin_bit_cast(bf16x8_t, dw);
       }
     }
     // dQ^T[d][q] += K^T[d][key] dS^T[key][q]; the K^T operand of dims
@@ -750,7 +763,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
         const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (FW_LDS v4i16_t *)(kb_l + kv_at(r + 8, d >> 3) + 2u * (d & 7)));
         const bf16x8_t kt = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        dqacc[c] = mfma32(kt, __builtin_bit_cast(bf16x8_t, dw_prev[u]), dqacc[c]);
+        dqacc[c] = mfma32(kt, dsop[u], dqacc[c]);
       }
   }
   if (t_end > 0) store_prev(t_end - 1);
@@ -779,34 +792,38 @@ __device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane)
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// ------------------------------------------------------------------ dk, dv from stored P, dS
-// The stored path: fw_bwd_dq_store_kernel wrote P and dS (bf16, the
-// values its own dq product used), so dk and dv are two plain products over
-// the query rows, with no score recomputed:
-//   dV^T[d][key] += dout^T[d][q] P[q][key],  dK^T[d][key] += q^T[d][q] dS[q][key]
+// ------------------------------------------------------------------ dk, dv from stored P
+// The stored path: fw_bwd_dq_store_kernel wrote P (bf16, the values its own
+// dq product used), so dv is a plain product over the query rows and dk needs
+// only dP recomputed, no score:
+//   dV^T[d][key] += dout^T[d][q] P[q][key]
+//   dP[q][key] = dout[q] . V[key],  dS = P (dP - delta)
+//   dK^T[d][key] += q^T[d][q] dS[q][key]
 // Workgroup = 8 waves = 256 keys of KV head hk (and one chunk of its query
-// heads); wave w < 4 accumulates dV of keys k0 + 64w .. + 63, wave w >= 4 dK
-// of keys k0 + 64(w - 4) .. + 63 (2 x 4 32x32 accumulators each).  The work
-// is a flat sequence of items (query head, 32-row query tile); each item's
-// P and dS blocks (32 rows x 256 keys) and dout and q rows (32 x 128) are
-// copied from global memory straight into one of three LDS buffers
-// (global_load_lds_dwordx4), two items ahead of the one computed, so that
-// about 96 KiB per CU are in flight.  Both MFMA operands come from
-// transposing LDS reads (the query row is the reduction index).  Entries of
-// P and dS that a tile's rows do not see (the dq kernel did not write them)
-// are zeroed in the operand registers, on tiles that need a mask only.
+// heads); wave w accumulates dV and dK of keys k0 + 32w .. + 31 (4 + 4 32x32
+// accumulators) and keeps those keys' V rows as the B operand of dP.  The
+// work is a flat sequence of items (query head, 32-row query tile); each
+// item's P blocks (32 rows x 256 keys), dout and q rows (32 x 128) and delta
+// (32 floats) are copied from global memory straight into one of three LDS
+// buffers (global_load_lds_dwordx4 / _dword), two items ahead of the one
+// computed.  The dV and dK products take both operands from transposing LDS
+// reads (the query row is the reduction index); dP's accumulator lane is the
+// key, so its values line up with the P operand's and dS is formed in
+// registers.  Entries of P that a tile's rows do not see (the dq kernel did
+// not write them) are zeroed by a select, on tiles that need a mask only.
 constexpr int kSQ = 32;                    // query rows per item
 constexpr int kStKeys = 256;               // keys per workgroup
-constexpr int kStPB = kSQ * kStKeys * 2;   // 16 KiB: P (or dS) of an item
+constexpr int kStPB = kSQ * kStKeys * 2;   // 16 KiB: P of an item
 constexpr int kStRB = kSQ * 128 * 2;       // 8 KiB: dout (or q) rows of an item
-constexpr int kStBuf = 2 * kStPB + 2 * kStRB;  // 48 KiB
+constexpr int kStBuf = kStPB + 2 * kStRB + 256;  // + delta
 constexpr int kStRing = 3;
 
-// LDS byte offset of (row r, dims d .. d + 3) of a staged 32 x 128 row tile:
-// 256-byte rows whose 16-byte chunks are permuted by 2(r & 7), so that the
-// four rows one transposing read covers fall on distinct banks.
+// LDS byte offset of (row r, dims d .. ) of a staged 32 x 128 row tile:
+// 256-byte rows whose 16-byte chunks are permuted by kv_swz(r), so that the
+// 16 rows of a plain 16-byte read and the 4 rows of a transposing read each
+// fall on distinct banks.
 __device__ __forceinline__ uint32_t st_row_off(int r, int d) {
-  return (uint32_t)(r * 256 + 16 * ((d >> 3) ^ (2 * (r & 7))) + 2 * (d & 7));
+  return (uint32_t)(r * 256 + 16 * ((d >> 3) ^ kv_swz(r)) + 2 * (d & 7));
 }
 
 template <bool CAUSAL>
@@ -825,146 +842,170 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
   const int b = z / a.Hk;
   const int chunk = a.G / a.split;
   const int off = a.Sk - a.Sq;
-  const bool is_k = w >= 4;
-  const int kq = 64 * (w & 3);  // wave's first key within the block
+  const int kq = 32 * w;  // wave's first key within the block
+  const int key = k0 + kq + n;  // this lane's key (accumulator column)
 
   const int q_first = CAUSAL ? max(0, k0 - off) : 0;
   const int t_begin = q_first / kSQ;
   const int nt = max(0, (a.Sq + kSQ - 1) / kSQ - t_begin);
   const int n_items = chunk * nt;
 
-  // ---- copies: per item, wave w moves P chunks w, w + 8 and dS chunks w,
-  // w + 8 (1 KiB each: 16 chunks per 256 keys), and dout / q rows 4w .. 4w + 3
+  // ---- copies: per item, wave w moves P chunks w and w + 8 (1 KiB each: 16
+  // chunks per 256 keys), dout and q rows 4w .. 4w + 3 and (every wave, the
+  // same bytes) the 32 delta values
   const uint32_t wu = __builtin_amdgcn_readfirstlane(w);  // w, in a scalar register
   const int rr = 4 * w + (lane >> 4);     // this lane's dout / q row within the item
-  const int rc = (lane & 15) ^ (2 * (rr & 7));  // the global chunk its LDS slot holds
+  const int rc = (lane & 15) ^ kv_swz(rr);  // the global chunk its LDS slot holds
   auto issue = [&](int it) __attribute__((always_inline)) {
     const int hi = it / nt, t = t_begin + it % nt;
     const int h = hk * a.G + sp * chunk + hi;
     const uint32_t buf = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(it % kStRing) * kStBuf);
     const uint8_t *pb = sgpr_ptr((const uint8_t *)(a.ws_p + stored_block(a, b * a.H + h, t, k0 / 64) * 2048));
-    const uint8_t *sb = sgpr_ptr(pb + ((const uint8_t *)a.ws_ds - (const uint8_t *)a.ws_p));
     const uint32_t pv = 1024u * w + 16u * lane;
     lds_dma16_nt(pb, pv, buf + 1024u * wu);
     lds_dma16_nt(pb, pv + 8192u, buf + 1024u * (wu + 8));
-    lds_dma16_nt(sb, pv, buf + kStPB + 1024u * wu);
-    lds_dma16_nt(sb, pv + 8192u, buf + kStPB + 1024u * (wu + 8));
     const int q = min(t * kSQ + rr, a.Sq - 1);
     const uint8_t *ob = sgpr_ptr((const uint8_t *)(a.dout + (size_t)b * a.osb + (size_t)h * a.osh));
     const uint8_t *qb = sgpr_ptr((const uint8_t *)(a.q + (size_t)b * a.qsb + (size_t)h * a.qsh));
-    lds_dma16(ob, (uint32_t)(2 * (size_t)q * a.ost) + 16u * rc, buf + 2 * kStPB + 1024u * wu);
-    lds_dma16(qb, (uint32_t)(2 * (size_t)q * a.qst) + 16u * rc, buf + 2 * kStPB + kStRB + 1024u * wu);
+    lds_dma16(ob, (uint32_t)(2 * (size_t)q * a.ost) + 16u * rc, buf + kStPB + 1024u * wu);
+    lds_dma16(qb, (uint32_t)(2 * (size_t)q * a.qst) + 16u * rc, buf + kStPB + kStRB + 1024u * wu);
+    const uint8_t *db = sgpr_ptr((const uint8_t *)(a.delta + ((size_t)b * a.H + h) * a.Sq));
+    if (lane < 32) lds_dma4(db, 4u * (uint32_t)min(t * kSQ + lane, a.Sq - 1), buf + kStPB + 2 * kStRB);
   };
-  constexpr int kCopies = 6;  // copies per wave per item
+  constexpr int kCopies = 5;  // copies per wave per item
 
   // ---- operand addresses (bytes within a buffer)
-  // B (col = key, k = query row) from the P / dS blocks: lane 4a + b of each
-  // 16-lane group reads row K0 + a, keys D0 + 4b .. + 3, which the dq kernel
-  // stored in slot 2(K0 + a) + (b & 1), bytes 8(b >> 1), of chunk
-  // (key tile, st, u2) = (.., kb, grp & 1); K0 = 16u + 4g (+ 8 for the hi half)
+  // P (B operand: col = key, k = query row): lane 4a + b of each 16-lane
+  // group reads row K0 + a, keys D0 + 4b .. + 3, which the dq kernel stored
+  // in slot 2(K0 + a) + (b & 1), bytes 8(b >> 1), of chunk (key tile, st, u2)
+  // = (w / 2, w % 2, grp & 1); K0 = 16u + 4g (+ 8 for the hi half)
   const int grp = lane >> 4, ia = (lane & 15) >> 2, ib = lane & 3;
-  const uint32_t b_base = (uint32_t)(is_k ? kStPB : 0) + 4096u * (kq >> 6) + 1024u * (grp & 1) +
-                          16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
-  // A (row = dim, k = query row) from the dout / q rows: row K0 + a, dims
-  // 32c + 16(grp & 1) + 4b .. + 3
-  const uint32_t a_base = 2 * kStPB + (is_k ? kStRB : 0);
-  auto b_off = [&](int kb, int u) { return b_base + 2048u * kb + 512u * u; };  // +16 rows = 32 slots
-  auto a_off = [&](int c, int u) { return a_base + st_row_off(16 * u + 4 * g + ia, 32 * c + 16 * (grp & 1) + 4 * ib); };
-  auto tr_pair = [&](uint32_t addr, uint32_t hi_delta) {
-    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)addr);
-    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)(addr + hi_delta));
+  const uint32_t p_base = 2048u * w + 1024u * (grp & 1) + 16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
+  // A operands (row = dim, k = query row) from the dout (dV) and q (dK) rows:
+  // row K0 + a, dims 32c + 16(grp & 1) + 4b .. + 3
+  const uint32_t do_base = kStPB, q_base = kStPB + kStRB, dl_base = kStPB + 2 * kStRB;
+  // (row K0 + a and K0 + 8 + a differ in their chunk permutation)
+  auto a_off = [&](int c, int u, int h8) {
+    return st_row_off(16 * u + 8 * h8 + 4 * g + ia, 32 * c + 16 * (grp & 1) + 4 * ib);
+  };
+  auto tr_pair = [&](uint32_t lo_addr, uint32_t hi_addr) {
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)lo_addr);
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)hi_addr);
     return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
-  f32x16_t acc[2][4];
+  // the V row of this lane's key (dims 16j + 8g .. + 7): dP's B operand
+  bf16x8_t vop[8];
+  {
+    const uint16_t *vp = a.v + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)min(key, a.Sk - 1) * a.vst;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+    for (int j = 0; j < 8; ++j) vop[j] = __builtin_bit_cast(bf16x8_t, ld16(vp + 16 * j + 8 * g));
+  }
+
+  f32x16_t dv_acc[4], dk_acc[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[kb][c][e] = 0.f;
+    for (int e = 0; e < 16; ++e) dv_acc[c][e] = dk_acc[c][e] = 0.f;
 
   for (int it = 0; it < min(kStRing - 1, n_items); ++it) issue(it);
   for (int it = 0; it < n_items; ++it) {
     // this wave's copies of item it are done (the next item's may be
     // outstanding); the barrier publishes every wave's, and frees the buffer
     // of item it - 1 for item it + 2
-    if (it + 1 < n_items) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    if (it + 1 < n_items) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    static_assert(kCopies == 6 && kStRing == 3, "the wait counts above assume 6 copies, 3 buffers");
+    static_assert(kCopies == 5 && kStRing == 3, "the wait counts above assume 5 copies, 3 buffers");
     __syncthreads();
     if (it + kStRing - 1 < n_items) issue(it + kStRing - 1);
     const int t = t_begin + it % nt;
     const uint32_t buf = lds0 + (uint32_t)(it % kStRing) * kStBuf;
     const int qb = t * kSQ;
     const bool full = qb + kSQ <= a.Sq && k0 + kStKeys <= a.Sk && (!CAUSAL || qb + off >= k0 + kStKeys - 1);
+    // P of k-step u: element e at query row qb + 16u + 4g + (e & 3) (+ 8 for e >= 4)
+    u32x4_t pw[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      bf16x8_t bop[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) bop[kb] = tr_pair(buf + b_off(kb, u), 256u);
+      const uint32_t pa = buf + p_base + 512u * u;
+      pw[u] = __builtin_bit_cast(u32x4_t, tr_pair(pa, pa + 256u));  // + 8 rows = 16 slots
       if (!full) {
         asm volatile("" ::: "memory");
-        // element e: query row qb + 16u + 4g + (e & 3) (+ 8 for e >= 4), key
-        // k0 + kq + 32kb + n
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const int key = k0 + kq + 32 * kb + n;
-          u32x4_t x = __builtin_bit_cast(u32x4_t, bop[kb]);
+        for (int e = 0; e < 8; e += 2) {
+          uint32_t m = 0;
 #pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            uint32_t m = 0;
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-              const int q = qb + 16 * u + 4 * g + ((e + h2) & 3) + ((e + h2) >= 4 ? 8 : 0);
-              const int vis = q >= a.Sq ? 0 : CAUSAL ? min(a.Sk, q + off + 1) : a.Sk;
-              m |= (key < vis ? 0xffffu : 0u) << (16 * h2);
-            }
-            x[e >> 1] &= m;
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int q = qb + 16 * u + 4 * g + ((e + h2) & 3) + ((e + h2) >= 4 ? 8 : 0);
+            const int vis = q >= a.Sq ? 0 : CAUSAL ? min(a.Sk, q + off + 1) : a.Sk;
+            m |= (key < vis ? 0xffffu : 0u) << (16 * h2);
           }
-          bop[kb] = __builtin_bit_cast(bf16x8_t, x);
+          pw[u][e >> 1] &= m;
         }
       }
+    }
+    // dP[q][key] for the item's 32 rows (value e at query row 8(e >> 2) + 4g
+    // + (e & 3)): a chain of 8 MFMAs on one accumulator, with the 8 dV
+    // products (which need only P) between its links
+    f32x16_t dp;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bf16x8_t aop = tr_pair(buf + a_off(c, u), 2048u);  // + 8 rows
+    for (int e = 0; e < 16; ++e) dp[e] = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) acc[kb][c] = mfma32(aop, bop[kb], acc[kb][c]);
+    for (int j = 0; j < 8; ++j) {
+      const bf16x8_t da = __builtin_bit_cast(
+          bf16x8_t, *(const FW_LDS u32x4_t *)(uintptr_t)(buf + do_base + st_row_off(n, 16 * j + 8 * g)));
+      dp = mfma32(da, vop[j], dp);
+      const int c = j & 3, u = j >> 2;
+      dv_acc[c] = mfma32(tr_pair(buf + do_base + a_off(c, u, 0), buf + do_base + a_off(c, u, 1)),
+                         __builtin_bit_cast(bf16x8_t, pw[u]), dv_acc[c]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      // dS = P (dP - delta); element e of k-step u is value 8u + e of dp
+      const f32x4_t d0 = *(const FW_LDS f32x4_t *)(uintptr_t)(buf + dl_base + 4u * (16 * u + 4 * g));
+      const f32x4_t d1 = *(const FW_LDS f32x4_t *)(uintptr_t)(buf + dl_base + 4u * (16 * u + 8 + 4 * g));
+      u32x4_t sw;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const float dl0 = e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4];
+        const float dl1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
+        sw[e2] = pack_bf16(bf16_lo(pw[u][e2]) * (dp[8 * u + 2 * e2] - dl0),
+                           bf16_hi(pw[u][e2]) * (dp[8 * u + 2 * e2 + 1] - dl1));
       }
+      const bf16x8_t sop = __builtin_bit_cast(bf16x8_t, sw);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        dk_acc[c] = mfma32(tr_pair(buf + q_base + a_off(c, u, 0), buf + q_base + a_off(c, u, 1)), sop, dk_acc[c]);
     }
   }
 
   // ---------------------------------------------------------------- store
-  // acc[kb][c] value e: dim 32c + 8(e >> 2) + 4g + (e & 3), key k0 + kq + 32kb + n
+  // acc[c] value e: dim 32c + 8(e >> 2) + 4g + (e & 3), key `key`
+  if (key >= a.Sk) return;
+  if (a.split == 1) {
+    uint16_t *kp = a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst;
+    uint16_t *vp = a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int key = k0 + kq + 32 * kb + n;
-    if (key >= a.Sk) continue;
-    if (a.split == 1) {
-      uint16_t *dst = is_k ? a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst
-                           : a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst;
-      const float f = is_k ? a.scale : 1.f;
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x16_t &K = dk_acc[c], &V = dv_acc[c];
+        const int d = 32 * c + 8 * r4 + 4 * g;
+        *(u32x2_t *)(kp + d) = u32x2_t{pack_bf16(K[4 * r4] * a.scale, K[4 * r4 + 1] * a.scale),
+                                       pack_bf16(K[4 * r4 + 2] * a.scale, K[4 * r4 + 3] * a.scale)};
+        *(u32x2_t *)(vp + d) = u32x2_t{pack_bf16(V[4 * r4], V[4 * r4 + 1]), pack_bf16(V[4 * r4 + 2], V[4 * r4 + 3])};
+      }
+  } else {
+    const size_t row = ((((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key) * 128;
 #pragma unroll
-        for (int rr2 = 0; rr2 < 4; ++rr2) {
-          const f32x16_t &X = acc[kb][c];
-          *(u32x2_t *)(dst + 32 * c + 8 * rr2 + 4 * g) =
-              u32x2_t{pack_bf16(X[4 * rr2] * f, X[4 * rr2 + 1] * f),
-                      pack_bf16(X[4 * rr2 + 2] * f, X[4 * rr2 + 3] * f)};
-        }
-    } else {
-      float *part = is_k ? a.dk_part : a.dv_part;
-      const size_t row = ((((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key) * 128;
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int rr2 = 0; rr2 < 4; ++rr2) {
-          const f32x16_t &X = acc[kb][c];
-          *(f32x4_t *)(part + row + 32 * c + 8 * rr2 + 4 * g) =
-              f32x4_t{X[4 * rr2], X[4 * rr2 + 1], X[4 * rr2 + 2], X[4 * rr2 + 3]};
-        }
-    }
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = 32 * c + 8 * r4 + 4 * g;
+        *(f32x4_t *)(a.dk_part + row + d) =
+            f32x4_t{dk_acc[c][4 * r4], dk_acc[c][4 * r4 + 1], dk_acc[c][4 * r4 + 2], dk_acc[c][4 * r4 + 3]};
+        *(f32x4_t *)(a.dv_part + row + d) =
+            f32x4_t{dv_acc[c][4 * r4], dv_acc[c][4 * r4 + 1], dv_acc[c][4 * r4 + 2], dv_acc[c][4 * r4 + 3]};
+      }
   }
 }
 
@@ -1361,10 +1402,10 @@ int pick_split(const fw_attn_bwd_params *p, long target) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// The stored path (128/128 head dims): the dq kernel writes P and dS once and
-// the dk / dv kernel reads them instead of recomputing the scores.  It needs
-// two bf16 (B, H, Sq rounded up to 128, Sk rounded up to 128) planes of
-// workspace; above kStoredMaxBytes the recomputing kernels run instead.
+// The stored path (128/128 head dims): the dq kernel writes P once and the
+// dk / dv kernel reads it instead of recomputing the scores.  It needs a bf16
+// (B, H, Sq rounded up to 128, Sk rounded up to 256) plane of workspace;
+// above kStoredMaxBytes the recomputing kernels run instead.
 // FW_BWD_STORED=0 selects the recomputing kernels at any size.
 constexpr size_t kStoredMaxBytes = (size_t)8 << 30;
 
@@ -1378,7 +1419,7 @@ bool use_stored(const fw_attn_bwd_params *p) {
   if (p->head_dim != 128 || head_dim_v_of(p) != 128) return false;
   const char *e = getenv("FW_BWD_STORED");
   if (e && e[0] == '0') return false;
-  return 2 * stored_plane_bytes(p) <= kStoredMaxBytes;
+  return stored_plane_bytes(p) <= kStoredMaxBytes;
 }
 
 // The stored dk / dv kernel runs two workgroups per CU and wants about four
@@ -1397,7 +1438,7 @@ extern "C" size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p) {
   const int split = bwd_split(p);
   const size_t keys = (size_t)split * p->batch * p->nheads_k * p->seqlen_k * 4;
   if (split > 1) bytes += align256(keys * p->head_dim) + align256(keys * head_dim_v_of(p));
-  if (use_stored(p)) bytes += 2 * stored_plane_bytes(p);
+  if (use_stored(p)) bytes += stored_plane_bytes(p);
   return bytes;
 }
 
@@ -1465,7 +1506,7 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     a.dv_part = (float *)(ws + 2 * align256(rows * 4) + align256(keys * p->head_dim));
   }
   const bool stored = use_stored(p);
-  a.ws_p = a.ws_ds = nullptr;
+  a.ws_p = nullptr;
   a.sq_pad = ceil_div(p->seqlen_q, 128) * 128;
   a.sk_pad = ceil_div(p->seqlen_k, 256) * 256;
   if (stored) {
@@ -1475,7 +1516,6 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
       o += align256(keys * p->head_dim) + align256(keys * dvw);
     }
     a.ws_p = (uint16_t *)(ws + o);
-    a.ws_ds = (uint16_t *)(ws + o + stored_plane_bytes(p));
   }
   a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qst = p->q_stride_t;
   const bool o_given = p->o_stride_b || p->o_stride_h || p->o_stride_t;
@@ -1499,9 +1539,12 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   a.qscale = p->softmax_scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
 
-  fw_bwd_prep_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a);  // 16 rows per block
-  int st = check_launch("fw_bwd_prep_kernel");
-  if (st != FW_OK) return st;
+  int st = FW_OK;
+  if (!stored) {
+    fw_bwd_prep_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a);  // 16 rows per block
+    st = check_launch("fw_bwd_prep_kernel");
+    if (st != FW_OK) return st;
+  }
   const bool wide = dkv_chunks(p) > 1 || dvw != p->head_dim;
   const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split, dkv_chunks(p));
   const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);

@@ -181,6 +181,12 @@ __device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, ui
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
 }
+// 4 bytes per active lane from base + voff[lane] into LDS at lds_addr + 4 *
+// lane (global_load_lds_dword).
+__device__ __forceinline__ void lds_dma4(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :: "s"(lds_addr), "v"(voff), "s"(base) : "memory", "m0");
+}
 // The same copy with the non-temporal hint, for data read once.
 __device__ __forceinline__ void lds_dma16_nt(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"

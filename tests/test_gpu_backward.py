@@ -226,10 +226,11 @@ def test_forward_backward_bitwise_repeat_head_dims(d):
 
 def test_stored_path_matches_recompute_at_c2_shape(monkeypatch):
     """At BASELINE C2's shape (1 x 32/4 heads x 4096, causal) the stored path
-    (P and dS planes, 16 key blocks of 256, 128 query tiles, heads split 8
-    ways) against the recomputing kernels (parity-tested above): the two
-    round P and dS at different points, so they agree to bf16 accuracy, not
-    bitwise; an indexing error in the planes would differ by O(1)."""
+    (the P plane, 16 key blocks of 256, 128 query tiles, heads split 8 ways)
+    against the recomputing kernels (parity-tested above).  dq is the same
+    computation; dk's dS is formed from the stored bf16 P, so it differs by
+    bf16 rounding (measured 0.45% of max |dk|); an indexing error in the
+    plane would differ by O(1)."""
     announce("bwd stored vs recompute at C2 shape")
     gen = torch.Generator(device=DEV).manual_seed(7)
     b, h, hk, s, d = 1, 32, 4, 4096, 128
@@ -250,4 +251,4 @@ def test_stored_path_matches_recompute_at_c2_shape(monkeypatch):
         scale = r.abs().max().item()
         print(f"C2 {name}: max |stored - recompute| {err:.3e}, max |grad| {scale:.3e}")
         assert torch.isfinite(a).all()
-        assert err <= 2e-3 * scale, (name, err, scale)  # measured: dq 0, dk / dv one bf16 step
+        assert err <= 1e-2 * scale, (name, err, scale)
