@@ -592,32 +592,26 @@ struct CombineArgs {
   const float *vd;  // device v_descale scalar, or null (v_descale above)
 };
 
-// One block per (b, work item, group of 4 rows): thread t merges row
-// 4*blockIdx.x + t/64 over the row's segments s = (t/16)%4, +4, ... for dims
-// 8*(t%16) .. +7 (and +128 for d256); the 4 segment groups then merge through
-// LDS.
+// One block per (work item, b), 16 threads per row of the q tile: thread t
+// merges row t / 16 over all of the row's segments, in segment order, for
+// dims 8 * (t % 16) .. + 7 (and + 128 for d256).  The loads of up to kBatch
+// segments are issued before any of them is used, so a row with at most
+// kBatch segments costs one memory latency after the range lookup.
 template <int D>
 __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
   constexpr int VH = kVH<D>;
-  const bool dims_ok = 8 * (threadIdx.x & 15) < D;  // head_dim 64: parts 8-15 hold no dims
-  const DecodeArgs &a = c.d;
-  __shared__ float s_acc[4][4][16][8 * VH];
-  __shared__ float2 s_ml[4][4];
-  const int lane = threadIdx.x & 63;
   const int part = threadIdx.x & 15;
-  const int grp = (threadIdx.x >> 4) & 3;
-  const int rl = threadIdx.x >> 6;
-  const int item = blockIdx.y;
+  const bool dims_ok = 8 * part < D;  // head_dim 64: parts 8-15 hold no dims
+  const DecodeArgs &a = c.d;
+  const int item = blockIdx.x;
   const int h = item / a.n_qtiles;
   const int qt = item % a.n_qtiles;
-  const int b = blockIdx.z;
-  const int row = 4 * blockIdx.x + rl;  // row inside the q tile
+  const int b = blockIdx.y;
+  const int row = threadIdx.x >> 4;  // row inside the q tile
   const int r = qt * 16 + row;
-  const bool valid = row < 16 && r < a.Rq;
+  if (row >= a.rows_item || r >= a.Rq) return;
   const int nact = active_rows(a);
   const bool active = b < nact;
-  // This row's segments: key ranges x_first .. x_last of the decode launch
-  // (a row longer than the tiles counted there has none past them).
   // This row's segments, as the decode launch recorded them.
   int nsp = 0, x_first = 0;
   if (active) {
@@ -633,77 +627,50 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
   float acc[8 * VH];
 #pragma unroll
   for (int e = 0; e < 8 * VH; ++e) acc[e] = 0.f;
-  // The loads of up to kBatch segments are issued before any of them is used
-  // (one memory latency per batch instead of one per segment).
   constexpr int kBatch = 8;
-  if (valid) {
-    for (int s0 = grp; s0 < nsp; s0 += 4 * kBatch) {
-      float2 ml[kBatch];
-      f32x4_t v[kBatch][2 * VH];
+  for (int s0 = 0; s0 < nsp; s0 += kBatch) {
+    float2 ml[kBatch];
+    f32x4_t v[kBatch][2 * VH];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int s = min(s0 + 4 * i, nsp - 1);
-        const size_t slot = ((size_t)(x_first + s + b) * n_items + item) * a.rows_item + row;
-        ml[i] = a.ws_ml[slot];
-        const float *po = a.ws_o + slot * D + part * 8;
+    for (int i = 0; i < kBatch; ++i) {
+      const int sg = min(s0 + i, nsp - 1);
+      const size_t slot = ((size_t)(x_first + sg + b) * n_items + item) * a.rows_item + row;
+      ml[i] = a.ws_ml[slot];
+      const float *po = a.ws_o + slot * D + part * 8;
 #pragma unroll
-        for (int vh = 0; vh < VH; ++vh) {
-          v[i][2 * vh] = dims_ok ? *(const f32x4_t *)(po + 128 * vh) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-          v[i][2 * vh + 1] = dims_ok ? *(const f32x4_t *)(po + 128 * vh + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        if (s0 + 4 * i >= nsp || ml[i].x == -INFINITY) continue;
-        const float Mn = fmaxf(M, ml[i].x);
-        const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml[i].x - Mn);
-#pragma unroll
-        for (int q4 = 0; q4 < 2 * VH; ++q4)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[4 * q4 + e] = acc[4 * q4 + e] * c_old + v[i][q4][e] * c_new;
-        Lsum = Lsum * c_old + ml[i].y * c_new;
-        M = Mn;
+      for (int vh = 0; vh < VH; ++vh) {
+        v[i][2 * vh] = dims_ok ? *(const f32x4_t *)(po + 128 * vh) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        v[i][2 * vh + 1] = dims_ok ? *(const f32x4_t *)(po + 128 * vh + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (s0 + i >= nsp || ml[i].x == -INFINITY) continue;
+      const float Mn = fmaxf(M, ml[i].x);
+      const float c_old = fast_exp2(M - Mn), c_new = fast_exp2(ml[i].x - Mn);
+#pragma unroll
+      for (int q4 = 0; q4 < 2 * VH; ++q4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[4 * q4 + e] = acc[4 * q4 + e] * c_old + v[i][q4][e] * c_new;
+      Lsum = Lsum * c_old + ml[i].y * c_new;
+      M = Mn;
+    }
   }
-#pragma unroll
-  for (int e = 0; e < 8 * VH; ++e) s_acc[rl][grp][part][e] = acc[e];
-  if (part == 0) s_ml[rl][grp] = make_float2(M, Lsum);
-  __syncthreads();
-  if (!valid || grp != 0) return;
-  float Mt = -INFINITY;
-#pragma unroll
-  for (int g2 = 0; g2 < 4; ++g2) Mt = fmaxf(Mt, s_ml[rl][g2].x);
   const int tok = r / a.G, hq = h * a.G + r % a.G;
-  float o[8 * VH];
-#pragma unroll
-  for (int e = 0; e < 8 * VH; ++e) o[e] = 0.f;
-  float Lt = 0.f;
-  if (Mt != -INFINITY) {
-#pragma unroll
-    for (int g2 = 0; g2 < 4; ++g2) {
-      const float2 ml = s_ml[rl][g2];
-      if (ml.x == -INFINITY) continue;
-      const float cf = fast_exp2(ml.x - Mt);
-      Lt += ml.y * cf;
-#pragma unroll
-      for (int e = 0; e < 8 * VH; ++e) o[e] += s_acc[rl][g2][part][e] * cf;
-    }
-  }
   if (c.sinks) {
     const float sk = c.sinks[hq] * kLog2e;
     if (sk != -INFINITY) {
-      const float Mn = fmaxf(Mt, sk);
-      const float c_old = fast_exp2(Mt - Mn);
+      const float Mn = fmaxf(M, sk);
+      const float c_old = fast_exp2(M - Mn);
 #pragma unroll
-      for (int e = 0; e < 8 * VH; ++e) o[e] *= c_old;
-      Lt = Lt * c_old + fast_exp2(sk - Mn);
-      Mt = Mn;
+      for (int e = 0; e < 8 * VH; ++e) acc[e] *= c_old;
+      Lsum = Lsum * c_old + fast_exp2(sk - Mn);
+      M = Mn;
     }
   }
-  const bool any = active && Lt > 0.f;
+  const bool any = active && Lsum > 0.f;
   const float vdesc = c.vd ? *c.vd : c.v_descale;
-  const float scale = any ? vdesc / Lt : 0.f;
+  const float scale = any ? vdesc / Lsum : 0.f;
 #pragma unroll
   for (int vh = 0; vh < VH; ++vh) {
     if (!dims_ok) break;
@@ -711,11 +678,11 @@ __global__ __launch_bounds__(256) void fw_decode_combine(CombineArgs c) {
     u32x4_t w;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      w[e] = pack_bf16(o[8 * vh + 2 * e] * scale, o[8 * vh + 2 * e + 1] * scale);
+      w[e] = pack_bf16(acc[8 * vh + 2 * e] * scale, acc[8 * vh + 2 * e + 1] * scale);
     *(u32x4_t *)op = w;
   }
   if (c.lse && part == 0)
-    c.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (Mt + __log2f(Lt)) * kLn2 : -INFINITY;
+    c.lse[((size_t)b * a.H + hq) * a.Sq + tok] = any ? (M + __log2f(Lsum)) * kLn2 : -INFINITY;
 }
 
 // Keys whose block-table entries one prefetch covers: 64 * kTblPerLane pages
@@ -871,11 +838,11 @@ static int decode_launch(const fw_decode_params *p, void *ws, size_t ws_bytes,
   c.lse = p->lse;
   c.v_descale = p->v_descale;
   c.vd = p->v_descale_ptr;
-  const int row_groups = (L.rows_item + 3) / 4;
-  const dim3 grid(row_groups, p->nheads_k * L.n_qtiles, p->batch);
-  if (p->head_dim == 256) fw_decode_combine<256><<<grid, 256, 0, s>>>(c);
-  else if (p->head_dim == 64) fw_decode_combine<64><<<grid, 256, 0, s>>>(c);
-  else fw_decode_combine<128><<<grid, 256, 0, s>>>(c);
+  const dim3 grid(p->nheads_k * L.n_qtiles, p->batch);
+  const int threads = 16 * L.rows_item;  // rows_item <= 16
+  if (p->head_dim == 256) fw_decode_combine<256><<<grid, threads, 0, s>>>(c);
+  else if (p->head_dim == 64) fw_decode_combine<64><<<grid, threads, 0, s>>>(c);
+  else fw_decode_combine<128><<<grid, threads, 0, s>>>(c);
   return check_launch("fw_decode_combine");
 }
 
