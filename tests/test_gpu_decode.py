@@ -138,6 +138,49 @@ def test_folded_verify_window(dtype):
     assert_lse(lse.cpu().numpy(), rl)
 
 
+@pytest.mark.parametrize("dtype,sq,nheads,splits", [
+    ("bf16", 3, 8, 0), ("e4m3", 16, 8, 0), ("bf16", 20, 24, 0), ("bf16", 5, 8, 300),
+    ("e4m3", 7, 8, 300)])
+def test_verify_window_boundaries(dtype, sq, nheads, splits):
+    """Folded verify windows of 3 to 20 tokens whose new keys straddle a
+    32-key tile (L0 % 32 = 30, 31) and, with 300 key ranges, the boundary
+    between two workgroups' ranges (every range a few tiles); the whole pool,
+    appended rows included, bit-exact."""
+    announce(f"verify window boundaries {dtype} sq={sq} heads={nheads} splits={splits}")
+    rng = np.random.default_rng(40 + sq)
+    lengths = [30, 62, 1000, 0, 95, 4127]
+    b = len(lengths)
+    dt = torch.bfloat16 if dtype == "bf16" else FP8[dtype]
+    ks, vs = (1.0, 1.0) if dtype == "bf16" else (1.25, 0.6)
+    case = PagedCase(rng, batch=b, nheads=nheads, nheads_k=8 if nheads == 8 else 4, lengths=lengths,
+                     new_tokens=[sq] * b, dtype=dt, k_descale=ks, v_descale=vs)
+    q = randn(rng, (b, sq, nheads, 128))
+    if splits:
+        # the API's two launches, the decode one with `splits` key ranges
+        from flywheel_tpu.decode import append_ragged
+        from tests.gpu_util import dev_from_codes
+        pool = case.pool()
+        shape = (b * sq, case.nheads_k, 128)
+        lens = torch.tensor(case.lengths, dtype=torch.int32, device=DEV)
+        table = torch.tensor(case.table, device=DEV)
+        append_ragged(pool, dev_from_codes(case.k_codes.reshape(shape), case.dtype),
+                      dev_from_codes(case.v_codes.reshape(shape), case.dtype), None, lens, table,
+                      None, case.nheads_k, batch=b)
+        out, lse = paged_decode(
+            to_dev_bf16(q), pool, None, None, lens, table, None, None, nheads_k=case.nheads_k,
+            softmax_scale=128 ** -0.5, softcap=0.0, causal=True, window_left=-1,
+            k_descale=case.k_descale, v_descale=case.v_descale, seqlen_add=sq, return_lse=True,
+            num_splits=splits)
+        torch.cuda.synchronize()
+    else:
+        out, lse, pool = run_decode(case, q, causal=True)
+    exp_pool = case.expected_pool()
+    np.testing.assert_array_equal(codes_of(pool), exp_pool)
+    ro, rl = oracle(case, q, exp_pool, causal=True)
+    assert_close(out.float().cpu().numpy(), ro, fp8=dtype != "bf16")
+    assert_lse(lse.cpu().numpy(), rl)
+
+
 def test_num_active_rows_skipped():
     announce("decode num_active=2")
     rng = np.random.default_rng(5)
