@@ -491,8 +491,8 @@ def workload_gemm(args, device):
                 cpu=None)
 
 
-def _c2_inputs(device):
-    b, h, hk, s, d = 1, 32, 4, 4096, 128
+def _c2_inputs(device, d=128):
+    b, h, hk, s = 1, 32, 4, 4096
     gen = torch.Generator(device=device).manual_seed(0)
     q = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
     k = torch.randn((b, hk, s, d), generator=gen, device=device, dtype=torch.bfloat16)
@@ -500,18 +500,20 @@ def _c2_inputs(device):
     return (b, h, hk, s, d), gen, q, k, v
 
 
-def workload_bwd(args, device):
-    """c2's shape through the dense backward (fw_attn_bwd: row statistics, dk/dv,
-    dq), inputs (q, k, v, out, lse, dout) resident; FLOPs counted as 2.5x the
-    forward's (the five backward products; the kernels also recompute two)."""
+def workload_bwd(args, device, d=128):
+    """c2's shape (at head dim d) through the dense backward (fw_attn_bwd),
+    inputs (q, k, v, out, lse, dout) resident; FLOPs counted as 2.5x the
+    forward's (the five backward products; the kernels evaluate six at
+    128/128, seven at the wide head dims)."""
     from flywheel_tpu import flash_attn_func
     from flywheel_tpu.backward import attn_bwd
-    (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device)
+    (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device, d)
     do = torch.randn((b, h, s, d), generator=gen, device=device, dtype=torch.bfloat16)
     out, lse = flash_attn_func(q, k, v, causal=True, return_softmax_lse=True)
     kw = dict(qs=(h * s * d, s * d, d), ks=(hk * s * d, s * d, d), vs=(hk * s * d, s * d, d),
               os_=(h * s * d, s * d, d), ls=(h * s, s), batch=b,
-              nheads=h, nheads_k=hk, seqlen_q=s, seqlen_k=s, softmax_scale=d ** -0.5, causal=True)
+              nheads=h, nheads_k=hk, seqlen_q=s, seqlen_k=s, softmax_scale=d ** -0.5, causal=True,
+              head_dim=d, head_dim_v=d)
     flops = 2.5 * 4.0 * s * s * h * d / 2 * b
     ms = timed(lambda: attn_bwd(q, k, v, out, do, lse, **kw), args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
@@ -529,12 +531,14 @@ def workload_bwd(args, device):
                         "TFLOP/s")
 
     return dict(
-        name="bwd", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
+        name="bwd" if d == 128 else f"bwd{d}", unit="TFLOP/s", value=tflops, ms=ms, dtype="bf16",
         config={"workload": "flash_attn_func backward (dq, dk, dv), causal GQA", "batch": b,
                 "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": "fw_bwd_prep + fw_bwd_dkv + fw_bwd_reduce + fw_bwd_dq (whole backward)",
+                  "kernel": ("fw_bwd_dq_store + fw_bwd_dkv_stored + fw_bwd_reduce (whole backward)"
+                             if d == 128 else
+                             "fw_bwd_prep + fw_bwd_dkv_wide + fw_bwd_reduce + fw_bwd_dq_wide (whole backward)"),
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=cpu)
 
@@ -707,6 +711,7 @@ WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": work
 # prefill shape (docs/v7x.md:60)
 DEFAULT = ["c2", "c3", "c4", "c5", "c2d256"]
 EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "bwd": workload_bwd, "rope": workload_rope,
+         "bwd256": lambda args, device: workload_bwd(args, device, d=256),
          "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
          "cp256": workload_cp256, "cp256mha": lambda args, device: workload_cp256(args, device, hk=32),
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}
