@@ -252,3 +252,27 @@ def test_stored_path_matches_recompute_at_c2_shape(monkeypatch):
         print(f"C2 {name}: max |stored - recompute| {err:.3e}, max |grad| {scale:.3e}")
         assert torch.isfinite(a).all()
         assert err <= 1e-2 * scale, (name, err, scale)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_backward_random_shapes(seed):
+    """Seeded random shapes through the 128/128 backward (the stored path:
+    P plane blocks of 32 rows x 64 keys, 256-key dk/dv workgroups, head
+    chunks): lengths that are multiples of none of 32, 64, 256, seqlen_q
+    above and below seqlen_k, MHA / GQA / MQA, batch 1-2, causal or full,
+    head-major or token-major; against the float64 oracle under the
+    reference's 3x rule."""
+    rng = np.random.default_rng(1000 + seed)
+    b = int(rng.integers(1, 3))
+    hk = int(rng.choice([1, 2, 4]))
+    h = hk * int(rng.choice([1, 2, 4]))
+    sq = int(rng.integers(1, 600))
+    sk = int(rng.integers(1, 600))
+    causal = bool(rng.integers(0, 2))
+    token_major = bool(rng.integers(0, 2))
+    what = (f"bwd random seed={seed} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+            f" token_major={token_major}")
+    announce(what)
+    q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
+    do = randn(rng, (b, sq, h, 128))
+    check_grads(run(q, k, v, do, causal, token_major=token_major), q, k, v, do, causal, what)
