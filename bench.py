@@ -706,11 +706,11 @@ def workload_dec256(args, device):
 
 
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5,
-             "c2d256": workload_c2d256}
+             "c2d256": workload_c2d256, "bwd": workload_bwd}
 # "all": the four BASELINE workloads, then the reference's published dense
-# prefill shape (docs/v7x.md:60)
-DEFAULT = ["c2", "c3", "c4", "c5", "c2d256"]
-EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "bwd": workload_bwd, "rope": workload_rope,
+# prefill shape (docs/v7x.md:60) and the dense backward at C2's shape
+DEFAULT = ["c2", "c3", "c4", "c5", "c2d256", "bwd"]
+EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "rope": workload_rope,
          "bwd256": lambda args, device: workload_bwd(args, device, d=256),
          "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
          "cp256": workload_cp256, "cp256mha": lambda args, device: workload_cp256(args, device, hk=32),
