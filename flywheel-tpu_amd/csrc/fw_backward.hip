@@ -62,6 +62,7 @@ struct BwdArgs {
   // stored_block(b * H + h, q / 32, key / 64)
   uint16_t *ws_p;
   int sq_pad, sk_pad;
+  int dq_hpw;  // stored path: query heads per dq workgroup (4, 2 or 1; divides G)
 };
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t *p) { return *(const u32x4_t *)p; }
@@ -591,14 +592,23 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];  // [K | V] x 2
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)smem;
 
+  // Workgroup = 4 waves = dq_hpw query heads of one KV head x (4 / dq_hpw)
+  // blocks of 32 query rows: the heads of a GQA group share the K / V rows
+  // copied into LDS (the workgroup's keys are those its last row sees).
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
-  const int n_qt = (a.Sq + 127) / 128;
+  const int hpw = a.dq_hpw, rpw = 4 / hpw;
+  const int wg_rows = 32 * rpw;
+  const int n_qt = (a.Sq + wg_rows - 1) / wg_rows;
   const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y;
-  const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
-  const int q0 = qt * 128;
+  const int groups = a.G / hpw;
+  const int hgi = blockIdx.y % groups, bk = blockIdx.y / groups;
+  const int b = bk / a.Hk, hk = bk % a.Hk;
+  const int h = hk * a.G + hgi * hpw + w % hpw;  // this wave's query head
+  const int bh = b * a.H + h;
+  const int q_wg = qt * wg_rows;
+  const int q0 = q_wg + 32 * (w / hpw);  // this wave's first row
   const int off = a.Sk - a.Sq;
-  const int qrow = q0 + 32 * w + n;
+  const int qrow = q0 + n;
   const bool row_ok = qrow < a.Sq;
 
   // The row's statistics are formed here (the recomputing path's prep
@@ -640,7 +650,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
 
   // visible keys of a row: [0, hi)
   auto row_hi = [&](int r) { return CAUSAL ? min(a.Sk, r + off + 1) : a.Sk; };
-  const int last_row = min(q0 + 127, a.Sq - 1);
+  const int last_row = min(q_wg + wg_rows - 1, a.Sq - 1);
   const int wg_hi = row_hi(last_row);
   const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
   const int r_hi = row_hi(qrow);
@@ -668,7 +678,8 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
 
   // ---- stored P: the wave's first block (key tile 0) and this lane's byte
   // offset in a block's 1 KiB chunks
-  const size_t blk = stored_block(a, bh, (q0 >> 5) + __builtin_amdgcn_readfirstlane(w), 0) * 4096;
+  const size_t blk = stored_block(a, __builtin_amdgcn_readfirstlane(bh),
+                                  __builtin_amdgcn_readfirstlane(q0 >> 5), 0) * 4096;
   const uint8_t *pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
   const uint32_t lane_st = 16u * (2 * n + g);
   u32x4_t pw_prev[4];   // the previous tile's P words, chunk 2st + u2
@@ -692,7 +703,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
     const uint32_t kb_l = lds0 + (uint32_t)(t & 1) * (2 * kTile), vb_l = kb_l + kTile;
     const int kb = t * kBT;
     // keys no row of the wave sees are masked to p = 0 (one code path)
-    const bool full = kb + kBT <= row_hi(q0 + 32 * w);
+    const bool full = kb + kBT <= row_hi(q0);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       f32x16_t sacc, dpacc;
@@ -1550,8 +1561,10 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);
   if (stored) {
     // dq first (it writes P and dS), then dk / dv from them
-    if (p->causal) fw_bwd_dq_store_kernel<true><<<gq, 256, 0, s>>>(a);
-    else fw_bwd_dq_store_kernel<false><<<gq, 256, 0, s>>>(a);
+    a.dq_hpw = a.G % 4 == 0 ? 4 : a.G % 2 == 0 ? 2 : 1;
+    const dim3 gqs(ceil_div(p->seqlen_q, 32 * (4 / a.dq_hpw)), p->batch * p->nheads / a.dq_hpw);
+    if (p->causal) fw_bwd_dq_store_kernel<true><<<gqs, 256, 0, s>>>(a);
+    else fw_bwd_dq_store_kernel<false><<<gqs, 256, 0, s>>>(a);
     st = check_launch("fw_bwd_dq_kernel");
     if (st != FW_OK) return st;
     const dim3 gst(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kStKeys));
