@@ -191,8 +191,11 @@ __global__ __launch_bounds__(256) void fw_bwd_dkv_kernel(BwdArgs a) {
   float *Dl = Ls + kBT;                                         // delta
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
-  const int k0 = blockIdx.x * 128;
-  int z = blockIdx.y;
+  // one-dimensional grid, key block slowest: the heaviest (causal: first) key
+  // blocks of every head are dispatched first
+  const int nz = a.B * a.Hk * a.split;
+  const int k0 = (int)(blockIdx.x / nz) * 128;
+  int z = (int)(blockIdx.x % nz);
   const int sp = z % a.split;
   z /= a.split;
   const int hk = z % a.Hk;
@@ -436,9 +439,11 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
   uint16_t *Kt = (uint16_t *)(smem + 2 * kRowTileB);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  // one-dimensional grid, query tile slowest: the longest causal rows of
+  // every head are dispatched first
   const int n_qt = (a.Sq + 127) / 128;
-  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / (a.B * a.H));
+  const int bh = (int)(blockIdx.x % (a.B * a.H));
   const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
   const int q0 = qt * 128;
   const int off = a.Sk - a.Sq;
@@ -599,9 +604,13 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   const int hpw = a.dq_hpw, rpw = 4 / hpw;
   const int wg_rows = 32 * rpw;
   const int n_qt = (a.Sq + wg_rows - 1) / wg_rows;
-  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
+  // one-dimensional grid, query tile slowest: the longest causal rows of
+  // every head group are dispatched first
+  const int n_hg = a.B * a.H / hpw;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / n_hg);
+  const int yb = (int)(blockIdx.x % n_hg);
   const int groups = a.G / hpw;
-  const int hgi = blockIdx.y % groups, bk = blockIdx.y / groups;
+  const int hgi = yb % groups, bk = yb / groups;
   const int b = bk / a.Hk, hk = bk % a.Hk;
   const int h = hk * a.G + hgi * hpw + w % hpw;  // this wave's query head
   const int bh = b * a.H + h;
@@ -1060,13 +1069,17 @@ __global__ __launch_bounds__(256, 1) void fw_bwd_dkv_wide_kernel(BwdArgs a) {
   const uint32_t lds_qr = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)Qr;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
-  const int k0 = blockIdx.x * 128;
-  int z = blockIdx.y;
+  // one-dimensional grid, key block slowest: the heaviest (causal: first) key
+  // blocks of every head and chunk are dispatched first
+  constexpr int C = (DQ > DV ? DQ : DV) / 128;
+  const int pc = a.B * a.Hk * a.split * C;
+  const int k0 = (int)(blockIdx.x / pc) * 128;
+  const int cc = (int)(blockIdx.x % pc) % C;
+  int z = (int)(blockIdx.x % pc) / C;
   const int sp = z % a.split;
   z /= a.split;
   const int hk = z % a.Hk;
   const int b = z / a.Hk;
-  const int cc = blockIdx.z;
   const bool do_k = cc < DQ / 128, do_v = cc < DV / 128;
   const int chunk = a.G / a.split;
   const int off = a.Sk - a.Sq;
@@ -1256,11 +1269,15 @@ __global__ __launch_bounds__(256, 1) void fw_bwd_dq_wide_kernel(BwdArgs a) {
   const uint32_t lds_ks = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)Ks;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  // one-dimensional grid, query tile slowest: the longest causal rows of
+  // every head and chunk are dispatched first
+  constexpr int C = DQ / 128;
+  const int hc = a.B * a.H * C;
   const int n_qt = (a.Sq + 127) / 128;
-  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / hc);
+  const int cc = (int)(blockIdx.x % hc) % C;
+  const int bh = (int)(blockIdx.x % hc) / C;
   const int b = bh / a.H, h = bh % a.H, hk = h / a.G;
-  const int cc = blockIdx.z;
   const int q0 = qt * 128;
   const int off = a.Sk - a.Sq;
   const int qrow = q0 + 32 * w + n;
@@ -1558,11 +1575,14 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   }
   const bool wide = dkv_chunks(p) > 1 || dvw != p->head_dim;
   const dim3 gkv(ceil_div(p->seqlen_k, 128), p->batch * p->nheads_k * a.split, dkv_chunks(p));
+  // one-dimensional grids, heaviest blocks first
+  const dim3 gkv1(gkv.x * gkv.y * gkv.z);
   const dim3 gq(ceil_div(p->seqlen_q, 128), p->batch * p->nheads, p->head_dim / 128);
+  const dim3 gq1(gq.x * gq.y * gq.z);
   if (stored) {
     // dq first (it writes P and dS), then dk / dv from them
     a.dq_hpw = a.G % 4 == 0 ? 4 : a.G % 2 == 0 ? 2 : 1;
-    const dim3 gqs(ceil_div(p->seqlen_q, 32 * (4 / a.dq_hpw)), p->batch * p->nheads / a.dq_hpw);
+    const dim3 gqs(ceil_div(p->seqlen_q, 32 * (4 / a.dq_hpw)) * (p->batch * p->nheads / a.dq_hpw));
     if (p->causal) fw_bwd_dq_store_kernel<true><<<gqs, 256, 0, s>>>(a);
     else fw_bwd_dq_store_kernel<false><<<gqs, 256, 0, s>>>(a);
     st = check_launch("fw_bwd_dq_kernel");
@@ -1577,12 +1597,12 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     return check_launch("fw_bwd_reduce_kernel");
   }
   if (wide) {
-    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, true, s);
-    else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, true, s);
+    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv1, gq1, true, s);
+    else launch_wide<false>(a, p->head_dim, dvw, gkv1, gq1, true, s);
   } else if (p->causal) {
-    fw_bwd_dkv_kernel<true><<<gkv, 256, 0, s>>>(a);
+    fw_bwd_dkv_kernel<true><<<gkv1, 256, 0, s>>>(a);
   } else {
-    fw_bwd_dkv_kernel<false><<<gkv, 256, 0, s>>>(a);
+    fw_bwd_dkv_kernel<false><<<gkv1, 256, 0, s>>>(a);
   }
   st = check_launch("fw_bwd_dkv_kernel");
   if (st != FW_OK) return st;
@@ -1593,12 +1613,12 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     if (st != FW_OK) return st;
   }
   if (wide) {
-    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv, gq, false, s);
-    else launch_wide<false>(a, p->head_dim, dvw, gkv, gq, false, s);
+    if (p->causal) launch_wide<true>(a, p->head_dim, dvw, gkv1, gq1, false, s);
+    else launch_wide<false>(a, p->head_dim, dvw, gkv1, gq1, false, s);
   } else if (p->causal) {
-    fw_bwd_dq_kernel<true><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<true><<<gq1, 256, 0, s>>>(a);
   } else {
-    fw_bwd_dq_kernel<false><<<gq, 256, 0, s>>>(a);
+    fw_bwd_dq_kernel<false><<<gq1, 256, 0, s>>>(a);
   }
   return check_launch("fw_bwd_dq_kernel");
 }
