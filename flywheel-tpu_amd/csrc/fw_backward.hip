@@ -61,6 +61,7 @@ struct BwdArgs {
   // dq kernel's register image of a 32-row x 64-key tile, at
   // stored_block(b * H + h, q / 32, key / 64)
   uint16_t *ws_p;
+  uint16_t *ws_ds;  // dS in the same layout (head dims 256/256), or null
   int sq_pad, sk_pad;
   int dq_hpw;  // stored path: query heads per dq workgroup (4, 2 or 1; divides G)
 };
@@ -586,14 +587,23 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_kernel(BwdArgs a) {
 // them: both have the whole tile's compute before the wait at the top of
 // tile t + 1.  K^T comes from the K rows by transposing reads, so no
 // transposed copy is staged.
-// LDS rows are 256 bytes (one key) whose 16-byte chunks are permuted by
-// kv_swz(row): the 16 rows of a plain 16-byte read and the 4 rows of a
-// transposing read each fall on distinct banks.
-__device__ __forceinline__ int kv_swz(int r) { return 2 * (r & 7) + ((r >> 3) & 1); }
+// LDS rows are 256 (or 512) bytes, one key, whose 16-byte chunks are permuted
+// by kv_swz(row) within each 256 bytes: the 16 rows of a plain 16-byte read
+// fall on distinct banks, and so do the 32 lanes of a transposing read (rows
+// 4m .. 4m + 3, two adjacent chunk pairs: the pair index is XORed with
+// 2(row & 3) + bit 2 of the row).
+__device__ __forceinline__ int kv_swz(int r) { return 4 * (r & 3) + 2 * ((r >> 2) & 1) + ((r >> 3) & 1); }
 
-template <bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
-  constexpr int kTile = 64 * 256;  // bytes of 64 key rows
+template <bool CAUSAL, int D>
+__global__ __launch_bounds__(256, D == 128 ? 2 : 1) void fw_bwd_dq_store_kernel(BwdArgs a) {
+  // D = 128 or 256 (q, k, v and out).  At 256 the kernel also stores dS
+  // beside P, and runs one wave per SIMD (q, dout and dq of 32 rows take 256
+  // registers).
+  constexpr int kRow = 2 * D;          // bytes of one K / V row
+  constexpr int kTile = 64 * kRow;     // bytes of 64 key rows
+  constexpr int kNJ = D / 16;          // k-steps of S and dP
+  constexpr int kNC = D / 32;          // 32-dim blocks of dq
+  constexpr bool kDs = D > 128;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * kTile];  // [K | V] x 2
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)smem;
 
@@ -624,14 +634,14 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   // kernel does this): delta = rowsum(dout * out) from the dout operand and
   // the out row, lse_log2 = lse * log2 e (+inf for a row with no key); delta
   // goes to the workspace for the dk / dv kernel.
-  bf16x8_t qop[8], dop[8];
+  bf16x8_t qop[kNJ], dop[kNJ];
   float l2 = INFINITY, dl = 0.f;
   {
     const size_t base = (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)(row_ok ? qrow : 0) * a.qst;
     const size_t obase = (size_t)b * a.osb + (size_t)h * a.osh + (size_t)(row_ok ? qrow : 0) * a.ost;
     const float qs = row_ok ? a.qscale : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < kNJ; ++j) {
       qop[j] = __builtin_bit_cast(bf16x8_t, scale_words(ld16(a.q + base + 16 * j + 8 * g), qs));
       const u32x4_t d = ld16(a.dout + obase + 16 * j + 8 * g);
       const u32x4_t o = ld16(a.o + obase + 16 * j + 8 * g);
@@ -642,7 +652,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
         dl += bf16_hi(o[e]) * bf16_hi(d[e]);
       }
     }
-    dl += __shfl_xor(dl, 32, 64);  // the row's other 64 dims
+    dl += __shfl_xor(dl, 32, 64);  // the row's other half of the dims
     if (row_ok) {
       const float l = a.lse[(size_t)b * a.lsb + (size_t)h * a.lsh + qrow];
       l2 = l == -INFINITY ? INFINITY : l * kLog2e;
@@ -651,9 +661,9 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
       dl = 0.f;
     }
   }
-  f32x16_t dqacc[4];
+  f32x16_t dqacc[kNC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < kNC; ++c)
 #pragma unroll
     for (int e = 0; e < 16; ++e) dqacc[c][e] = 0.f;
 
@@ -664,40 +674,48 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   const int t_end = wg_hi > 0 ? (wg_hi + kBT - 1) / kBT : 0;
   const int r_hi = row_hi(qrow);
 
-  // ---- copies: wave w moves key rows 16w .. 16w + 15 of K and of V (4 rows
-  // of 256 bytes per instruction; lane: row 4i + lane / 16, LDS slot lane % 16
+  // ---- copies: wave w moves key rows 16w .. 16w + 15 of K and of V (kRPI
+  // rows per instruction; lane: row kRPI i + lane / kLPR, LDS slot lane % kLPR
   // holding global chunk slot ^ kv_swz(row))
+  constexpr int kRPI = 1024 / kRow, kLPR = 64 / kRPI;
   const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
   const uint8_t *kg = sgpr_ptr((const uint8_t *)(a.k + (size_t)b * a.ksb + (size_t)hk * a.ksh));
   const uint8_t *vg = sgpr_ptr((const uint8_t *)(a.v + (size_t)b * a.vsb + (size_t)hk * a.vsh));
   auto issue = [&](int t) __attribute__((always_inline)) {
     const uint32_t buf = lds0 + (uint32_t)(t & 1) * (2 * kTile);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + 4 * i + (lane >> 4);
+    for (int i = 0; i < 16 / kRPI; ++i) {
+      const int r = 16 * w + kRPI * i + lane / kLPR;
       const int key = min(t * kBT + r, a.Sk - 1);
-      const uint32_t ch = 16u * (uint32_t)((lane & 15) ^ kv_swz(r));
-      const uint32_t dst = buf + 256u * (16 * wu + 4 * i);
+      const uint32_t ch = 16u * (uint32_t)((lane % kLPR) ^ kv_swz(r));
+      const uint32_t dst = buf + (uint32_t)kRow * (16 * wu + kRPI * i);
       lds_dma16(kg, (uint32_t)(2 * (size_t)key * a.kst) + ch, dst);
       lds_dma16(vg, (uint32_t)(2 * (size_t)key * a.vst) + ch, dst + kTile);
     }
   };
   // byte offset of (row r, 16-byte chunk c) in a K or V tile
-  auto kv_at = [](int r, int c) { return (uint32_t)(256 * r + 16 * (c ^ kv_swz(r))); };
+  auto kv_at = [](int r, int c) { return (uint32_t)(kRow * r + 16 * (c ^ kv_swz(r))); };
 
   // ---- stored P: the wave's first block (key tile 0) and this lane's byte
   // offset in a block's 1 KiB chunks
   const size_t blk = stored_block(a, __builtin_amdgcn_readfirstlane(bh),
                                   __builtin_amdgcn_readfirstlane(q0 >> 5), 0) * 4096;
   const uint8_t *pst = sgpr_ptr((const uint8_t *)a.ws_p + blk);
+  const uint8_t *pds = kDs ? sgpr_ptr((const uint8_t *)a.ws_ds + blk) : nullptr;
   const uint32_t lane_st = 16u * (2 * n + g);
   u32x4_t pw_prev[4];   // the previous tile's P words, chunk 2st + u2
-  bf16x8_t dsop[4];     // this tile's dS, the B operand of dQ
+  bf16x8_t dsop[4];     // this tile's dS, the B operand of dQ (the same chunks)
+  // (the host keeps one head's plane below 4 GiB, so o fits 32 bits; the
+  // deferred stores run before the tile's compute overwrites pw_prev, dsop)
   auto store_prev = [&](int t) __attribute__((always_inline)) {
     const uint32_t o = ((uint32_t)(t >> 2) * (uint32_t)(a.sq_pad / 32) * 4u + (t & 3)) * 4096u + lane_st;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)  // written once, read once by the dk / dv kernel: non-temporal
+    for (int j = 0; j < 4; ++j) {  // written once, read once by the dk / dv kernel: non-temporal
       __builtin_nontemporal_store(pw_prev[j], (FW_GLOBAL u32x4_t *)(pst + o + 1024u * j));
+      if constexpr (kDs)
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, dsop[j]),
+                                    (FW_GLOBAL u32x4_t *)(pds + o + 1024u * j));
+    }
   };
 
   if (t_end > 0) issue(0);
@@ -731,13 +749,19 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
           va[j] = ld(vb_l, j);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j + 3 < 8) {
+        for (int j = 0; j < kNJ; ++j) {
+          if (j + 3 < kNJ) {
             ka[(j + 3) % 4] = ld(kb_l, j + 3);
             va[(j + 3) % 4] = ld(vb_l, j + 3);
           }
+          // at one wave per SIMD, fences keep each read three steps ahead of
+          // its MFMA (the scheduler would otherwise move it down to the MFMA;
+          // at D = 128 the fenced ring spills, and the SIMD's second wave
+          // covers the reads)
+          if constexpr (D > 128) __builtin_amdgcn_sched_barrier(0);
           sacc = mfma32(ka[j % 4], qop[j], sacc);    // S^T[key][q]
           dpacc = mfma32(va[j % 4], dop[j], dpacc);  // dP^T[key][q]
+          if constexpr (D > 128) __builtin_amdgcn_sched_barrier(0);
         }
       }
       if (!full) {
@@ -775,7 +799,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kNC; ++c) {
         const int r = 16 * u + 4 * g + ia;
         const int d = 32 * c + 16 * (grp & 1) + 4 * ib;
         const uint32_t ad = kb_l + kv_at(r, d >> 3) + 2u * (d & 7);
@@ -791,7 +815,7 @@ __global__ __launch_bounds__(256, 2) void fw_bwd_dq_store_kernel(BwdArgs a) {
   if (!row_ok) return;
   uint16_t *dp = a.dq + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qrow * a.qst;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < kNC; ++c)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const f32x16_t &Q = dqacc[c];
@@ -833,7 +857,11 @@ __device__ __forceinline__ bf16x8_t tr_rm(uint32_t Rb, int col, int u, int lane)
 // not write them) are zeroed by a select, on tiles that need a mask only.
 constexpr int kSQ = 32;                    // query rows per item
 constexpr int kStKeys = 256;               // keys per workgroup
-constexpr int kStPB = kSQ * kStKeys * 2;   // 16 KiB: P of an item
+// P of an item sits in LDS as 1 KiB chunks at a 1152-byte stride: the two
+// 16-lane groups of a transposing read that take chunks j and j + 1 then fall
+// on different banks.
+constexpr int kPChunk = 1152;
+constexpr int kStPB = kStKeys / 16 * kPChunk;  // 18 KiB: P of an item (16 chunks)
 constexpr int kStRB = kSQ * 128 * 2;       // 8 KiB: dout (or q) rows of an item
 constexpr int kStBuf = kStPB + 2 * kStRB + 256;  // + delta
 constexpr int kStRing = 3;
@@ -882,8 +910,8 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
     const uint32_t buf = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(it % kStRing) * kStBuf);
     const uint8_t *pb = sgpr_ptr((const uint8_t *)(a.ws_p + stored_block(a, b * a.H + h, t, k0 / 64) * 2048));
     const uint32_t pv = 1024u * w + 16u * lane;
-    lds_dma16_nt(pb, pv, buf + 1024u * wu);
-    lds_dma16_nt(pb, pv + 8192u, buf + 1024u * (wu + 8));
+    lds_dma16_nt(pb, pv, buf + kPChunk * wu);
+    lds_dma16_nt(pb, pv + 8192u, buf + kPChunk * (wu + 8));
     const int q = min(t * kSQ + rr, a.Sq - 1);
     const uint8_t *ob = sgpr_ptr((const uint8_t *)(a.dout + (size_t)b * a.osb + (size_t)h * a.osh));
     const uint8_t *qb = sgpr_ptr((const uint8_t *)(a.q + (size_t)b * a.qsb + (size_t)h * a.qsh));
@@ -900,7 +928,7 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
   // in slot 2(K0 + a) + (b & 1), bytes 8(b >> 1), of chunk (key tile, st, u2)
   // = (w / 2, w % 2, grp & 1); K0 = 16u + 4g (+ 8 for the hi half)
   const int grp = lane >> 4, ia = (lane & 15) >> 2, ib = lane & 3;
-  const uint32_t p_base = 2048u * w + 1024u * (grp & 1) + 16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
+  const uint32_t p_base = kPChunk * (2 * w + (grp & 1)) + 16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
   // A operands (row = dim, k = query row) from the dout (dV) and q (dK) rows:
   // row K0 + a, dims 32c + 16(grp & 1) + 4b .. + 3
   const uint32_t do_base = kStPB, q_base = kStPB + kStRB, dl_base = kStPB + 2 * kStRB;
@@ -1026,6 +1054,221 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
         *(f32x4_t *)(a.dv_part + row + d) =
             f32x4_t{dv_acc[c][4 * r4], dv_acc[c][4 * r4 + 1], dv_acc[c][4 * r4 + 2], dv_acc[c][4 * r4 + 3]};
       }
+  }
+}
+
+// ------------------------------------------------------------------ dk, dv from stored P and dS
+// Head dims 256/256: fw_bwd_dq_store_kernel<CAUSAL, 256> wrote dS beside P, so
+// dk and dv are two plain products over the query rows, nothing recomputed:
+//   dV^T[d][key] += dout^T[d][q] P[q][key],  dK^T[d][key] += q^T[d][q] dS[q][key]
+// (A dP recomputed here would need the keys' 256-dim V rows as a resident
+// operand beside 256 accumulator registers.)
+// Workgroup = 4 waves (one per SIMD) = 128 keys of KV head hk (and one chunk
+// of its query heads); wave w accumulates keys k0 + 64(w & 1) .. + 63 (two
+// 32-key halves s) over dims 128(w >> 1) .. + 127: 16 accumulators, 256
+// registers.  An item (query head, 32-row query tile) brings P and dS of the
+// 128 keys (8 KiB each) and the dout and q rows (16 KiB each) into one of
+// three LDS buffers, two items ahead; each dout or q operand read feeds the
+// products of both key halves.  Entries of P and dS the dq kernel did not
+// write (keys no row of the tile sees) are zeroed by a select on tiles that
+// need a mask.
+constexpr int kDsKeys = 128;                    // keys per workgroup
+constexpr int kDsPB = kDsKeys / 16 * kPChunk;  // 9 KiB: P (or dS) of an item (8 chunks)
+constexpr int kDsRB = kSQ * 256 * 2;            // 16 KiB: dout (or q) rows of an item
+constexpr int kDsBuf = 2 * kDsPB + 2 * kDsRB;   // 50 KiB
+constexpr int kDsRing = 3;
+
+// LDS byte offset of (row r, dims d ..) of a staged 32 x 256 row tile
+// (512-byte rows, 16-byte chunks permuted within each 256 bytes by kv_swz(r)).
+__device__ __forceinline__ uint32_t ds_row_off(int r, int d) {
+  return (uint32_t)(r * 512 + 16 * ((d >> 3) ^ kv_swz(r)) + 2 * (d & 7));
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void fw_bwd_dkv_ds_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kDsRing * kDsBuf];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FW_LDS uint8_t *)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, g = lane >> 5;
+  // blockIdx.y = key block: the heaviest (causal: first) key blocks of every
+  // head are dispatched first
+  const int k0 = blockIdx.y * kDsKeys;
+  int z = blockIdx.x;
+  const int sp = z % a.split;
+  z /= a.split;
+  const int hk = z % a.Hk;
+  const int b = z / a.Hk;
+  const int chunk = a.G / a.split;
+  const int off = a.Sk - a.Sq;
+  const int kg = w & 1, dh = w >> 1;
+  const int key0 = k0 + 64 * kg + n;  // this lane's key in half s: key0 + 32 s
+
+  const int q_first = CAUSAL ? max(0, k0 - off) : 0;
+  const int t_begin = q_first / kSQ;
+  const int nt = max(0, (a.Sq + kSQ - 1) / kSQ - t_begin);
+  const int n_items = chunk * nt;
+
+  // ---- copies: per item, wave w moves 1 KiB chunks 2w, 2w + 1 of P and of
+  // dS, and dout and q rows 8w .. 8w + 7 (two 512-byte rows per instruction)
+  const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
+  const int rr0 = 8 * w + (lane >> 5);          // this lane's row, + 2i
+  auto issue = [&](int it) __attribute__((always_inline)) {
+    const int hi = it / nt, t = t_begin + it % nt;
+    const int h = hk * a.G + sp * chunk + hi;
+    const uint32_t buf = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(it % kDsRing) * kDsBuf);
+    const size_t blk = stored_block(a, b * a.H + h, t, k0 / 64) * 2048;
+    const uint8_t *pb = sgpr_ptr((const uint8_t *)(a.ws_p + blk));
+    const uint8_t *sb = sgpr_ptr((const uint8_t *)(a.ws_ds + blk));
+    const uint32_t pv = 2048u * w + 16u * lane;
+    lds_dma16_nt(pb, pv, buf + 2 * kPChunk * wu);
+    lds_dma16_nt(pb, pv + 1024u, buf + 2 * kPChunk * wu + kPChunk);
+    lds_dma16_nt(sb, pv, buf + kDsPB + 2 * kPChunk * wu);
+    lds_dma16_nt(sb, pv + 1024u, buf + kDsPB + 2 * kPChunk * wu + kPChunk);
+    const uint8_t *ob = sgpr_ptr((const uint8_t *)(a.dout + (size_t)b * a.osb + (size_t)h * a.osh));
+    const uint8_t *qb = sgpr_ptr((const uint8_t *)(a.q + (size_t)b * a.qsb + (size_t)h * a.qsh));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rr0 + 2 * i;
+      const int q = min(t * kSQ + r, a.Sq - 1);
+      const uint32_t ch = 16u * (uint32_t)((lane & 31) ^ kv_swz(r));
+      const uint32_t dst = buf + 2 * kDsPB + 512u * (8 * wu + 2 * i);
+      lds_dma16(ob, (uint32_t)(2 * (size_t)q * a.ost) + ch, dst);
+      lds_dma16(qb, (uint32_t)(2 * (size_t)q * a.qst) + ch, dst + kDsRB);
+    }
+  };
+  constexpr int kCopies = 12;  // copies per wave per item
+
+  // ---- operand addresses (bytes within a buffer)
+  // P / dS (B operand: col = key, k = query row) of 32-key group kk of the
+  // 128: lane 4a + b of each 16-lane group reads row K0 + a, keys D0 + 4b ..
+  // + 3, which the dq kernel stored in slot 2(K0 + a) + (b & 1), bytes
+  // 8(b >> 1), of chunk (key tile, st, u2) = (kk / 2, kk % 2, grp & 1);
+  // K0 = 16u + 4g (+ 8 for the hi half)
+  const int grp = lane >> 4, ia = (lane & 15) >> 2, ib = lane & 3;
+  const uint32_t p_lane = kPChunk * (grp & 1) + 16u * (2 * (4 * g + ia) + (ib & 1)) + 8u * (ib >> 1);
+  // A operands (row = dim, k = query row) from the dout (dV) and q (dK) rows:
+  // row K0 + a, dims 128 dh + 32c + 16(grp & 1) + 4b .. + 3
+  const uint32_t do_base = 2 * kDsPB, q_base = 2 * kDsPB + kDsRB;
+  auto a_off = [&](int c, int u, int h8) {
+    return ds_row_off(16 * u + 8 * h8 + 4 * g + ia, 128 * dh + 32 * c + 16 * (grp & 1) + 4 * ib);
+  };
+  auto tr_pair = [&](uint32_t lo_addr, uint32_t hi_addr) {
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)lo_addr);
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FW_LDS v4i16_t *)hi_addr);
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  f32x16_t dv_acc[2][4], dk_acc[2][4];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dv_acc[s2][c][e] = dk_acc[s2][c][e] = 0.f;
+
+  for (int it = 0; it < min(kDsRing - 1, n_items); ++it) issue(it);
+  for (int it = 0; it < n_items; ++it) {
+    // this wave's copies of item it are done (the next item's may be
+    // outstanding); the barrier publishes every wave's, and frees the buffer
+    // of item it - 1 for item it + 2
+    if (it + 1 < n_items) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    static_assert(kCopies == 12 && kDsRing == 3, "the wait counts above assume 12 copies, 3 buffers");
+    __syncthreads();
+    if (it + kDsRing - 1 < n_items) issue(it + kDsRing - 1);
+    const int t = t_begin + it % nt;
+    const uint32_t buf = lds0 + (uint32_t)(it % kDsRing) * kDsBuf;
+    const int qb = t * kSQ;
+    const bool full = qb + kSQ <= a.Sq && k0 + kDsKeys <= a.Sk && (!CAUSAL || qb + off >= k0 + kDsKeys - 1);
+    // P and dS of both k-steps u and key halves s: element e at query row
+    // qb + 16u + 4g + (e & 3) (+ 8 for e >= 4)
+    u32x4_t pw[2][2], sw[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const uint32_t pa = buf + 2 * kPChunk * (2 * kg + s2) + p_lane + 512u * u;
+        pw[u][s2] = __builtin_bit_cast(u32x4_t, tr_pair(pa, pa + 256u));  // + 8 rows = 16 slots
+        sw[u][s2] = __builtin_bit_cast(u32x4_t, tr_pair(pa + kDsPB, pa + kDsPB + 256u));
+      }
+    if (!full) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int key = key0 + 32 * s2;
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int q = qb + 16 * u + 4 * g + ((e + h2) & 3) + ((e + h2) >= 4 ? 8 : 0);
+              const int vis = q >= a.Sq ? 0 : CAUSAL ? min(a.Sk, q + off + 1) : a.Sk;
+              m |= (key < vis ? 0xffffu : 0u) << (16 * h2);
+            }
+            pw[u][s2][e >> 1] &= m;
+            sw[u][s2][e >> 1] &= m;
+          }
+        }
+    }
+    // 16 steps i = (u, c, dout or q), two MFMAs each (both key halves); the
+    // A operand of step i + 3 is read during step i.  sched_barrier fences
+    // keep that order: left alone, the scheduler moves every read down to
+    // its MFMA, and one wave per SIMD then waits out each read's latency.
+    auto ld_op = [&](int i) __attribute__((always_inline)) {
+      const int u = i >> 3, c = (i >> 1) & 3;
+      const uint32_t base = buf + ((i & 1) ? q_base : do_base);
+      return tr_pair(base + a_off(c, u, 0), base + a_off(c, u, 1));
+    };
+    bf16x8_t ops[4];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) ops[i] = ld_op(i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 3 < 16) ops[(i + 3) & 3] = ld_op(i + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      const int u = i >> 3, c = (i >> 1) & 3;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        if (i & 1) dk_acc[s2][c] = mfma32(ops[i & 3], __builtin_bit_cast(bf16x8_t, sw[u][s2]), dk_acc[s2][c]);
+        else dv_acc[s2][c] = mfma32(ops[i & 3], __builtin_bit_cast(bf16x8_t, pw[u][s2]), dv_acc[s2][c]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---------------------------------------------------------------- store
+  // acc[s][c] value e: dim 128 dh + 32c + 8(e >> 2) + 4g + (e & 3), key key0 + 32 s
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int key = key0 + 32 * s2;
+    if (key >= a.Sk) continue;
+    if (a.split == 1) {
+      uint16_t *kp = a.dk + (size_t)b * a.ksb + (size_t)hk * a.ksh + (size_t)key * a.kst;
+      uint16_t *vp = a.dv + (size_t)b * a.vsb + (size_t)hk * a.vsh + (size_t)key * a.vst;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x16_t &K = dk_acc[s2][c], &V = dv_acc[s2][c];
+          const int d = 128 * dh + 32 * c + 8 * r4 + 4 * g;
+          *(u32x2_t *)(kp + d) = u32x2_t{pack_bf16(K[4 * r4] * a.scale, K[4 * r4 + 1] * a.scale),
+                                         pack_bf16(K[4 * r4 + 2] * a.scale, K[4 * r4 + 3] * a.scale)};
+          *(u32x2_t *)(vp + d) = u32x2_t{pack_bf16(V[4 * r4], V[4 * r4 + 1]), pack_bf16(V[4 * r4 + 2], V[4 * r4 + 3])};
+        }
+    } else {
+      const size_t row = ((((size_t)sp * a.B + b) * a.Hk + hk) * a.Sk + key) * 256;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x16_t &K = dk_acc[s2][c], &V = dv_acc[s2][c];
+          const int d = 128 * dh + 32 * c + 8 * r4 + 4 * g;
+          *(f32x4_t *)(a.dk_part + row + d) = f32x4_t{K[4 * r4], K[4 * r4 + 1], K[4 * r4 + 2], K[4 * r4 + 3]};
+          *(f32x4_t *)(a.dv_part + row + d) = f32x4_t{V[4 * r4], V[4 * r4 + 1], V[4 * r4 + 2], V[4 * r4 + 3]};
+        }
+    }
   }
 }
 
@@ -1430,29 +1673,56 @@ int pick_split(const fw_attn_bwd_params *p, long target) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// The stored path (128/128 head dims): the dq kernel writes P once and the
-// dk / dv kernel reads it instead of recomputing the scores.  It needs a bf16
-// (B, H, Sq rounded up to 128, Sk rounded up to 256) plane of workspace;
-// above kStoredMaxBytes the recomputing kernels run instead.
-// FW_BWD_STORED=0 selects the recomputing kernels at any size.
+// The stored path (head dims 128/128 and 256/256): the dq kernel writes P
+// (and at 256, dS) once and the dk / dv kernel reads it instead of
+// recomputing the scores.  Each plane is bf16 (B, H, Sq rounded up to 128, Sk
+// rounded up to 256) of workspace; above kStoredMaxBytes in all, or with one
+// head's plane at 4 GiB or more (the dq kernel's 32-bit store offsets), the
+// recomputing kernels run instead.  FW_BWD_STORED=0 selects the recomputing
+// kernels at any size.
 constexpr size_t kStoredMaxBytes = (size_t)8 << 30;
+
+size_t head_plane_bytes(const fw_attn_bwd_params *p) {
+  return (size_t)ceil_div(p->seqlen_q, 128) * 128 * (size_t)ceil_div(p->seqlen_k, 256) * 256 * 2;
+}
 
 // Rows rounded up to the dq workgroup's 128, keys to the dk / dv one's 256.
 size_t stored_plane_bytes(const fw_attn_bwd_params *p) {
-  return align256((size_t)p->batch * p->nheads * (size_t)ceil_div(p->seqlen_q, 128) * 128 *
-                  (size_t)ceil_div(p->seqlen_k, 256) * 256 * 2);
+  return align256((size_t)p->batch * p->nheads * head_plane_bytes(p));
 }
+
+// planes the stored path keeps: P, and dS at head dims 256/256
+int stored_planes(const fw_attn_bwd_params *p) { return p->head_dim == 256 ? 2 : 1; }
 
 bool use_stored(const fw_attn_bwd_params *p) {
-  if (p->head_dim != 128 || head_dim_v_of(p) != 128) return false;
+  const int dvw = head_dim_v_of(p);
+  if (!((p->head_dim == 128 && dvw == 128) || (p->head_dim == 256 && dvw == 256))) return false;
   const char *e = getenv("FW_BWD_STORED");
   if (e && e[0] == '0') return false;
-  return stored_plane_bytes(p) <= kStoredMaxBytes;
+  return head_plane_bytes(p) < ((size_t)1 << 32) &&
+         stored_planes(p) * stored_plane_bytes(p) <= kStoredMaxBytes;
 }
 
-// The stored dk / dv kernel runs two workgroups per CU and wants about four
-// per CU so that the causal imbalance evens out; the recomputing one runs one.
-int bwd_split(const fw_attn_bwd_params *p) { return pick_split(p, use_stored(p) ? 1024 : 512); }
+// The stored dk / dv kernel at 128/128 runs two workgroups per CU and wants
+// about four per CU so that the causal imbalance evens out; the recomputing
+// one runs one.  At 256/256 (128-key workgroups, one per CU) the split is
+// chosen over its own grid.
+int bwd_split(const fw_attn_bwd_params *p) {
+  if (use_stored(p) && p->head_dim == 256) {
+    const int G = p->nheads / p->nheads_k;
+    const long base = (long)p->batch * p->nheads_k * ceil_div(p->seqlen_k, 128);
+    long target = 512;
+    if (const char *e = getenv("FW_BWD_DS_TARGET")) target = atol(e);
+    int split = 1;
+    while (split < G && base * split < target) {
+      int nxt = split + 1;
+      while (G % nxt) ++nxt;
+      split = nxt;
+    }
+    return split;
+  }
+  return pick_split(p, use_stored(p) ? 1024 : 512);
+}
 
 }  // namespace
 }  // namespace fw
@@ -1466,7 +1736,7 @@ extern "C" size_t fw_attn_bwd_workspace_bytes(const fw_attn_bwd_params *p) {
   const int split = bwd_split(p);
   const size_t keys = (size_t)split * p->batch * p->nheads_k * p->seqlen_k * 4;
   if (split > 1) bytes += align256(keys * p->head_dim) + align256(keys * head_dim_v_of(p));
-  if (use_stored(p)) bytes += stored_plane_bytes(p);
+  if (use_stored(p)) bytes += stored_planes(p) * stored_plane_bytes(p);
   return bytes;
 }
 
@@ -1505,9 +1775,10 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
   FW_REQUIRE(p->workspace && p->workspace_bytes >= need, FW_ERR_VALUE,
              "workspace of %zu bytes is smaller than the %zu needed", p->workspace_bytes, need);
   // the stored path's copies address dout / q rows by 32-bit byte offsets
+  const int64_t hd = p->head_dim;
   FW_REQUIRE(!use_stored(p) ||
-                 (2 * (long)p->seqlen_q * std::max(std::max(p->q_stride_t, p->o_stride_t), (int64_t)128) < (1l << 32) &&
-                  2 * (long)p->seqlen_k * std::max(std::max(p->k_stride_t, p->v_stride_t), (int64_t)128) < (1l << 32)),
+                 (2 * (long)p->seqlen_q * std::max(std::max(p->q_stride_t, p->o_stride_t), hd) < (1l << 32) &&
+                  2 * (long)p->seqlen_k * std::max(std::max(p->k_stride_t, p->v_stride_t), hd) < (1l << 32)),
              FW_ERR_VALUE, "q / dout or k / v rows of one head span more than 4 GiB");
   FW_REQUIRE((long)p->batch * p->nheads * p->seqlen_q * 16 < (1l << 32) &&
                  (long)p->batch * p->nheads_k * p->seqlen_k * 16 < (1l << 32),
@@ -1534,7 +1805,7 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     a.dv_part = (float *)(ws + 2 * align256(rows * 4) + align256(keys * p->head_dim));
   }
   const bool stored = use_stored(p);
-  a.ws_p = nullptr;
+  a.ws_p = a.ws_ds = nullptr;
   a.sq_pad = ceil_div(p->seqlen_q, 128) * 128;
   a.sk_pad = ceil_div(p->seqlen_k, 256) * 256;
   if (stored) {
@@ -1544,6 +1815,7 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
       o += align256(keys * p->head_dim) + align256(keys * dvw);
     }
     a.ws_p = (uint16_t *)(ws + o);
+    if (stored_planes(p) == 2) a.ws_ds = (uint16_t *)(ws + o + stored_plane_bytes(p));
   }
   a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qst = p->q_stride_t;
   const bool o_given = p->o_stride_b || p->o_stride_h || p->o_stride_t;
@@ -1583,13 +1855,25 @@ extern "C" int fw_attn_bwd(const fw_attn_bwd_params *p, fw_stream_t stream) {
     // dq first (it writes P and dS), then dk / dv from them
     a.dq_hpw = a.G % 4 == 0 ? 4 : a.G % 2 == 0 ? 2 : 1;
     const dim3 gqs(ceil_div(p->seqlen_q, 32 * (4 / a.dq_hpw)) * (p->batch * p->nheads / a.dq_hpw));
-    if (p->causal) fw_bwd_dq_store_kernel<true><<<gqs, 256, 0, s>>>(a);
-    else fw_bwd_dq_store_kernel<false><<<gqs, 256, 0, s>>>(a);
+    const bool d256 = p->head_dim == 256;
+    if (d256) {
+      if (p->causal) fw_bwd_dq_store_kernel<true, 256><<<gqs, 256, 0, s>>>(a);
+      else fw_bwd_dq_store_kernel<false, 256><<<gqs, 256, 0, s>>>(a);
+    } else {
+      if (p->causal) fw_bwd_dq_store_kernel<true, 128><<<gqs, 256, 0, s>>>(a);
+      else fw_bwd_dq_store_kernel<false, 128><<<gqs, 256, 0, s>>>(a);
+    }
     st = check_launch("fw_bwd_dq_kernel");
     if (st != FW_OK) return st;
-    const dim3 gst(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kStKeys));
-    if (p->causal) fw_bwd_dkv_stored_kernel<true><<<gst, 512, 0, s>>>(a);
-    else fw_bwd_dkv_stored_kernel<false><<<gst, 512, 0, s>>>(a);
+    if (d256) {
+      const dim3 gds(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kDsKeys));
+      if (p->causal) fw_bwd_dkv_ds_kernel<true><<<gds, 256, 0, s>>>(a);
+      else fw_bwd_dkv_ds_kernel<false><<<gds, 256, 0, s>>>(a);
+    } else {
+      const dim3 gst(p->batch * p->nheads_k * a.split, ceil_div(p->seqlen_k, kStKeys));
+      if (p->causal) fw_bwd_dkv_stored_kernel<true><<<gst, 512, 0, s>>>(a);
+      else fw_bwd_dkv_stored_kernel<false><<<gst, 512, 0, s>>>(a);
+    }
     st = check_launch("fw_bwd_dkv_stored_kernel");
     if (st != FW_OK || a.split == 1) return st;
     const long thr = (long)p->batch * p->nheads_k * p->seqlen_k * 16;

@@ -276,3 +276,71 @@ def test_backward_random_shapes(seed):
     q, k, v = randn(rng, (b, sq, h, 128)), randn(rng, (b, sk, hk, 128)), randn(rng, (b, sk, hk, 128))
     do = randn(rng, (b, sq, h, 128))
     check_grads(run(q, k, v, do, causal, token_major=token_major), q, k, v, do, causal, what)
+
+
+@pytest.mark.parametrize("d", [192, 256])
+@pytest.mark.parametrize("b,h,hk,sq,sk,causal", [(2, 4, 2, 200, 333, True), (1, 4, 1, 333, 200, True),
+                                                 (1, 16, 2, 260, 260, True)])
+def test_backward_wide_recompute_path(d, b, h, hk, sq, sk, causal, monkeypatch):
+    """At head dims 192/192 and 256/256 the stored path (P and dS planes)
+    runs by default; FW_BWD_STORED=0 selects the recomputing wide kernels,
+    the path above the planes' size limit."""
+    monkeypatch.setenv("FW_BWD_STORED", "0")
+    what = f"bwd recompute d{d} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+    announce(what)
+    rng = np.random.default_rng(62 + d)
+    q, k, v = randn(rng, (b, sq, h, d)), randn(rng, (b, sk, hk, d)), randn(rng, (b, sk, hk, d))
+    do = randn(rng, (b, sq, h, d))
+    check_grads(run(q, k, v, do, causal), q, k, v, do, causal, what)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_backward_random_shapes_d256(seed):
+    """Seeded random shapes through the 256/256 stored path (the dq kernel
+    writes P and dS; 128-key dk/dv workgroups read them, with key halves
+    and head chunks): lengths that are multiples of none of 32, 64, 128, 256,
+    MHA / GQA / MQA, causal or full, head-major or token-major; against the
+    float64 oracle under the reference's 3x rule."""
+    rng = np.random.default_rng(2000 + seed)
+    b = int(rng.integers(1, 3))
+    hk = int(rng.choice([1, 2, 4]))
+    h = hk * int(rng.choice([1, 2, 4]))
+    sq = int(rng.integers(1, 400))
+    sk = int(rng.integers(1, 400))
+    causal = bool(rng.integers(0, 2))
+    token_major = bool(rng.integers(0, 2))
+    what = (f"bwd d256 random seed={seed} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal}"
+            f" token_major={token_major}")
+    announce(what)
+    q, k, v = randn(rng, (b, sq, h, 256)), randn(rng, (b, sk, hk, 256)), randn(rng, (b, sk, hk, 256))
+    do = randn(rng, (b, sq, h, 256))
+    check_grads(run(q, k, v, do, causal, token_major=token_major), q, k, v, do, causal, what)
+
+
+def test_stored_path_matches_recompute_at_c2_shape_d256(monkeypatch):
+    """C2's shape at head dim 256 (1 x 32/4 heads x 4096, causal): the stored
+    path (P and dS planes, 32 key blocks of 128, heads split over
+    workgroups) against the recomputing wide kernels.  dq is the same
+    computation; dk and dv read the bf16-rounded dS and P, so they differ by
+    bf16 rounding; an indexing error in a plane would differ by O(1)."""
+    announce("bwd d256 stored vs recompute at C2 shape")
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    b, h, hk, s, d = 1, 32, 4, 4096, 256
+    q, k, v, do = (torch.randn((b, n, s, d), generator=gen, device=DEV, dtype=torch.bfloat16)
+                   for n in (h, hk, hk, h))
+
+    def grads():
+        t = [x.clone().requires_grad_() for x in (q, k, v)]
+        flash_attn_func(*t, causal=True).backward(do)
+        torch.cuda.synchronize()
+        return [x.grad.float() for x in t]
+
+    stored = grads()
+    monkeypatch.setenv("FW_BWD_STORED", "0")
+    recompute = grads()
+    for name, a, r in zip(("dq", "dk", "dv"), stored, recompute):
+        err = (a - r).abs().max().item()
+        scale = r.abs().max().item()
+        print(f"C2 d256 {name}: max |stored - recompute| {err:.3e}, max |grad| {scale:.3e}")
+        assert torch.isfinite(a).all()
+        assert err <= 1e-2 * scale, (name, err, scale)
