@@ -994,18 +994,47 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
     // dP[q][key] for the item's 32 rows (value e at query row 8(e >> 2) + 4g
     // + (e & 3)): a chain of 8 MFMAs on one accumulator, with the 8 dV
     // products (which need only P) between its links
+    // The operands of step j + 2 are read during step j; sched_barrier
+    // fences keep that order (the scheduler would otherwise move each read
+    // down to its MFMA).
     f32x16_t dp;
 #pragma unroll
     for (int e = 0; e < 16; ++e) dp[e] = 0.f;
+    auto ld_da = [&](int j) __attribute__((always_inline)) {
+      return __builtin_bit_cast(
+          bf16x8_t, *(const FW_LDS u32x4_t *)(uintptr_t)(buf + do_base + st_row_off(n, 16 * j + 8 * g)));
+    };
+    auto ld_dv = [&](int j) __attribute__((always_inline)) {
+      const int c = j & 3, u = j >> 2;
+      return tr_pair(buf + do_base + a_off(c, u, 0), buf + do_base + a_off(c, u, 1));
+    };
+    bf16x8_t dar[3], dvr[3];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dar[j] = ld_da(j);
+      dvr[j] = ld_dv(j);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const bf16x8_t da = __builtin_bit_cast(
-          bf16x8_t, *(const FW_LDS u32x4_t *)(uintptr_t)(buf + do_base + st_row_off(n, 16 * j + 8 * g)));
-      dp = mfma32(da, vop[j], dp);
+      if (j + 2 < 8) {
+        dar[(j + 2) % 3] = ld_da(j + 2);
+        dvr[(j + 2) % 3] = ld_dv(j + 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      dp = mfma32(dar[j % 3], vop[j], dp);
       const int c = j & 3, u = j >> 2;
-      dv_acc[c] = mfma32(tr_pair(buf + do_base + a_off(c, u, 0), buf + do_base + a_off(c, u, 1)),
-                         __builtin_bit_cast(bf16x8_t, pw[u]), dv_acc[c]);
+      dv_acc[c] = mfma32(dvr[j % 3], __builtin_bit_cast(bf16x8_t, pw[u]), dv_acc[c]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // the dK operands (q rows) of the first two steps, before dS is formed
+    auto ld_q = [&](int i) __attribute__((always_inline)) {
+      const int u = i >> 2, c = i & 3;
+      return tr_pair(buf + q_base + a_off(c, u, 0), buf + q_base + a_off(c, u, 1));
+    };
+    bf16x8_t qr[3];
+    qr[0] = ld_q(0);
+    qr[1] = ld_q(1);
+    bf16x8_t sop[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       // dS = P (dP - delta); element e of k-step u is value 8u + e of dp
@@ -1019,10 +1048,14 @@ __global__ __launch_bounds__(512, 1) void fw_bwd_dkv_stored_kernel(BwdArgs a) {
         sw[e2] = pack_bf16(bf16_lo(pw[u][e2]) * (dp[8 * u + 2 * e2] - dl0),
                            bf16_hi(pw[u][e2]) * (dp[8 * u + 2 * e2 + 1] - dl1));
       }
-      const bf16x8_t sop = __builtin_bit_cast(bf16x8_t, sw);
+      sop[u] = __builtin_bit_cast(bf16x8_t, sw);
+    }
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        dk_acc[c] = mfma32(tr_pair(buf + q_base + a_off(c, u, 0), buf + q_base + a_off(c, u, 1)), sop, dk_acc[c]);
+    for (int i = 0; i < 8; ++i) {
+      if (i + 2 < 8) qr[(i + 2) % 3] = ld_q(i + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      dk_acc[i & 3] = mfma32(qr[i % 3], sop[i >> 2], dk_acc[i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
