@@ -504,7 +504,7 @@ def workload_bwd(args, device, d=128):
     """c2's shape (at head dim d) through the dense backward (fw_attn_bwd),
     inputs (q, k, v, out, lse, dout) resident; FLOPs counted as 2.5x the
     forward's (the five backward products; the kernels evaluate six at
-    128/128, seven at the wide head dims)."""
+    128/128 and five at 256/256)."""
     from flywheel_tpu import flash_attn_func
     from flywheel_tpu.backward import attn_bwd
     (b, h, hk, s, d), gen, q, k, v = _c2_inputs(device, d)
@@ -536,9 +536,9 @@ def workload_bwd(args, device, d=128):
                 "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": ("fw_bwd_dq_store + fw_bwd_dkv_stored + fw_bwd_reduce (whole backward)"
+                  "kernel": ("fw_bwd_dq_store<128> + fw_bwd_dkv_stored + fw_bwd_reduce (whole backward)"
                              if d == 128 else
-                             "fw_bwd_prep + fw_bwd_dkv_wide + fw_bwd_reduce + fw_bwd_dq_wide (whole backward)"),
+                             "fw_bwd_dq_store<256> + fw_bwd_dkv_ds + fw_bwd_reduce (whole backward)"),
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=cpu)
 
@@ -706,12 +706,13 @@ def workload_dec256(args, device):
 
 
 WORKLOADS = {"c2": workload_c2, "c3": workload_c3, "c4": workload_c4, "c5": workload_c5,
-             "c2d256": workload_c2d256, "bwd": workload_bwd}
+             "c2d256": workload_c2d256, "bwd": workload_bwd,
+             "bwd256": lambda args, device: workload_bwd(args, device, d=256)}
 # "all": the four BASELINE workloads, then the reference's published dense
-# prefill shape (docs/v7x.md:60) and the dense backward at C2's shape
-DEFAULT = ["c2", "c3", "c4", "c5", "c2d256", "bwd"]
+# prefill shape (docs/v7x.md:60) and the dense backward at C2's shape, at head
+# dims 128 and 256
+DEFAULT = ["c2", "c3", "c4", "c5", "c2d256", "bwd", "bwd256"]
 EXTRA = {"copy": workload_copy, "gemm": workload_gemm, "rope": workload_rope,
-         "bwd256": lambda args, device: workload_bwd(args, device, d=256),
          "c2d256mha": workload_c2d256mha, "dec256": workload_dec256,
          "cp256": workload_cp256, "cp256mha": lambda args, device: workload_cp256(args, device, hk=32),
          "c4fp8": lambda args, device: workload_c4(args, device, fp8=True)}

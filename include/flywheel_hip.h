@@ -263,10 +263,12 @@ int fw_prefill(const fw_prefill_params *p, fw_stream_t stream);
  * from fw_attn_bwd_workspace_bytes) holds f32 row statistics, f32 dk / dv
  * partials when the query heads of one KV head are split over workgroups,
  * and, at head dims 128/128, the bf16 P plane (2 * batch * nheads *
- * seqlen_q * seqlen_k bytes, rounded up) through which dk and dv are
- * computed without recomputing the scores, as long as it fits in 8 GiB
- * (beyond that, or with the environment variable FW_BWD_STORED=0, the scores
- * are recomputed and the workspace holds no plane).
+ * seqlen_q * seqlen_k bytes, the lengths rounded up to 128 and 256), at
+ * 256/256 a P and a dS plane, through which dk and dv are computed without
+ * recomputing the scores, as long as the planes fit in 8 GiB and one head's
+ * share in 4 GiB (beyond that, or with the environment variable
+ * FW_BWD_STORED=0, the scores are recomputed and the workspace holds no
+ * plane).
  */
 typedef struct fw_attn_bwd_params {
   const void *q, *k, *v, *out, *dout;

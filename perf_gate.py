@@ -41,8 +41,9 @@ import sys
 ROOT = pathlib.Path(__file__).resolve().parent
 SCHEMA_VERSION = 1
 # Bench workloads the gate times by default: the four BASELINE configs, the
-# head_dim-256 prefill, fp8 chunked prefill, d256 decode and the backward.
-CONFIGS = ("c2", "c3", "c4", "c5", "c2d256", "c4fp8", "dec256", "bwd")
+# head_dim-256 prefill, fp8 chunked prefill, d256 decode and the backward at
+# head dims 128 and 256.
+CONFIGS = ("c2", "c3", "c4", "c5", "c2d256", "c4fp8", "dec256", "bwd", "bwd256")
 # Run metadata that must match before two runs' times compare.
 ENV_KEYS = ("device_arch", "torch", "hip")
 
