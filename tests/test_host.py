@@ -163,6 +163,37 @@ def test_capi_validation_status_codes():
         assert lib.fw_rotary(r, None) == N.FW_ERR_VALUE  # no buffers
 
 
+def test_backward_workspace_planes(monkeypatch):
+    """The stored backward's planes in fw_attn_bwd_workspace_bytes: bf16 P
+    (and dS at 256/256) of B x H x roundup(Sq, 128) x roundup(Sk, 256), kept
+    while the planes fit in 8 GiB and one head's share in 4 GiB (the dq
+    kernel's 32-bit store offsets); otherwise, at other head-dim pairs and
+    with FW_BWD_STORED=0 the recomputing kernels run and the workspace holds
+    no plane."""
+    lib = N.lib()
+    GiB = 1 << 30
+
+    def ws(d, dv, h, s, batch=1):
+        bw = N.AttnBwdParams()
+        bw.head_dim, bw.head_dim_v, bw.nheads, bw.nheads_k = d, dv, h, h
+        bw.batch, bw.seqlen_q, bw.seqlen_k = batch, s, s
+        return lib.fw_attn_bwd_workspace_bytes(bw)
+
+    def plane(h, s, batch=1):
+        return batch * h * (-(-s // 128) * 128) * (-(-s // 256) * 256) * 2
+
+    assert ws(128, 128, 1, 32768) >= plane(1, 32768)          # one 2 GiB plane
+    assert ws(256, 256, 1, 32768) >= 2 * plane(1, 32768)      # P and dS
+    assert ws(256, 256, 2, 32768) >= 2 * plane(2, 32768)      # 8 GiB in all: kept
+    assert ws(256, 256, 3, 32768) < GiB                       # 12 GiB: recompute
+    assert ws(128, 128, 5, 32768) < GiB                       # 10 GiB: recompute
+    assert plane(1, 46341) >= 4 * GiB and ws(128, 128, 1, 46341) < GiB  # one head >= 4 GiB
+    assert ws(256, 128, 1, 32768) < GiB                       # wide pair: no plane
+    monkeypatch.setenv("FW_BWD_STORED", "0")
+    assert ws(128, 128, 1, 32768) < GiB
+    assert ws(256, 256, 1, 32768) < GiB
+
+
 def bf(*shape):
     return torch.zeros(shape, dtype=torch.bfloat16)
 
