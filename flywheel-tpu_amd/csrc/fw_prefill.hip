@@ -572,8 +572,23 @@ __device__ __attribute__((aligned(256))) uint8_t kZeroKV[1024];
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
 
-template <int MODE, bool SOFTCAP, int KV = FW_BF16>
-__global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
+// The dense q tile and head group of workgroup bid: heaviest q tiles first,
+// XCD-aware when the head groups divide by 8 (bid runs on XCD bid % 8, and
+// each XCD gets the query heads of one KV head, so its K/V stay in that L2).
+__device__ __forceinline__ void pp_dense_item(const PrefillArgs &a, int bid, int &qt, int &bh) {
+  const int nbh = a.B * (a.H >> a.hpw_shift);
+  if (nbh % 8 == 0) {
+    const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
+    qt = a.n_qt - 1 - wi / hx;
+    bh = x * hx + wi % hx;
+  } else {
+    qt = a.n_qt - 1 - bid / nbh;
+    bh = bid % nbh;
+  }
+}
+
+template <int MODE, bool SOFTCAP, int KV>
+__device__ __forceinline__ void pp_body(const PrefillArgs &a, const int dense_qt, const int dense_bh) {
   // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile j+2 into
   // registers in its softmax slot of tile j, and widens them to bf16 into the
   // tile's LDS buffer at the end of its next MFMA slot, where it would
@@ -601,17 +616,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   int split = -1;  // key split of the slot: -1 none, else 2 * pair + part
   if constexpr (MODE == FW_KV_DENSE) {
     const int ng = a.H >> a.hpw_shift;
-    const int nbh = a.B * ng;
-    const int bid = blockIdx.x;
-    int qt, bh;
-    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
-      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
-      qt = a.n_qt - 1 - wi / hx;
-      bh = x * hx + wi % hx;
-    } else {
-      qt = a.n_qt - 1 - bid / nbh;
-      bh = bid % nbh;
-    }
+    const int qt = dense_qt, bh = dense_bh;
     b = bh / ng;
     hg = bh % ng;
     q0 = qt * R;
@@ -1317,6 +1322,29 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   }
 }
 
+template <int MODE, bool SOFTCAP, int KV = FW_BF16>
+__global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
+  int qt = 0, bh = 0;
+  if constexpr (MODE == FW_KV_DENSE) pp_dense_item(a, blockIdx.x, qt, bh);
+  pp_body<MODE, SOFTCAP, KV>(a, qt, bh);
+}
+
+// Dense, an even number of q tiles: half as many workgroups, each running a
+// heavy q tile (the upper half, heaviest first) and then its mirror n_qt - 1 -
+// qt of the same head group, so every workgroup's two items cost about the
+// same and a CU runs them back to back, without a second workgroup launch.
+// Between the two, every wave's copies are complete and the barrier frees the
+// LDS (the first item's O staging) for the second item's tiles.
+template <bool SOFTCAP>
+__global__ __launch_bounds__(512, 1) void fw_prefill_pp_pair_kernel(PrefillArgs a) {
+  int qt, bh;
+  pp_dense_item(a, blockIdx.x, qt, bh);
+  pp_body<FW_KV_DENSE, SOFTCAP, FW_BF16>(a, qt, bh);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+  pp_body<FW_KV_DENSE, SOFTCAP, FW_BF16>(a, a.n_qt - 1 - qt, bh);
+}
+
 // ---------------------------------------------------------------------------
 // head_dim 256, bf16 K/V: one wave per SIMD.  Workgroup = 4 waves = 128 q
 // rows of one query head (wave w owns rows 32w .. 32w+31).  At head_dim 256 a
@@ -1338,6 +1366,8 @@ constexpr int kD2TileB = kD2Keys * kD2RowB;   // 16 KiB per K or V tile
 constexpr int kD2Bufs = 4;
 
 template <int MODE, bool SOFTCAP, int KV = FW_BF16>
+
+
 __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) {
   // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile t+3 into
   // registers in step t and widens them to bf16 into the tile's LDS buffer in
@@ -2000,6 +2030,15 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 // launches over chunks of v and out, which keeps O within one wave's
 // registers: 256 dims each at head dim 64, 128 each at head dims 384 and 512
 // (whose Q^T operand alone takes 96-128 registers).
+// The dense ping-pong kernel runs as pairs of q tiles (fw_prefill_pp_pair_kernel)
+// when the q tiles pair up and half the grid still covers every CU.
+// FW_PREFILL_PAIR=0 keeps one q tile per workgroup.
+static bool use_pair(const PrefillArgs &a, dim3 grid) {
+  if (a.n_qt % 2 != 0 || (int)(grid.x / 2) < device_cus()) return false;
+  const char *e = getenv("FW_PREFILL_PAIR");
+  return !(e && e[0] == '0');
+}
+
 template <int MODE, int KV, int D, int DV>
 static void launch_staged(const PrefillArgs &a, dim3 grid, hipStream_t s) {
   fw_prefill_staged_kernel<MODE, KV, D, DV><<<grid, 256, 0, s>>>(a);
@@ -2009,6 +2048,14 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
                         hipStream_t s) {
   if (kv_dtype == FW_BF16) {
     if (d == 128 && dv == 128) {
+      if constexpr (MODE == FW_KV_DENSE) {
+        if (use_pair(a, grid)) {
+          const dim3 half(grid.x / 2);
+          if (a.softcap_log2 != 0.f) fw_prefill_pp_pair_kernel<true><<<half, 512, 0, s>>>(a);
+          else fw_prefill_pp_pair_kernel<false><<<half, 512, 0, s>>>(a);
+          return;
+        }
+      }
       if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
       else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
     } else if (d == 256 && dv == 256) {
