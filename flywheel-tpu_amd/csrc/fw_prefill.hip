@@ -572,11 +572,10 @@ __device__ __attribute__((aligned(256))) uint8_t kZeroKV[1024];
 constexpr int kPPRows = 32 * kPPWaves;  // q rows per workgroup
 constexpr int kPPBuf = 2 * kTileB;      // [K tile | V tile]
 
-// The dense q tile and head group of workgroup bid: heaviest q tiles first,
+// The dense q tile and head group (of nbh) of workgroup bid: heaviest q tiles first,
 // XCD-aware when the head groups divide by 8 (bid runs on XCD bid % 8, and
 // each XCD gets the query heads of one KV head, so its K/V stay in that L2).
-__device__ __forceinline__ void pp_dense_item(const PrefillArgs &a, int bid, int &qt, int &bh) {
-  const int nbh = a.B * (a.H >> a.hpw_shift);
+__device__ __forceinline__ void dense_item(const PrefillArgs &a, int bid, int nbh, int &qt, int &bh) {
   if (nbh % 8 == 0) {
     const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
     qt = a.n_qt - 1 - wi / hx;
@@ -1325,7 +1324,7 @@ __device__ __forceinline__ void pp_body(const PrefillArgs &a, const int dense_qt
 template <int MODE, bool SOFTCAP, int KV = FW_BF16>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
   int qt = 0, bh = 0;
-  if constexpr (MODE == FW_KV_DENSE) pp_dense_item(a, blockIdx.x, qt, bh);
+  if constexpr (MODE == FW_KV_DENSE) dense_item(a, blockIdx.x, a.B * (a.H >> a.hpw_shift), qt, bh);
   pp_body<MODE, SOFTCAP, KV>(a, qt, bh);
 }
 
@@ -1338,7 +1337,7 @@ __global__ __launch_bounds__(512, 1) void fw_prefill_pp_kernel(PrefillArgs a) {
 template <bool SOFTCAP>
 __global__ __launch_bounds__(512, 1) void fw_prefill_pp_pair_kernel(PrefillArgs a) {
   int qt, bh;
-  pp_dense_item(a, blockIdx.x, qt, bh);
+  dense_item(a, blockIdx.x, a.B * (a.H >> a.hpw_shift), qt, bh);
   pp_body<FW_KV_DENSE, SOFTCAP, FW_BF16>(a, qt, bh);
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
@@ -1365,10 +1364,8 @@ constexpr int kD2RowB = 512;                  // LDS bytes of one key row
 constexpr int kD2TileB = kD2Keys * kD2RowB;   // 16 KiB per K or V tile
 constexpr int kD2Bufs = 4;
 
-template <int MODE, bool SOFTCAP, int KV = FW_BF16>
-
-
-__global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) {
+template <int MODE, bool SOFTCAP, int KV>
+__device__ __forceinline__ void d256_body(const PrefillArgs &a, const int dense_qt, const int dense_bh) {
   // fp8 pools (paged only): a wave loads its 8 fp8 K and V rows of tile t+3 into
   // registers in step t and widens them to bf16 into the tile's LDS buffer in
   // step t+1, one step before the QK that reads them; the rest is the bf16 kernel.
@@ -1384,17 +1381,7 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
   // ------------------------------------------------------------ tile decode
   int b = 0, h, seq = 0, q0, sq_len, sk_len, qtok0 = 0, kbase = 0;
   if constexpr (MODE == FW_KV_DENSE) {
-    const int nbh = a.B * a.H;
-    const int bid = blockIdx.x;
-    int qt, bh;
-    if (nbh % 8 == 0) {  // XCD-aware: workgroup bid runs on XCD bid % 8
-      const int x = bid & 7, wi = bid >> 3, hx = nbh >> 3;
-      qt = a.n_qt - 1 - wi / hx;
-      bh = x * hx + wi % hx;
-    } else {
-      qt = a.n_qt - 1 - bid / nbh;
-      bh = bid % nbh;
-    }
+    const int qt = dense_qt, bh = dense_bh;
     b = bh / a.H;
     h = bh % a.H;
     q0 = qt * kD2Rows;
@@ -1807,6 +1794,24 @@ __global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) 
   }
 }
 
+template <int MODE, bool SOFTCAP, int KV = FW_BF16>
+__global__ __launch_bounds__(256, 1) void fw_prefill_d256_kernel(PrefillArgs a) {
+  int qt = 0, bh = 0;
+  if constexpr (MODE == FW_KV_DENSE) dense_item(a, blockIdx.x, a.B * a.H, qt, bh);
+  d256_body<MODE, SOFTCAP, KV>(a, qt, bh);
+}
+
+// Dense pairs of mirrored q tiles, as fw_prefill_pp_pair_kernel.
+template <bool SOFTCAP>
+__global__ __launch_bounds__(256, 1) void fw_prefill_d256_pair_kernel(PrefillArgs a) {
+  int qt, bh;
+  dense_item(a, blockIdx.x, a.B * a.H, qt, bh);
+  d256_body<FW_KV_DENSE, SOFTCAP, FW_BF16>(a, qt, bh);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+  d256_body<FW_KV_DENSE, SOFTCAP, FW_BF16>(a, a.n_qt - 1 - qt, bh);
+}
+
 // One workgroup: per-sequence q tiles from cu_seqlens_q, then padding tiles
 // for the packed rows past cu_seqlens_q[num_active] (schedule.py:617-717).
 // When there are at most kSortTiles sequence tiles they are ordered by cost,
@@ -2030,8 +2035,9 @@ extern "C" size_t fw_prefill_workspace_bytes(const fw_prefill_params *p) {
 // launches over chunks of v and out, which keeps O within one wave's
 // registers: 256 dims each at head dim 64, 128 each at head dims 384 and 512
 // (whose Q^T operand alone takes 96-128 registers).
-// The dense ping-pong kernel runs as pairs of q tiles (fw_prefill_pp_pair_kernel)
-// when the q tiles pair up and half the grid still covers every CU.
+// The dense ping-pong and head_dim-256 kernels run as pairs of q tiles
+// (fw_prefill_pp_pair_kernel, fw_prefill_d256_pair_kernel) when the q tiles
+// pair up and half the grid still covers every CU.
 // FW_PREFILL_PAIR=0 keeps one q tile per workgroup.
 static bool use_pair(const PrefillArgs &a, dim3 grid) {
   if (a.n_qt % 2 != 0 || (int)(grid.x / 2) < device_cus()) return false;
@@ -2059,6 +2065,14 @@ static void launch_mode(const PrefillArgs &a, dim3 grid, int kv_dtype, int d, in
       if (a.softcap_log2 != 0.f) fw_prefill_pp_kernel<MODE, true><<<grid, 512, 0, s>>>(a);
       else fw_prefill_pp_kernel<MODE, false><<<grid, 512, 0, s>>>(a);
     } else if (d == 256 && dv == 256) {
+      if constexpr (MODE == FW_KV_DENSE) {
+        if (use_pair(a, grid)) {
+          const dim3 half(grid.x / 2);
+          if (a.softcap_log2 != 0.f) fw_prefill_d256_pair_kernel<true><<<half, 256, 0, s>>>(a);
+          else fw_prefill_d256_pair_kernel<false><<<half, 256, 0, s>>>(a);
+          return;
+        }
+      }
       if (a.softcap_log2 != 0.f) fw_prefill_d256_kernel<MODE, true><<<grid, 256, 0, s>>>(a);
       else fw_prefill_d256_kernel<MODE, false><<<grid, 256, 0, s>>>(a);
     } else if (d == 64 && dv == 64) {

@@ -102,20 +102,21 @@ def test_flash_attn_func_c2_full_size():
     (1, 32, 4, 4096, 6000, True, (-1, -1), 0.0, False),     # keys past the queries
     (2, 32, 32, 4096, 4096, True, (-1, -1), 0.0, False),    # MHA: XCD-aware head groups
 ])
-def test_pair_kernel_matches_one_tile_kernel(b, h, hk, sq, sk, causal, window, softcap, sinks,
+@pytest.mark.parametrize("d", [128, 256])
+def test_pair_kernel_matches_one_tile_kernel(d, b, h, hk, sq, sk, causal, window, softcap, sinks,
                                              monkeypatch):
     """Dense grids whose q tiles pair up and whose half still covers every CU
-    run fw_prefill_pp_pair_kernel (a heavy q tile, then its mirror of the
-    same head group, per workgroup); FW_PREFILL_PAIR=0 runs one q tile per
-    workgroup.  Both compute every tile the same way: bitwise equal out and
+    run fw_prefill_pp_pair_kernel / fw_prefill_d256_pair_kernel (a heavy q
+    tile, then its mirror of the same head group, per workgroup);
+    FW_PREFILL_PAIR=0 runs one q tile per workgroup.  Both compute every tile the same way: bitwise equal out and
     lse, and the C2 full-size test above checks the pair kernel against the
     oracle."""
-    announce(f"pair kernel b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window}"
+    announce(f"pair kernel d{d} b{b} h{h}/{hk} sq{sq} sk{sk} causal={causal} window={window}"
              f" softcap={softcap} sinks={sinks}")
     gen = torch.Generator(device=DEV).manual_seed(21)
-    q = torch.randn((b, h, sq, 128), generator=gen, device=DEV, dtype=torch.bfloat16)
-    k = torch.randn((b, hk, sk, 128), generator=gen, device=DEV, dtype=torch.bfloat16)
-    v = torch.randn((b, hk, sk, 128), generator=gen, device=DEV, dtype=torch.bfloat16)
+    q = torch.randn((b, h, sq, d), generator=gen, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn((b, hk, sk, d), generator=gen, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn((b, hk, sk, d), generator=gen, device=DEV, dtype=torch.bfloat16)
     kw = dict(causal=causal, window_size=window, softcap=softcap, return_softmax_lse=True)
     if sinks:
         kw["learnable_sink"] = torch.randn((h,), generator=gen, device=DEV, dtype=torch.float32)
