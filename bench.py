@@ -234,7 +234,7 @@ def workload_c2(args, device):
                 "nheads_k": hk, "seqlen": s, "head_dim": d, "layout": "head-major (B,H,S,D)"},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                  "traffic": read_traffic("c2"), "kernel": "fw_prefill_pp_kernel<DENSE> (bf16)",
+                  "traffic": read_traffic("c2"), "kernel": "fw_prefill_pp_pair_kernel (dense bf16, pairs of q tiles)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=cpu)
 
@@ -391,7 +391,7 @@ def workload_c4(args, device, fp8=False):
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                   "traffic": None if fp8 else read_traffic("c4"),
-                  "kernel": "fw_append_kernel + fw_prefill_schedule + " + (
+                  "kernel": "fw_append_schedule_kernel + " + (
                       "fw_prefill_pp_kernel<PAGED, softcap, e4m3>" if fp8
                       else "fw_prefill_pp_kernel<PAGED, softcap>") + " (whole step)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
@@ -559,7 +559,7 @@ def workload_rope(args, device):
                 "batch": b, "nheads": h, "nheads_k": hk, "seqlen": s, "head_dim": d},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": "fw_rotary (K) + fw_prefill_pp_kernel<DENSE> (Q rotated on load)",
+                  "kernel": "fw_rotary (K) + fw_prefill_pp_pair_kernel (dense, Q rotated on load)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=None)
 
@@ -599,7 +599,7 @@ def workload_c2d256(args, device):
                 "published": "653 TFLOP/s, TPU v7x one core (docs/v7x.md:60)"},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": "fw_prefill_d256_kernel<DENSE, false>",
+                  "kernel": "fw_prefill_d256_pair_kernel (dense, pairs of q tiles)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=cpu)
 
@@ -623,7 +623,7 @@ def workload_c2d256mha(args, device):
                 "published": "630 TFLOP/s, TPU v7x one core (docs/v7x.md:49)"},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": "fw_prefill_d256_kernel<DENSE, false>",
+                  "kernel": "fw_prefill_d256_pair_kernel (dense, pairs of q tiles)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP"},
         cpu=None)
 
@@ -666,7 +666,7 @@ def workload_cp256(args, device, hk=4):
                 "published": f"{pub}, TPU v7x one core (docs/v7x.md:155-157)"},
         roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "kernel": "fw_append_kernel + fw_prefill_schedule + fw_prefill_d256_kernel"
+                  "kernel": "fw_append_schedule_kernel + fw_prefill_d256_kernel"
                             "<PAGED, false> (16 calls)",
                   "algorithmic_per_launch": f"{flops:.4e} FLOP per 16 calls (causal count)"},
         cpu=None)
