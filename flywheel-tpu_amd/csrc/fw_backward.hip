@@ -7,19 +7,22 @@
 //   dp = dout v^T,  ds = p (dp - delta),  delta = rowsum(dout * out)
 //   dv += p^T dout,  dk += scale ds^T q,  dq += scale ds k
 // Here that work is split into launches, all deterministic (no atomics).
-// At head dims 128/128, while a bf16 (B, H, Sq, Sk) plane fits in 8 GiB of
-// workspace (the stored path):
-//   fw_bwd_dq_store_kernel    one workgroup per 128 query rows of one head; q
-//                             and dout live in registers, kv tiles stream
-//                             through LDS; it also forms the row statistics
-//                             (delta, lse_log2; bwd.py:685-720) and writes P
-//                             and delta
-//   fw_bwd_dkv_stored_kernel  dv = P^T dout from the stored P, dk = scale
-//                             dS^T q with dS = P (dout v^T - delta): three
-//                             products, no score recomputed
+// At head dims 128/128 and 256/256, while the bf16 (B, H, Sq, Sk) planes fit
+// in 8 GiB of workspace and one head's in 4 GiB (the stored path):
+//   fw_bwd_dq_store_kernel    up to four query heads of one KV head over the
+//                             same 32 query rows per workgroup; q and dout live
+//                             in registers, kv tiles stream through LDS; it
+//                             also forms the row statistics (delta, lse_log2;
+//                             bwd.py:685-720) and writes P and delta (at 256
+//                             also dS)
+//   fw_bwd_dkv_stored_kernel  (128/128) dv = P^T dout from the stored P, dk =
+//                             scale dS^T q with dS = P (dout v^T - delta):
+//                             three products, no score recomputed
+//   fw_bwd_dkv_ds_kernel      (256/256) dv = P^T dout and dk = scale dS^T q
+//                             from the stored P and dS: two products
 //   fw_bwd_reduce_kernel      sums the per-chunk dk / dv partials when a KV
 //                             head's query heads were split over workgroups
-// Otherwise (and at the wide head dims) fw_bwd_prep_kernel forms lse_log2 and
+// Otherwise (and at the other wide head dims) fw_bwd_prep_kernel forms lse_log2 and
 // delta per query row, and fw_bwd_dkv_kernel recomputes the
 // scores: one workgroup per 128 keys of one KV head (and one chunk of its
 // query heads); K and V live in registers, q tiles stream through LDS, dk, dv
