@@ -8,14 +8,20 @@
 // fwd_blocks.qk / online_softmax / pv (fwd_blocks.py:812-942), and the
 // schedule tables of schedule.py:617-717.
 //
-// Two forward kernels share one argument block and the q-tile schedule:
-//   fw_prefill_pp_kernel     bf16 K/V: 8 waves, ping-pong schedule
-//   fw_prefill_staged_kernel fp8 paged pools: K/V widened to bf16 in registers
+// The forward kernels share one argument block and the q-tile schedule:
+//   fw_prefill_pp_kernel       head dims 128/128: 8 waves, ping-pong schedule;
+//                              bf16 K/V, or fp8 pools widened to bf16 in LDS
+//   fw_prefill_d256_kernel     head dims 256/256: 4 waves, one per SIMD
+//   fw_prefill_pp_pair_kernel, fw_prefill_d256_pair_kernel
+//                              the same on large dense grids, two mirrored q
+//                              tiles per workgroup
+//   fw_prefill_staged_kernel   the other head dims (64, 96, 192, 384, 512 and
+//                              mixed q / v widths): K/V staged in registers
 // In all of them a wave owns 32 query rows, each lane one row, and computes
 //   S^T (32 keys x 32 rows) = K x Q^T        (Q^T resident in registers)
 //   online softmax in log2 units
 //   O^T (32 dims x 32 rows) += V^T x P^T     (P^T = the S^T registers, bf16)
-// with v_mfma_f32_32x32x16_bf16 over 64-key tiles staged through LDS.
+// with v_mfma_f32_32x32x16_bf16 over key tiles staged through LDS.
 #include "fw_common.h"
 #include <algorithm>
 #include <type_traits>
